@@ -1,0 +1,147 @@
+/*
+ * qlin -- quantized-linear engine for AMD MI355X (gfx950).  C ABI.
+ *
+ * Every entry point is extern "C", takes plain pointers/sizes (qlin_tensor descriptors) and a
+ * HIP stream, launches asynchronously on that stream and never allocates device memory: the
+ * caller passes a workspace sized by qlin_workspace_size().  The caller owns every buffer.
+ * Inputs are read-only; packed weights are never copied or rewritten.
+ *
+ * Return codes: QLIN_OK on success; QLIN_EUNSUPPORTED when the call is well-formed but outside
+ * what the kernels implement (the caller falls back, as the reference's registry does with
+ * NoCapableBackendError); QLIN_EINVAL for malformed arguments; QLIN_EHIP for a HIP runtime
+ * error; QLIN_EWORKSPACE when the workspace is too small.  qlin_last_error() returns a message
+ * for the calling thread's most recent failure.
+ *
+ * Each entry point cites the reference interface it replaces (roblennon/mac-kernels-public);
+ * the reference's own implementations live in un-vendored comfy-kitchen forks, so the cited
+ * lines are its call sites, which pin names, argument order and semantics.
+ */
+#ifndef QLIN_H
+#define QLIN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    QLIN_OK = 0,
+    QLIN_EUNSUPPORTED = 1,
+    QLIN_EINVAL = 2,
+    QLIN_EHIP = 3,
+    QLIN_EWORKSPACE = 4,
+} qlin_status;
+
+typedef enum {
+    QLIN_DT_F32 = 0,
+    QLIN_DT_F16 = 1,
+    QLIN_DT_BF16 = 2,
+    QLIN_DT_I8 = 3,
+    QLIN_DT_U8 = 4,
+    QLIN_DT_I32 = 5,
+    QLIN_DT_E4M3 = 6,
+} qlin_dtype;
+
+/* Strided tensor view.  shape/stride are in elements; unused dims are ignored. */
+typedef struct {
+    void* data;
+    int32_t dtype;   /* qlin_dtype */
+    int32_t ndim;    /* 1..4 */
+    int64_t shape[4];
+    int64_t stride[4];
+} qlin_tensor;
+
+/* Operation ids for qlin_workspace_size(). */
+typedef enum {
+    QLIN_OP_INT8_LINEAR = 0,
+    QLIN_OP_W4A8_LINEAR = 1,
+    QLIN_OP_GGUF_LINEAR = 2,
+} qlin_op;
+
+/* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
+enum {
+    QLIN_GGML_Q4_0 = 2, QLIN_GGML_Q4_1 = 3, QLIN_GGML_Q5_0 = 6, QLIN_GGML_Q5_1 = 7,
+    QLIN_GGML_Q8_0 = 8, QLIN_GGML_Q2_K = 10, QLIN_GGML_Q3_K = 11, QLIN_GGML_Q4_K = 12,
+    QLIN_GGML_Q5_K = 13, QLIN_GGML_Q6_K = 14, QLIN_GGML_IQ4_NL = 20, QLIN_GGML_IQ4_XS = 23,
+};
+
+int qlin_version(void);
+const char* qlin_status_string(qlin_status s);
+const char* qlin_last_error(void);
+
+/* Bytes of device workspace an op needs for activations of M rows against an [N, K] weight.
+ * `param` is the ConvRot group size (INT8), bits (W4A8: 4 or 6) or the ggml type (GGUF).
+ * `x_dtype` is the activation's qlin_dtype. */
+size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, int x_dtype);
+
+/* Capability probe: QLIN_OK if the op would accept these shapes/parameters, else
+ * QLIN_EUNSUPPORTED (message in qlin_last_error()).  Launches nothing. */
+qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x_dtype, int out_dtype);
+
+/* y[M,N] = rot(x)[M,K] @ (q[N,K] * scale[N])^T + bias, weight-only INT8 with optional ConvRot.
+ * x: f16/bf16/f32 [M,K] (rows contiguous); q: i8 [N,K] contiguous; scale: f32/f16 [N] or [N,1]
+ * or a single element; bias: optional (NULL) f32/f16/bf16 [N]; y: f16/bf16/f32 [M,N].
+ * convrot_groupsize: 0 for no rotation, else a Hadamard size (power of 4, or 2*4^p), <= 256.
+ * Replaces comfy_kitchen.int8_linear(x, qdata, scale, bias, out_dtype, convrot=...,
+ * convrot_groupsize=...)  (bench/bench_ck01_int8.py:57; bench/bench_lora_sidepath_kernel.py:77). */
+qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                             const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* A8 linear over AsymW4A8Int8 packed weights: per-token int8 activation quantization
+ * (quantize_int8_rowwise after the ConvRot rotation), int8 x int8 -> int32 MFMA on the int8
+ * weight grid w8 = clamp(rne(level * s_rel), -127, 127), epilogue fp32(acc) * sx[m] * s_channel[n]
+ * + bias.  qdata: i8/u8 [N, K*bits/8] (4-bit plane, then for 6 bits the 2-bit plane);
+ * s_rel: e4m3/f16/f32 [N, K/group_size]; s_channel: f32 [N]; codebook: optional f32 [16] (4-bit
+ * only; NULL = uniform levels code - 2^(bits-1)).
+ * Replaces comfy_kitchen ...w4a8_int8.w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook,
+ * correction, bias, group_size, convrot_groupsize, out_dtype)  (bench/bench_w4a8_linear.py:82-83;
+ * bench/bench_lora_fused_rank.py:42-44); `correction` (asymmetric variant) is not accepted. */
+qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                             const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                             qlin_tensor* y, int bits, int group_size, int convrot_groupsize,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* y[M,N] = x[M,K] @ W^T + bias, W decoded from GGUF blocks of `ggml_type` laid out as
+ * consecutive blocks over the row-major [N,K] elements (the GGUF tensor bytes, N*K/qk*ts long).
+ * Replaces comfy_kitchen.gguf_linear(x, weight, qtype, shape, bias, out_dtype)
+ * (docs/research/2026-10-03-gguf-on-metal.md:85; bench/bench_gguf_linear.py:120). */
+qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                             const qlin_tensor* bias, qlin_tensor* y,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* Decode GGUF blocks to a dense [N,K] f32 (bit-exact with gguf-py 0.19.0's fp32 decode), or
+ * f16/bf16 (that value rounded once, to nearest even).  Rows may straddle blocks (flat index).
+ * Replaces comfy_kitchen dequantize_gguf (docs/research/2026-10-03-gguf-on-metal.md:85, 100). */
+qlin_status qlin_dequantize_gguf(const void* weight, int ggml_type, int64_t N, int64_t K, qlin_tensor* out,
+                                 void* stream);
+
+/* Decode INT8 codes: out[n,k] = f32(q[n,k]) * scale[n] (rotated basis, bit-exact), then when
+ * convrot_groupsize > 0 rotate back to the original basis per group.
+ * Replaces dequantize_int8 / dequantize_int8_convrot_weight (modal/weight_error_app.py:122-127;
+ * bench/bench_ck01_int8.py:49). */
+qlin_status qlin_dequantize_int8(const qlin_tensor* qdata, const qlin_tensor* scale, qlin_tensor* out,
+                                 int convrot_groupsize, void* stream);
+
+/* Decode AsymW4A8Int8 storage: int8 grid w8 (when out is i8) or f32 w8*s_channel, rotated back
+ * per group when convrot_groupsize > 0 (f32 only).
+ * Replaces dequantize_w4a8_int8_weight (modal/weight_error_app.py:326-339;
+ * tests/test_training_packed.py:25-26). */
+qlin_status qlin_dequantize_w4a8(const qlin_tensor* qdata, const qlin_tensor* s_rel, const qlin_tensor* s_channel,
+                                 const qlin_tensor* codebook, qlin_tensor* out, int bits, int group_size,
+                                 int convrot_groupsize, void* stream);
+
+/* Per-token activation quantization: q[m,:], scale[m] = quantize_int8_rowwise(rot(x[m,:])) with
+ * the arithmetic done in x's dtype as the reference does (modal/weight_error_app.py:109-115).
+ * x: f16/bf16/f32 [M,K]; q: i8 [M,K]; scale: f32 [M]; convrot_groupsize 0 = no rotation.
+ * xrot (optional, may be NULL): receives the rotated activation in x's dtype. */
+qlin_status qlin_quantize_act_int8(const qlin_tensor* x, qlin_tensor* q, qlin_tensor* scale,
+                                   int convrot_groupsize, qlin_tensor* xrot, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLIN_H */

@@ -1,0 +1,78 @@
+"""Build libqlin.so (the HIP kernels + C ABI) for gfx950 with hipcc, in-tree.
+
+    python mac-kernels-public_amd/build_lib.py [--jobs N]
+
+Each .hip translation unit is compiled to an object in parallel, then linked into
+mac-kernels-public_amd/qlin/libqlin.so.  Packed-FP32 VALU instructions are disabled for all
+device code (-Xclang -target-feature -Xclang -packed-fp32-ops).
+"""
+import argparse
+import concurrent.futures as cf
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "qlin", "libqlin.so")
+BUILD = os.path.join(HERE, "_build")
+ARCH = os.environ.get("QLIN_ARCH", "gfx950")
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(HERE, "..", "include"),
+]
+
+
+def _stale(src, obj):
+    if not os.path.exists(obj):
+        return True
+    deps = [src] + glob.glob(os.path.join(CSRC, "*.h")) + [os.path.join(HERE, "..", "include", "qlin.h"), __file__]
+    return max(os.path.getmtime(d) for d in deps) > os.path.getmtime(obj)
+
+
+def _compile(src, force=True):
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if not force and not _stale(src, obj):
+        return src, obj, 0, ""
+    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that noise.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(line for line in r.stderr.splitlines() if noise not in line)
+    return src, obj, r.returncode, err
+
+
+def build(jobs=None, verbose=False, force=True):
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
+    objs = []
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        for src, obj, rc, err in ex.map(lambda s: _compile(s, force), srcs):
+            if err.strip() and (verbose or rc):
+                print(err, file=sys.stderr)
+            if rc:
+                raise RuntimeError(f"hipcc failed on {os.path.basename(src)}")
+            objs.append(obj)
+    tmp = OUT + ".tmp"
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs],
+                       capture_output=True, text=True)
+    if r.returncode:
+        print(r.stderr, file=sys.stderr)
+        raise RuntimeError("link failed")
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--incremental", action="store_true", help="recompile only stale objects")
+    a = ap.parse_args()
+    print(build(a.jobs, a.verbose, force=not a.incremental))

@@ -1,0 +1,477 @@
+// C ABI of libqlin (include/qlin.h): argument validation, workspace layout and dispatch.
+// Host code only; kernels live in the other translation units.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/qlin.h"
+#include "hadamard.h"
+#include "gguf_exact.h"
+#include "qlin_internal.h"
+
+using namespace qlin;
+
+namespace {
+
+thread_local std::string g_err;
+
+qlin_status fail(qlin_status s, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return s;
+}
+
+qlin_status hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return QLIN_OK;
+    return fail(QLIN_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool valid_group(int g) {
+    return g == 0 || g == 4 || g == 8 || g == 16 || g == 32 || g == 64 || g == 128 || g == 256;
+}
+
+struct Mat {
+    void* data;
+    int dtype;
+    int64_t rows, cols, ld;
+};
+
+// A 2-D matrix view with unit column stride; a 1-D tensor is one row.
+qlin_status as_matrix(const qlin_tensor* t, const char* name, Mat& m) {
+    if (!t || !t->data) return fail(QLIN_EINVAL, "%s is missing", name);
+    if (t->ndim == 1) {
+        if (t->shape[0] > 1 && t->stride[0] != 1) return fail(QLIN_EUNSUPPORTED, "%s must be contiguous", name);
+        m = {t->data, t->dtype, 1, t->shape[0], t->shape[0]};
+        return QLIN_OK;
+    }
+    if (t->ndim != 2) return fail(QLIN_EUNSUPPORTED, "%s must be 1-D or 2-D (flatten leading dims)", name);
+    if (t->shape[1] > 1 && t->stride[1] != 1) return fail(QLIN_EUNSUPPORTED, "%s needs unit column stride", name);
+    int64_t ld = t->shape[0] > 1 ? t->stride[0] : t->shape[1];
+    if (ld < t->shape[1]) return fail(QLIN_EINVAL, "%s row stride %lld < cols %lld", name, (long long)ld,
+                                      (long long)t->shape[1]);
+    m = {t->data, t->dtype, t->shape[0], t->shape[1], ld};
+    return QLIN_OK;
+}
+
+int64_t numel(const qlin_tensor* t) {
+    int64_t n = 1;
+    for (int i = 0; i < t->ndim; ++i) n *= t->shape[i];
+    return n;
+}
+
+// A vector of n elements (any of [n], [n,1], [1,n]); returns its element stride.
+qlin_status as_vector(const qlin_tensor* t, const char* name, int64_t n, bool allow_scalar, int64_t& stride) {
+    if (!t || !t->data) return fail(QLIN_EINVAL, "%s is missing", name);
+    int64_t cnt = numel(t);
+    if (allow_scalar && cnt == 1) {
+        stride = 0;
+        return QLIN_OK;
+    }
+    if (cnt != n) return fail(QLIN_EINVAL, "%s has %lld elements, expected %lld", name, (long long)cnt, (long long)n);
+    stride = 1;
+    for (int i = 0; i < t->ndim; ++i)
+        if (t->shape[i] == n) stride = t->stride[i];
+    if (n > 1 && stride != 1) return fail(QLIN_EUNSUPPORTED, "%s must be contiguous", name);
+    return QLIN_OK;
+}
+
+bool is_float(int dt) { return dt == QLIN_DT_F32 || dt == QLIN_DT_F16 || dt == QLIN_DT_BF16; }
+
+qlin_status check_bias(const qlin_tensor* bias, int64_t N, int& bias_dtype) {
+    bias_dtype = DT_NONE;
+    if (!bias || !bias->data) return QLIN_OK;
+    int64_t st;
+    qlin_status s = as_vector(bias, "bias", N, false, st);
+    if (s) return s;
+    if (!is_float(bias->dtype)) return fail(QLIN_EUNSUPPORTED, "bias dtype %d unsupported", bias->dtype);
+    bias_dtype = bias->dtype;
+    return QLIN_OK;
+}
+
+qlin_status check_xy(const qlin_tensor* x, qlin_tensor* y, int64_t N, int64_t K, Mat& X, Mat& Y) {
+    qlin_status s = as_matrix(x, "x", X);
+    if (s) return s;
+    if (!is_float(X.dtype)) return fail(QLIN_EUNSUPPORTED, "x dtype %d unsupported", X.dtype);
+    if (X.cols != K) return fail(QLIN_EINVAL, "x has K=%lld, weight has K=%lld", (long long)X.cols, (long long)K);
+    s = as_matrix(y, "y", Y);
+    if (s) return s;
+    if (!is_float(Y.dtype)) return fail(QLIN_EUNSUPPORTED, "y dtype %d unsupported", Y.dtype);
+    if (Y.rows != X.rows || Y.cols != N)
+        return fail(QLIN_EINVAL, "y must be [%lld, %lld]", (long long)X.rows, (long long)N);
+    return QLIN_OK;
+}
+
+// Workspace carve-out (256-byte aligned pieces).
+struct Carver {
+    uint8_t* base;
+    size_t cap, used = 0;
+    void* take(size_t bytes) {
+        void* p = base ? base + used : nullptr;
+        used += align_up(bytes);
+        return p;
+    }
+};
+
+size_t ws_int8(int64_t M, int64_t K) { return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4); }
+size_t ws_gguf(int64_t M, int64_t N, int64_t K) {
+    return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4);
+}
+size_t ws_w4a8(int64_t M, int64_t K) { return align_up((size_t)(M * K)) + align_up((size_t)M * 4); }
+
+// Runs the weight-only prologue unless x is already usable as the fp16 MFMA operand (fp16, no
+// rotation, aligned rows), in which case x itself is used and no exponents are needed.
+qlin_status wo_activations(const Mat& X, int G, Carver& ws, hipStream_t st, const f16*& xo, int64_t& ldx,
+                           const int32_t*& eo) {
+    if (G == 0 && X.dtype == QLIN_DT_F16 && X.ld % 8 == 0 && (uintptr_t)X.data % 16 == 0) {
+        xo = (const f16*)X.data;
+        ldx = X.ld;
+        eo = nullptr;
+        (void)ws.take((size_t)(X.rows * X.cols * 2));
+        (void)ws.take((size_t)X.rows * 4);
+        return QLIN_OK;
+    }
+    PrologueArgs p;
+    p.mode = PROLOGUE_WO;
+    p.x_dtype = X.dtype;
+    p.x = X.data;
+    p.ldx = X.ld;
+    p.M = X.rows;
+    p.K = (int)X.cols;
+    p.G = G;
+    p.xo = (f16*)ws.take((size_t)(X.rows * X.cols * 2));
+    p.ldo = X.cols;
+    p.eo = (int32_t*)ws.take((size_t)X.rows * 4);
+    xo = p.xo;
+    ldx = X.cols;
+    eo = p.eo;
+    return hip_status(run_prologue(p, st), "prologue");
+}
+
+}  // namespace
+
+extern "C" {
+
+int qlin_version(void) { return 1; }
+
+const char* qlin_status_string(qlin_status s) {
+    switch (s) {
+        case QLIN_OK: return "ok";
+        case QLIN_EUNSUPPORTED: return "unsupported";
+        case QLIN_EINVAL: return "invalid argument";
+        case QLIN_EHIP: return "HIP error";
+        case QLIN_EWORKSPACE: return "workspace too small";
+    }
+    return "unknown";
+}
+
+const char* qlin_last_error(void) { return g_err.c_str(); }
+
+size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, int x_dtype) {
+    (void)param;
+    (void)x_dtype;
+    switch (op) {
+        case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
+        case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, K);
+        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K);
+    }
+    return 0;
+}
+
+qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x_dtype, int out_dtype) {
+    if (M < 0 || N < 0 || K < 0) return fail(QLIN_EINVAL, "negative shape");
+    if (!is_float(x_dtype) || !is_float(out_dtype)) return fail(QLIN_EUNSUPPORTED, "dtype unsupported");
+    switch (op) {
+        case QLIN_OP_INT8_LINEAR:
+            if (!valid_group(param)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", param);
+            if (param && K % param) return fail(QLIN_EUNSUPPORTED, "K %% group != 0");
+            if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+            return QLIN_OK;
+        case QLIN_OP_W4A8_LINEAR:
+            if (param != 4 && param != 6) return fail(QLIN_EUNSUPPORTED, "bits %d unsupported", param);
+            if (K % 64) return fail(QLIN_EUNSUPPORTED, "K %% 64 != 0");
+            if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+            return QLIN_OK;
+        case QLIN_OP_GGUF_LINEAR: {
+            int qk, ts;
+            if (!gguf::type_info(param, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", param);
+            if (K % qk) return fail(QLIN_EUNSUPPORTED, "K %% block != 0 (rows straddle blocks)");
+            if (K % 32) return fail(QLIN_EUNSUPPORTED, "K %% 32 != 0");
+            if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+            return QLIN_OK;
+        }
+    }
+    return fail(QLIN_EUNSUPPORTED, "unknown op %d", op);
+}
+
+qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                             const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    Mat Q, X, Y;
+    qlin_status s = as_matrix(qdata, "qdata", Q);
+    if (s) return s;
+    if (Q.dtype != QLIN_DT_I8) return fail(QLIN_EUNSUPPORTED, "qdata must be int8");
+    const int64_t N = Q.rows, K = Q.cols;
+    if ((s = check_xy(x, y, N, K, X, Y))) return s;
+    if (!valid_group(convrot_groupsize)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
+    if (convrot_groupsize && K % convrot_groupsize)
+        return fail(QLIN_EINVAL, "K=%lld is not a multiple of the ConvRot group %d", (long long)K, convrot_groupsize);
+    if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    int64_t sst;
+    if ((s = as_vector(scale, "scale", N, true, sst))) return s;
+    if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype %d unsupported", scale->dtype);
+    int bdt;
+    if ((s = check_bias(bias, N, bdt))) return s;
+    const int64_t M = X.rows;
+    if (workspace_bytes < ws_int8(M, K)) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_int8(M, K));
+    if (M == 0 || N == 0) return QLIN_OK;
+    hipStream_t st = (hipStream_t)stream;
+    Carver ws{(uint8_t*)workspace, workspace_bytes};
+    GemmF16Args a;
+    if ((s = wo_activations(X, convrot_groupsize, ws, st, a.x, a.ldx, a.xexp))) return s;
+    a.wkind = WO_INT8;
+    a.M = M; a.N = N; a.K = K;
+    a.w = Q.data; a.ldw = Q.ld;
+    a.scale = scale->data; a.scale_dtype = scale->dtype; a.scale_stride = sst;
+    a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
+    a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+    return hip_status(run_gemm_f16(a, st), "int8 gemm");
+}
+
+qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                             const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+    int qk, ts;
+    if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
+    if (!weight) return fail(QLIN_EINVAL, "weight is missing");
+    if (K % qk) return fail(QLIN_EUNSUPPORTED, "K=%lld is not a whole number of %d-value blocks", (long long)K, qk);
+    if (K % 32) return fail(QLIN_EUNSUPPORTED, "K %% 32 != 0");
+    if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    Mat X, Y;
+    qlin_status s = check_xy(x, y, N, K, X, Y);
+    if (s) return s;
+    int bdt;
+    if ((s = check_bias(bias, N, bdt))) return s;
+    const int64_t M = X.rows;
+    if (workspace_bytes < ws_gguf(M, N, K))
+        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_gguf(M, N, K));
+    if (M == 0 || N == 0) return QLIN_OK;
+    const int64_t row_bytes = (K / qk) * ts;
+    hipStream_t st = (hipStream_t)stream;
+    Carver ws{(uint8_t*)workspace, workspace_bytes};
+    const bool aligned = ((uintptr_t)weight % 4) == 0;
+    if (aligned && gguf_smallm_supported(ggml_type, M, K, row_bytes)) {
+        GgufSmallMArgs a;
+        a.type = ggml_type;
+        int64_t ldx;
+        if ((s = wo_activations(X, 0, ws, st, a.x, ldx, a.xexp))) return s;
+        a.ldx = ldx;
+        a.M = (int)M; a.N = (int)N; a.K = (int)K;
+        a.w = (const uint8_t*)weight; a.row_bytes = row_bytes;
+        a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
+        a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+        return hip_status(run_gguf_smallm(a, st), "gguf small-M");
+    }
+    GemmF16Args a;
+    if ((s = wo_activations(X, 0, ws, st, a.x, a.ldx, a.xexp))) return s;
+    int32_t* wexp = (int32_t*)ws.take((size_t)N * 4);
+    if ((s = hip_status(run_gguf_row_exp(ggml_type, (const uint8_t*)weight, N, K, wexp, st), "gguf row exponents")))
+        return s;
+    a.wkind = WO_GGUF;
+    a.gguf_type = ggml_type;
+    a.M = M; a.N = N; a.K = K;
+    a.w = weight; a.ldw = row_bytes;
+    a.wexp = wexp;
+    a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
+    a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+    return hip_status(run_gemm_f16(a, st), "gguf gemm");
+}
+
+qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                             const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                             qlin_tensor* y, int bits, int group_size, int convrot_groupsize, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    if (bits != 4 && bits != 6) return fail(QLIN_EUNSUPPORTED, "bits=%d unsupported (4 or 6)", bits);
+    Mat Q, X, Y, SR;
+    qlin_status s = as_matrix(qdata, "qdata", Q);
+    if (s) return s;
+    if (Q.dtype != QLIN_DT_I8 && Q.dtype != QLIN_DT_U8) return fail(QLIN_EUNSUPPORTED, "qdata must be int8/uint8");
+    if ((Q.cols * 8) % bits) return fail(QLIN_EINVAL, "qdata columns do not hold whole codes");
+    const int64_t N = Q.rows, K = Q.cols * 8 / bits;
+    if ((s = check_xy(x, y, N, K, X, Y))) return s;
+    if (group_size <= 0 || group_size % 8 || K % group_size)
+        return fail(QLIN_EUNSUPPORTED, "group_size %d unsupported for K=%lld", group_size, (long long)K);
+    if (K % 64) return fail(QLIN_EUNSUPPORTED, "K %% 64 != 0");
+    if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    if (Q.ld % 16 || (uintptr_t)Q.data % 16) return fail(QLIN_EUNSUPPORTED, "qdata rows must be 16-byte aligned");
+    if (!valid_group(convrot_groupsize)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
+    if (convrot_groupsize && K % convrot_groupsize) return fail(QLIN_EINVAL, "K %% ConvRot group != 0");
+    if ((s = as_matrix(s_rel, "s_rel", SR))) return s;
+    if (SR.rows != N || SR.cols != K / group_size)
+        return fail(QLIN_EINVAL, "s_rel must be [%lld, %lld]", (long long)N, (long long)(K / group_size));
+    if (SR.dtype != QLIN_DT_E4M3 && SR.dtype != QLIN_DT_F16 && SR.dtype != QLIN_DT_BF16 && SR.dtype != QLIN_DT_F32 &&
+        SR.dtype != QLIN_DT_U8)
+        return fail(QLIN_EUNSUPPORTED, "s_rel dtype %d unsupported", SR.dtype);
+    int64_t sst;
+    if ((s = as_vector(s_channel, "s_channel", N, false, sst))) return s;
+    if (s_channel->dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "s_channel must be float32");
+    const float* cb = nullptr;
+    if (codebook && codebook->data) {
+        if (bits != 4) return fail(QLIN_EUNSUPPORTED, "a codebook is only defined for 4-bit codes");
+        int64_t cst;
+        if ((s = as_vector(codebook, "codebook", 16, false, cst))) return s;
+        if (codebook->dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "codebook must be float32");
+        cb = (const float*)codebook->data;
+    }
+    int bdt;
+    if ((s = check_bias(bias, N, bdt))) return s;
+    const int64_t M = X.rows;
+    if (workspace_bytes < ws_w4a8(M, K)) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_w4a8(M, K));
+    if (M == 0 || N == 0) return QLIN_OK;
+    hipStream_t st = (hipStream_t)stream;
+    Carver ws{(uint8_t*)workspace, workspace_bytes};
+    PrologueArgs p;
+    p.mode = PROLOGUE_A8;
+    p.x_dtype = X.dtype;
+    p.x = X.data;
+    p.ldx = X.ld;
+    p.M = M;
+    p.K = (int)K;
+    p.G = convrot_groupsize;
+    p.qo = (int8_t*)ws.take((size_t)(M * K));
+    p.ldo = K;
+    p.so = (float*)ws.take((size_t)M * 4);
+    if ((s = hip_status(run_prologue(p, st), "A8 prologue"))) return s;
+    GemmI8Args g;
+    g.xq = p.qo; g.ldx = K; g.sx = p.so;
+    g.M = M; g.N = N; g.K = K;
+    g.q = (const uint8_t*)Q.data; g.ldq = Q.ld; g.bits = bits; g.group_size = group_size;
+    g.s_rel = SR.data; g.s_rel_dtype = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype; g.ld_srel = SR.ld;
+    g.s_ch = (const float*)s_channel->data; g.codebook = cb;
+    g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
+    g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
+    return hip_status(run_gemm_i8(g, st), "A8 gemm");
+}
+
+qlin_status qlin_dequantize_gguf(const void* weight, int ggml_type, int64_t N, int64_t K, qlin_tensor* out,
+                                 void* stream) {
+    int qk, ts;
+    if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
+    if (!weight) return fail(QLIN_EINVAL, "weight is missing");
+    if ((N * K) % qk) return fail(QLIN_EINVAL, "N*K is not a whole number of blocks");
+    if (!out || !out->data || !is_float(out->dtype)) return fail(QLIN_EINVAL, "out must be a float tensor");
+    if (numel(out) != N * K) return fail(QLIN_EINVAL, "out must hold N*K elements");
+    for (int i = out->ndim - 1, expect = 1; i >= 0; --i) {
+        if (out->shape[i] > 1 && out->stride[i] != expect) return fail(QLIN_EUNSUPPORTED, "out must be contiguous");
+        expect *= (int)out->shape[i];
+    }
+    if (out->dtype == QLIN_DT_F32 && (uintptr_t)out->data % 16) return fail(QLIN_EUNSUPPORTED, "out must be 16-byte aligned");
+    return hip_status(run_dequant_gguf(ggml_type, (const uint8_t*)weight, N * K, out->data, out->dtype,
+                                       (hipStream_t)stream), "gguf dequantize");
+}
+
+qlin_status qlin_dequantize_int8(const qlin_tensor* qdata, const qlin_tensor* scale, qlin_tensor* out,
+                                 int convrot_groupsize, void* stream) {
+    Mat Q, O;
+    qlin_status s = as_matrix(qdata, "qdata", Q);
+    if (s) return s;
+    if (Q.dtype != QLIN_DT_I8) return fail(QLIN_EUNSUPPORTED, "qdata must be int8");
+    if ((s = as_matrix(out, "out", O))) return s;
+    if (O.dtype != QLIN_DT_F32 || O.rows != Q.rows || O.cols != Q.cols || O.ld != O.cols)
+        return fail(QLIN_EINVAL, "out must be a contiguous float32 [N, K]");
+    int64_t sst;
+    if ((s = as_vector(scale, "scale", Q.rows, true, sst))) return s;
+    if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype unsupported");
+    if (!valid_group(convrot_groupsize) || (convrot_groupsize && Q.cols % convrot_groupsize))
+        return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported for K=%lld", convrot_groupsize, (long long)Q.cols);
+    hipStream_t st = (hipStream_t)stream;
+    if ((s = hip_status(run_dequant_int8((const int8_t*)Q.data, Q.rows, Q.cols, Q.ld, scale->data, scale->dtype, sst,
+                                         (float*)O.data, st), "int8 dequantize")))
+        return s;
+    if (convrot_groupsize) {
+        if (Q.cols > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+        PrologueArgs p;
+        p.mode = PROLOGUE_ROT_F32; p.x_dtype = DT_F32; p.x = O.data; p.ldx = O.cols;
+        p.M = O.rows; p.K = (int)O.cols; p.G = convrot_groupsize; p.fo = (float*)O.data; p.ldo = O.cols;
+        return hip_status(run_prologue(p, st), "rotation");
+    }
+    return QLIN_OK;
+}
+
+qlin_status qlin_dequantize_w4a8(const qlin_tensor* qdata, const qlin_tensor* s_rel, const qlin_tensor* s_channel,
+                                 const qlin_tensor* codebook, qlin_tensor* out, int bits, int group_size,
+                                 int convrot_groupsize, void* stream) {
+    if (bits != 4 && bits != 6) return fail(QLIN_EUNSUPPORTED, "bits=%d unsupported", bits);
+    Mat Q, SR, O;
+    qlin_status s = as_matrix(qdata, "qdata", Q);
+    if (s) return s;
+    const int64_t N = Q.rows, K = Q.cols * 8 / bits;
+    if (group_size <= 0 || K % group_size) return fail(QLIN_EINVAL, "group_size does not divide K");
+    if ((s = as_matrix(s_rel, "s_rel", SR))) return s;
+    if (SR.rows != N || SR.cols != K / group_size) return fail(QLIN_EINVAL, "s_rel shape mismatch");
+    if ((s = as_matrix(out, "out", O))) return s;
+    if (O.rows != N || O.cols != K || O.ld != K) return fail(QLIN_EINVAL, "out must be a contiguous [N, K]");
+    if (O.dtype != QLIN_DT_I8 && O.dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "out must be int8 or float32");
+    if (O.dtype == QLIN_DT_I8 && convrot_groupsize) return fail(QLIN_EINVAL, "the int8 grid has no original-basis form");
+    int64_t sst;
+    if ((s = as_vector(s_channel, "s_channel", N, false, sst))) return s;
+    const float* cb = nullptr;
+    if (codebook && codebook->data) {
+        int64_t cst;
+        if ((s = as_vector(codebook, "codebook", 16, false, cst))) return s;
+        cb = (const float*)codebook->data;
+    }
+    if (!valid_group(convrot_groupsize) || (convrot_groupsize && K % convrot_groupsize))
+        return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
+    hipStream_t st = (hipStream_t)stream;
+    const int srdt = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype;
+    if ((s = hip_status(run_dequant_w4a8((const uint8_t*)Q.data, N, K, Q.ld, bits, group_size, SR.data, srdt, SR.ld,
+                                         (const float*)s_channel->data, cb, O.data, O.dtype, st), "w4a8 dequantize")))
+        return s;
+    if (convrot_groupsize) {
+        if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+        PrologueArgs p;
+        p.mode = PROLOGUE_ROT_F32; p.x_dtype = DT_F32; p.x = O.data; p.ldx = K;
+        p.M = N; p.K = (int)K; p.G = convrot_groupsize; p.fo = (float*)O.data; p.ldo = K;
+        return hip_status(run_prologue(p, st), "rotation");
+    }
+    return QLIN_OK;
+}
+
+qlin_status qlin_quantize_act_int8(const qlin_tensor* x, qlin_tensor* q, qlin_tensor* scale, int convrot_groupsize,
+                                   qlin_tensor* xrot, void* stream) {
+    Mat X, Qm;
+    qlin_status s = as_matrix(x, "x", X);
+    if (s) return s;
+    if (!is_float(X.dtype)) return fail(QLIN_EUNSUPPORTED, "x dtype unsupported");
+    if ((s = as_matrix(q, "q", Qm))) return s;
+    if (Qm.dtype != QLIN_DT_I8 || Qm.rows != X.rows || Qm.cols != X.cols || Qm.ld != X.cols)
+        return fail(QLIN_EINVAL, "q must be a contiguous int8 [M, K]");
+    int64_t sst;
+    if ((s = as_vector(scale, "scale", X.rows, false, sst))) return s;
+    if (scale->dtype != QLIN_DT_F32) return fail(QLIN_EINVAL, "scale must be float32");
+    if (!valid_group(convrot_groupsize) || (convrot_groupsize && X.cols % convrot_groupsize))
+        return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
+    if (X.cols > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    void* xr = nullptr;
+    if (xrot && xrot->data) {
+        Mat XR;
+        if ((s = as_matrix(xrot, "xrot", XR))) return s;
+        if (XR.dtype != X.dtype || XR.rows != X.rows || XR.cols != X.cols || XR.ld != X.cols)
+            return fail(QLIN_EINVAL, "xrot must be a contiguous [M, K] in x's dtype");
+        xr = XR.data;
+    }
+    PrologueArgs p;
+    p.mode = PROLOGUE_A8; p.x_dtype = X.dtype; p.x = X.data; p.ldx = X.ld; p.M = X.rows; p.K = (int)X.cols;
+    p.G = convrot_groupsize; p.qo = (int8_t*)Qm.data; p.ldo = X.cols; p.so = (float*)scale->data; p.xr = xr;
+    return hip_status(run_prologue(p, (hipStream_t)stream), "activation quantization");
+}
+
+}  // extern "C"

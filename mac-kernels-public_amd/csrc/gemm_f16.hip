@@ -1,0 +1,273 @@
+// Weight-only linear for large M on the fp16 MFMA (v_mfma_f32_16x16x32_f16), fp32 accumulate.
+//
+// Tile 128 (M) x 128 (N) x 64 (K), 256 threads = 4 waves in a 2x2 grid, each wave 64x64 (4x4
+// MFMA tiles).  Activations arrive as the prologue's range-normalized fp16 rows (x * 2^-E[m]).
+// The packed weight tile is decoded in the load stage, straight into the fp16 B tile in LDS:
+//   INT8: w = q exactly (|q| <= 128 is exact in fp16); the per-channel scale joins the epilogue.
+//   GGUF: w = fp16(value * 2^-e[n]) with value the exact fp32 decode and e[n] the row exponent of
+//         max|w[n,:]| (so |w| < 1 and the fp16 GEMM cannot overflow for K <= 65504).
+// Epilogue: y = acc * 2^E[m] * (scale[n] | 2^e[n]) + bias[n], cast to the output dtype.
+// Global->LDS is double-buffered through registers: the next tile's loads are issued before the
+// current tile's MFMAs.
+#include "qlin_internal.h"
+#include "gguf_exact.h"
+
+namespace qlin {
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64, PADK = 8, LDK = BK + PADK;  // LDS row: 72 halves
+
+struct TileRegs {
+    u32x4 a[4];   // 32 fp16 of one A row half
+    u32x4 b[4];   // 32 fp16 of one B row half (already decoded)
+};
+
+__device__ __forceinline__ uint32_t pack2(f16 lo, f16 hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+// A: row r = tid/2 of the tile, 32 halves from column 32*(tid%2).
+__device__ __forceinline__ void load_a(const f16* __restrict__ x, int64_t ldx, int64_t M, int64_t K, int64_t m0,
+                                       int64_t k0, int tid, bool vec_ok, TileRegs& R) {
+    const int r = tid >> 1, h = tid & 1;
+    const int64_t m = m0 + r, k = k0 + 32 * h;
+    if (m < M && vec_ok && k + 32 <= K) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(x + m * ldx + k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) R.a[i] = p[i];
+    } else {
+        uint32_t w[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            f16 lo = (f16)0.0f, hi = (f16)0.0f;
+            if (m < M && k + 2 * i < K) lo = x[m * ldx + k + 2 * i];
+            if (m < M && k + 2 * i + 1 < K) hi = x[m * ldx + k + 2 * i + 1];
+            w[i] = pack2(lo, hi);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) R.a[i] = u32x4{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+    }
+}
+
+// INT8 weight tile: row n = tid/2, 32 int8 from column 32*(tid%2) -> 32 exact fp16.
+__device__ __forceinline__ void load_b_int8(const int8_t* __restrict__ w, int64_t ldw, int64_t N, int64_t K,
+                                            int64_t n0, int64_t k0, int tid, bool vec_ok, TileRegs& R) {
+    const int r = tid >> 1, h = tid & 1;
+    const int64_t n = n0 + r, k = k0 + 32 * h;
+    int8_t v[32];
+    if (n < N && vec_ok && k + 32 <= K) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(w + n * ldw + k);
+        u32x4 a = p[0], b = p[1];
+        uint32_t ww[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = (int8_t)(ww[i >> 2] >> (8 * (i & 3)));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = (n < N && k + i < K) ? w[n * ldw + k + i] : (int8_t)0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t p[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = pack2((f16)(float)v[8 * i + 2 * j], (f16)(float)v[8 * i + 2 * j + 1]);
+        R.b[i] = u32x4{p[0], p[1], p[2], p[3]};
+    }
+}
+
+// GGUF weight tile: row n = tid/2, 32 values from column 32*(tid%2): exact fp32 decode, scaled by
+// 2^-e[n], rounded once to fp16.  Requires K % 32 == 0 and rows made of whole blocks.
+template <int T>
+__device__ __forceinline__ void load_b_gguf(const uint8_t* __restrict__ w, int64_t N, int64_t K,
+                                            const int32_t* __restrict__ wexp, int64_t n0, int64_t k0, int tid,
+                                            TileRegs& R) {
+    constexpr int QK = gguf::Info<T>::QK, TS = gguf::Info<T>::TS;
+    const int r = tid >> 1, h = tid & 1;
+    const int64_t n = n0 + r, k = k0 + 32 * h;
+    if (n < N && k < K) {
+        const int64_t row_bytes = (K / QK) * TS;
+        const int64_t blk = k / QK;
+        const int j0 = (int)(k - blk * QK);
+        const uint8_t* b = w + n * row_bytes + blk * TS;
+        const int e = wexp[n];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v[8];
+            gguf::decode8<T>(b, j0 + 8 * i, v);
+            uint32_t p[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                p[j] = pack2((f16)__builtin_ldexpf(v[2 * j], -e), (f16)__builtin_ldexpf(v[2 * j + 1], -e));
+            R.b[i] = u32x4{p[0], p[1], p[2], p[3]};
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) R.b[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+__device__ __forceinline__ void store_tile(f16* As, f16* Bs, int tid, const TileRegs& R) {
+    const int r = tid >> 1, h = tid & 1;
+    u32x4* pa = reinterpret_cast<u32x4*>(As + r * LDK + 32 * h);
+    u32x4* pb = reinterpret_cast<u32x4*>(Bs + r * LDK + 32 * h);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        pa[i] = R.a[i];
+        pb[i] = R.b[i];
+    }
+}
+
+template <int WK, int GT, typename TOut, typename TBias, typename TScale>
+__global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
+    __shared__ __attribute__((aligned(16))) f16 smem[2][2][BM * LDK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
+    const f16* x = a.x;
+    const bool a_vec = (a.ldx % 8 == 0) && ((uintptr_t)x % 16 == 0);
+    const bool b_vec = (a.ldw % 16 == 0) && ((uintptr_t)a.w % 16 == 0);
+    const int ktiles = (int)((a.K + BK - 1) / BK);
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    TileRegs R;
+    auto fetch = [&](int kt) {
+        const int64_t k0 = (int64_t)kt * BK;
+        load_a(x, a.ldx, a.M, a.K, m0, k0, tid, a_vec, R);
+        if constexpr (WK == WO_INT8) load_b_int8((const int8_t*)a.w, a.ldw, a.N, a.K, n0, k0, tid, b_vec, R);
+        else load_b_gguf<GT>((const uint8_t*)a.w, a.N, a.K, a.wexp, n0, k0, tid, R);
+    };
+
+    fetch(0);
+    store_tile(smem[0][0], smem[0][1], tid, R);
+    __syncthreads();
+    const int r16 = lane & 15, g = lane >> 4;
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ktiles) fetch(kt + 1);
+        const f16* As = smem[buf][0];
+        const f16* Bs = smem[buf][1];
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            f16x8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[i] = *reinterpret_cast<const f16x8*>(As + (wm * 64 + i * 16 + r16) * LDK + kk * 32 + 8 * g);
+                bf[i] = *reinterpret_cast<const f16x8*>(Bs + (wn * 64 + i * 16 + r16) * LDK + kk * 32 + 8 * g);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < ktiles) store_tile(smem[buf ^ 1][0], smem[buf ^ 1][1], tid, R);
+        __syncthreads();
+    }
+
+    // Epilogue.  acc[i][j][v] = D[m = wm*64 + 16i + 4g + v][n = wn*64 + 16j + r16].
+    TOut* y = (TOut*)a.y;
+    const TBias* bias = (const TBias*)a.bias;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t n = n0 + wn * 64 + 16 * j + r16;
+        if (n >= a.N) continue;
+        float cs;
+        int ce = 0;
+        if constexpr (WK == WO_INT8) cs = load_f((const TScale*)a.scale + n * a.scale_stride);
+        else { cs = 1.0f; ce = a.wexp[n]; }
+        const float bv = bias ? load_f(bias + n) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t m = m0 + wm * 64 + 16 * i + 4 * g + v;
+                if (m >= a.M) continue;
+                const int e = (a.xexp ? a.xexp[m] : 0) + ce;
+                float val = __builtin_ldexpf(acc[i][j][v], e);
+                if constexpr (WK == WO_INT8) val *= cs;
+                val += bv;
+                store_out(y + m * a.ldy + n, val);
+            }
+    }
+}
+
+template <int WK, int GT, typename TOut, typename TBias>
+hipError_t launch3(const GemmF16Args& a, hipStream_t st) {
+    dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);
+    if constexpr (WK == WO_INT8) {
+        if (a.scale_dtype == DT_F32) hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, float>), grid, block, 0, st, a);
+        else if (a.scale_dtype == DT_F16) hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, f16>), grid, block, 0, st, a);
+        else if (a.scale_dtype == DT_BF16) hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, bf16_t>), grid, block, 0, st, a);
+        else return hipErrorInvalidValue;
+    } else {
+        hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, float>), grid, block, 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <int WK, int GT, typename TOut>
+hipError_t launch2(const GemmF16Args& a, hipStream_t st) {
+    switch (a.bias_dtype) {
+        case DT_F16: return launch3<WK, GT, TOut, f16>(a, st);
+        case DT_BF16: return launch3<WK, GT, TOut, bf16_t>(a, st);
+        default: return launch3<WK, GT, TOut, float>(a, st);
+    }
+}
+
+template <int WK, int GT>
+hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
+    switch (a.y_dtype) {
+        case DT_F32: return launch2<WK, GT, float>(a, st);
+        case DT_F16: return launch2<WK, GT, f16>(a, st);
+        case DT_BF16: return launch2<WK, GT, bf16_t>(a, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void gguf_row_exp_kernel(const uint8_t* __restrict__ w, int64_t K,
+                                                            int32_t* __restrict__ e) {
+    constexpr int QK = gguf::Info<T>::QK, TS = gguf::Info<T>::TS;
+    __shared__ float red[4];
+    const int64_t n = blockIdx.x;
+    const int64_t row_bytes = (K / QK) * TS;
+    const uint8_t* row = w + n * row_bytes;
+    float amax = 0.0f;
+    for (int64_t j = (int64_t)threadIdx.x * 8; j < K; j += 256 * 8) {
+        const int64_t blk = j / QK;
+        float v[8];
+        gguf::decode8<T>(row + blk * TS, (int)(j - blk * QK), v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(v[t]));
+    }
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) e[n] = frexp_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+
+}  // namespace
+
+hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st) {
+    if (a.M == 0 || a.N == 0) return hipSuccess;
+    if (a.wkind == WO_INT8) return launch1<WO_INT8, 0>(a, st);
+    hipError_t err = hipErrorInvalidValue;
+    bool ok = gguf::dispatch_type(a.gguf_type, [&]<int T>() { err = launch1<WO_GGUF, T>(a, st); });
+    return ok ? err : hipErrorInvalidValue;
+}
+
+hipError_t run_gguf_row_exp(int type, const uint8_t* w, int64_t N, int64_t K, int32_t* e, hipStream_t st) {
+    if (N == 0) return hipSuccess;
+    hipError_t err = hipErrorInvalidValue;
+    bool ok = gguf::dispatch_type(type, [&]<int T>() {
+        hipLaunchKernelGGL((gguf_row_exp_kernel<T>), dim3((unsigned)N), dim3(256), 0, st, w, K, e);
+        err = hipGetLastError();
+    });
+    return ok ? err : hipErrorInvalidValue;
+}
+
+}  // namespace qlin

@@ -1,0 +1,202 @@
+// Activation prologue: per-row ConvRot rotation, then either
+//   * weight-only mode: x' = rot(x) * 2^-E (E = frexp exponent of the row's max |rot(x)|),
+//     rounded once to fp16, plus E -- the range-safe operand of the fp16 MFMA GEMMs; or
+//   * A8 mode: quantize_int8_rowwise of rot(x) in x's dtype (roblennon/mac-kernels-public
+//     modal/weight_error_app.py:109-115): scale = max(absmax/127, 1e-30) in fp32,
+//     s = dtype(scale) (0 -> dtype tiny), q = clamp(rne(dtype(x / s)), -128, 127); or
+//   * rotate-only mode (fp32 rows in, fp32 rows out), used to bring decoded weights back to the
+//     original basis.
+// One 256-thread workgroup per row; each thread holds 16 consecutive elements per 4096-element
+// slot, so a rotation group (<= 256 elements) lives in one 16-lane DPP row.
+#include "qlin_internal.h"
+#include "hadamard.h"
+
+namespace qlin {
+
+template <typename T> struct vec16_io;
+
+template <typename TIn>
+__device__ __forceinline__ void load16(const TIn* row, int64_t e0, int K, bool vec_ok, float* v) {
+    if (vec_ok && e0 + 16 <= K) {
+        if constexpr (sizeof(TIn) == 2) {
+            const u32x4* p = reinterpret_cast<const u32x4*>(row + e0);
+            u32x4 a = p[0], b = p[1];
+            uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                TIn lo, hi;
+                uint16_t l16 = (uint16_t)(w[i] & 0xFFFFu), h16 = (uint16_t)(w[i] >> 16);
+                __builtin_memcpy(&lo, &l16, 2);
+                __builtin_memcpy(&hi, &h16, 2);
+                v[2 * i] = dtype_traits<TIn>::to_f32(lo);
+                v[2 * i + 1] = dtype_traits<TIn>::to_f32(hi);
+            }
+        } else {
+            const f32x4* p = reinterpret_cast<const f32x4*>(row + e0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f32x4 a = p[i];
+                v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = (e0 + i < K) ? dtype_traits<TIn>::to_f32(row[e0 + i]) : 0.0f;
+    }
+}
+
+template <typename TIn, int MODE, int G, int SLOTS>
+__global__ __launch_bounds__(256) void prologue_kernel(const TIn* __restrict__ x, int64_t ldx, int K,
+                                                       bool vec_ok, f16* __restrict__ xo, int64_t ldo,
+                                                       int32_t* __restrict__ eo, int8_t* __restrict__ qo,
+                                                       float* __restrict__ so, TIn* __restrict__ xr,
+                                                       float* __restrict__ fo) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const TIn* row = x + (int64_t)m * ldx;
+    float v[SLOTS][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+        load16<TIn>(row, e0, K, vec_ok, v[s]);
+        if constexpr (G > 0) {
+            hadamard16<G>(v[s], lane);
+            const float nrm = hadamard_norm<G>();
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[s][i] *= nrm;
+        }
+        if constexpr (MODE == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[s][i] = round_to<TIn>(v[s][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[s][i]));
+    }
+    if constexpr (MODE != 2) {
+        amax = wave_max(amax);
+        if (lane == 0) red[wave] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    }
+
+    if constexpr (MODE == 0) {
+        const int E = frexp_exp(amax);
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+            if (e0 >= K) break;
+            f16 h[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) h[i] = (f16)__builtin_ldexpf(v[s][i], -E);
+            f16* dst = xo + (int64_t)m * ldo + e0;
+            if (e0 + 16 <= K && vec_ok) {
+                u32x4* d = reinterpret_cast<u32x4*>(dst);
+                u32x4 a, b;
+                uint32_t w[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    w[i] = (uint32_t)__builtin_bit_cast(uint16_t, h[2 * i]) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, h[2 * i + 1]) << 16);
+                }
+                a = u32x4{w[0], w[1], w[2], w[3]};
+                b = u32x4{w[4], w[5], w[6], w[7]};
+                d[0] = a;
+                d[1] = b;
+            } else {
+                for (int i = 0; i < 16; ++i)
+                    if (e0 + i < K) dst[i] = h[i];
+            }
+        }
+        if (tid == 0) eo[m] = E;
+    } else if constexpr (MODE == 1) {
+        float scale = amax / 127.0f;
+        if (!(scale >= 1e-30f)) scale = (scale != scale) ? scale : 1e-30f;
+        float st = round_to<TIn>(scale);
+        if (st == 0.0f) st = dtype_traits<TIn>::tiny();
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+            if (e0 >= K) break;
+            int8_t qq[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float t = __builtin_rintf(round_to<TIn>(v[s][i] / st));
+                t = fminf(fmaxf(t, -128.0f), 127.0f);
+                qq[i] = (int8_t)(int)t;
+            }
+            int8_t* dst = qo + (int64_t)m * ldo + e0;
+            if (e0 + 16 <= K && vec_ok) {
+                uint32_t w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    w[i] = (uint32_t)(uint8_t)qq[4 * i] | ((uint32_t)(uint8_t)qq[4 * i + 1] << 8) |
+                           ((uint32_t)(uint8_t)qq[4 * i + 2] << 16) | ((uint32_t)(uint8_t)qq[4 * i + 3] << 24);
+                *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+            } else {
+                for (int i = 0; i < 16; ++i)
+                    if (e0 + i < K) dst[i] = qq[i];
+            }
+            if (xr) {
+                TIn* xd = xr + (int64_t)m * ldo + e0;
+                for (int i = 0; i < 16; ++i)
+                    if (e0 + i < K) xd[i] = dtype_traits<TIn>::from_f32(v[s][i]);
+            }
+        }
+        if (tid == 0) so[m] = scale;
+    } else {
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+            if (e0 >= K) break;
+            float* dst = fo + (int64_t)m * ldo + e0;
+            for (int i = 0; i < 16; ++i)
+                if (e0 + i < K) dst[i] = v[s][i];
+        }
+    }
+}
+
+template <typename TIn, int MODE>
+static hipError_t launch_prologue(const PrologueArgs& a, hipStream_t st) {
+    const int slots = (a.K + 4095) / 4096;
+    const bool vec_ok = (a.K % 16 == 0) && (a.ldx % 16 == 0) && (a.ldo % 16 == 0) &&
+                        ((uintptr_t)a.x % 64 == 0);
+    bool ok = false;
+    auto go = [&]<int G>() {
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3((unsigned)a.M), dim3(256), 0, st, (const TIn*)a.x, a.ldx, a.K, vec_ok,
+                               a.xo, a.ldo, a.eo, a.qo, a.so, (TIn*)a.xr, a.fo);
+            ok = true;
+        };
+        if (slots <= 1) launch(prologue_kernel<TIn, MODE, G, 1>);
+        else if (slots <= 2) launch(prologue_kernel<TIn, MODE, G, 2>);
+        else if (slots <= 4) launch(prologue_kernel<TIn, MODE, G, 4>);
+        else if (slots <= 8) launch(prologue_kernel<TIn, MODE, G, 8>);
+    };
+    if (!dispatch_group(a.G, go) || !ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t run_prologue(const PrologueArgs& a, hipStream_t st) {
+    if (a.M == 0) return hipSuccess;
+    if (a.K > 32768) return hipErrorInvalidValue;
+    switch (a.mode) {
+        case PROLOGUE_WO:
+            if (a.x_dtype == DT_F16) return launch_prologue<f16, 0>(a, st);
+            if (a.x_dtype == DT_BF16) return launch_prologue<bf16_t, 0>(a, st);
+            if (a.x_dtype == DT_F32) return launch_prologue<float, 0>(a, st);
+            break;
+        case PROLOGUE_A8:
+            if (a.x_dtype == DT_F16) return launch_prologue<f16, 1>(a, st);
+            if (a.x_dtype == DT_BF16) return launch_prologue<bf16_t, 1>(a, st);
+            if (a.x_dtype == DT_F32) return launch_prologue<float, 1>(a, st);
+            break;
+        case PROLOGUE_ROT_F32:
+            if (a.x_dtype == DT_F32) return launch_prologue<float, 2>(a, st);
+            break;
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace qlin

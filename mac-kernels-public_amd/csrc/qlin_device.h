@@ -1,0 +1,157 @@
+// Device-side helpers shared by the qlin kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qlin {
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct bf16_t { uint16_t bits; };
+
+// ---------------------------------------------------------------------------------------------
+// Scalar conversions.  All exact or correctly rounded (round to nearest even).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    // v_cvt_f32_f16 is exact for every fp16 input (denormals are kept: HIP's default fp16 mode).
+    return (float)__builtin_bit_cast(f16, h);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// f32 -> IEEE fp16 bits, round to nearest even, overflow to inf, subnormals kept; computed with
+// integer operations so the result does not depend on the hardware conversion's mode bits.
+__device__ __forceinline__ uint16_t f32_to_f16_bits_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((a >> 13) & 0x3FFu));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (a < 0x38800000u) {  // fp16 subnormal or zero: quantum 2^-24
+        if (a < 0x33000000u) return (uint16_t)sign;
+        const uint32_t e = a >> 23, m = (a & 0x7FFFFFu) | 0x800000u;
+        const uint32_t sh = 126u - e;
+        uint32_t q = m >> sh;
+        const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = (((a >> 23) - 112u) << 10) | ((a & 0x7FFFFFu) >> 13);
+    const uint32_t rem = a & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+}
+
+// float8_e4m3fn -> f32 (bias 7, no infinities, S.1111.111 = NaN).
+__device__ __forceinline__ float e4m3_to_f32(uint8_t v) {
+    uint32_t sign = (uint32_t)(v & 0x80u) << 24;
+    uint32_t e = (v >> 3) & 0xFu, m = v & 7u;
+    if (e == 15u && m == 7u) return __uint_as_float(sign | 0x7FC00000u);
+    if (e == 0u) {
+        float x = (float)m * 0.001953125f;
+        return sign ? -x : x;
+    }
+    return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+template <typename T> struct dtype_traits;
+template <> struct dtype_traits<float> {
+    static __device__ __forceinline__ float to_f32(float v) { return v; }
+    static __device__ __forceinline__ float from_f32(float v) { return v; }
+    static __device__ __forceinline__ float tiny() { return 1.17549435e-38f; }
+};
+template <> struct dtype_traits<f16> {
+    static __device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
+    static __device__ __forceinline__ f16 from_f32(float v) { return (f16)v; }
+    static __device__ __forceinline__ float tiny() { return 6.103515625e-05f; }
+};
+template <> struct dtype_traits<bf16_t> {
+    static __device__ __forceinline__ float to_f32(bf16_t v) { return bf16_bits_to_f32(v.bits); }
+    static __device__ __forceinline__ bf16_t from_f32(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+    static __device__ __forceinline__ float tiny() { return 1.17549435e-38f; }
+};
+
+// Round a float to the storage type T and back (the value an x.dtype tensor would hold).
+template <typename T>
+__device__ __forceinline__ float round_to(float v) { return dtype_traits<T>::to_f32(dtype_traits<T>::from_f32(v)); }
+
+// ---------------------------------------------------------------------------------------------
+// Cross-lane helpers.
+// ---------------------------------------------------------------------------------------------
+// xor-shuffle within groups of 32 lanes through ds_swizzle (bit mode), for masks < 32.
+template <int MASK>
+__device__ __forceinline__ float swz_xor(float v) {
+    static_assert(MASK > 0 && MASK < 32, "ds_swizzle bit mode reaches 32 lanes");
+    constexpr int pattern = 0x1F | (MASK << 10);
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), pattern));
+}
+
+// DPP quad permutation (lane r of each quad reads lane SEL[r]).
+template <int A, int B, int C, int D>
+__device__ __forceinline__ float dpp_quad(float v) {
+    constexpr int ctrl = A | (B << 2) | (C << 4) | (D << 6);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+template <int MASK>
+__device__ __forceinline__ float lane_xor(float v) {
+    if constexpr (MASK == 1) return dpp_quad<1, 0, 3, 2>(v);
+    else if constexpr (MASK == 2) return dpp_quad<2, 3, 0, 1>(v);
+    else if constexpr (MASK == 3) return dpp_quad<3, 2, 1, 0>(v);
+    else if constexpr (MASK < 32) return swz_xor<MASK>(v);
+    else return __shfl_xor(v, MASK, 64);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// Exponent E with |v| = mant * 2^E, mant in [0.5, 1) (frexp); 0 for zero / non-finite.
+__device__ __forceinline__ int frexp_exp(float v) {
+    if (!(v != 0.0f) || !__builtin_isfinite(v)) return 0;
+    return __builtin_amdgcn_frexp_expf(v);
+}
+
+// Unaligned 32-bit read from a 4-byte aligned base: bytes [off, off+4).
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* base, int off) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (off & ~3));
+    const int sh = off & 3;
+    if (sh == 0) return p[0];
+    return __builtin_amdgcn_alignbyte(p[1], p[0], sh);  // shift is in bytes
+}
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* base, int off) {
+    return (uint16_t)(ld_u32(base, off) & 0xFFFFu);
+}
+
+// Output stores for the supported output dtypes.
+__device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_out(f16* p, float v) { *p = (f16)v; }
+__device__ __forceinline__ void store_out(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); }
+
+__device__ __forceinline__ float load_f(const float* p) { return *p; }
+__device__ __forceinline__ float load_f(const f16* p) { return (float)*p; }
+__device__ __forceinline__ float load_f(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
+
+}  // namespace qlin

@@ -1,0 +1,109 @@
+// Internal launcher interfaces between the kernel translation units and the C ABI (capi.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qlin_device.h"
+
+namespace qlin {
+
+enum { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I8 = 3, DT_U8 = 4, DT_I32 = 5, DT_E4M3 = 6, DT_NONE = -1 };
+enum { PROLOGUE_WO = 0, PROLOGUE_A8 = 1, PROLOGUE_ROT_F32 = 2 };
+
+// ---- activation prologue (prologue.hip) ----
+struct PrologueArgs {
+    int mode = PROLOGUE_WO;
+    int x_dtype = DT_F16;
+    const void* x = nullptr;
+    int64_t ldx = 0;
+    int64_t M = 0;
+    int K = 0;
+    int G = 0;                 // rotation group, 0 = none
+    f16* xo = nullptr;         // WO: normalized fp16 rows
+    int64_t ldo = 0;           // row stride of every output (elements)
+    int32_t* eo = nullptr;     // WO: row exponents
+    int8_t* qo = nullptr;      // A8: int8 rows
+    float* so = nullptr;       // A8: fp32 scales
+    void* xr = nullptr;        // A8: optional rotated copy in x's dtype
+    float* fo = nullptr;       // ROT_F32: rotated fp32 rows
+};
+hipError_t run_prologue(const PrologueArgs& a, hipStream_t st);
+
+// ---- GGUF small-M linear (gguf_smallm.hip) ----
+struct GgufSmallMArgs {
+    int type = 0;
+    const f16* x = nullptr;
+    int64_t ldx = 0;
+    int M = 0;
+    const int32_t* xexp = nullptr;  // per-row exponent to restore (nullptr = 0)
+    const uint8_t* w = nullptr;
+    int64_t row_bytes = 0;
+    int N = 0, K = 0;
+    const void* bias = nullptr;
+    int bias_dtype = DT_NONE;
+    void* y = nullptr;
+    int y_dtype = DT_F16;
+    int64_t ldy = 0;
+};
+bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes);
+hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st);
+
+// ---- weight-only fp16 MFMA tile GEMM (gemm_f16.hip) ----
+enum { WO_INT8 = 0, WO_GGUF = 1 };
+struct GemmF16Args {
+    int wkind = WO_INT8;
+    int gguf_type = 0;
+    const f16* x = nullptr;          // normalized fp16 activations [M, K]
+    int64_t ldx = 0;
+    const int32_t* xexp = nullptr;   // per-row exponents of x (nullptr = 0)
+    int64_t M = 0, N = 0, K = 0;
+    const void* w = nullptr;         // int8 [N, K] (ldw elements) or GGUF bytes
+    int64_t ldw = 0;
+    const void* scale = nullptr;     // INT8: per-row scale (f32 or f16), scale_stride 0 = scalar
+    int scale_dtype = DT_F32;
+    int64_t scale_stride = 1;
+    const int32_t* wexp = nullptr;   // GGUF: per-row weight exponent
+    const void* bias = nullptr;
+    int bias_dtype = DT_NONE;
+    void* y = nullptr;
+    int y_dtype = DT_F16;
+    int64_t ldy = 0;
+};
+hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st);
+
+// GGUF per-row weight exponent: e[n] = exponent bounding max |w[n, :]| (gemm_f16.hip).
+hipError_t run_gguf_row_exp(int type, const uint8_t* w, int64_t N, int64_t K, int32_t* e, hipStream_t st);
+
+// ---- A8 int8 MFMA tile GEMM for AsymW4A8Int8 weights (gemm_i8.hip) ----
+struct GemmI8Args {
+    const int8_t* xq = nullptr;      // int8 activations [M, K]
+    int64_t ldx = 0;
+    const float* sx = nullptr;       // per-row activation scale
+    int64_t M = 0, N = 0, K = 0;
+    const uint8_t* q = nullptr;      // packed codes [N, K*bits/8]
+    int64_t ldq = 0;                 // bytes per row
+    int bits = 4;
+    int group_size = 16;
+    const void* s_rel = nullptr;     // [N, K/gs]
+    int s_rel_dtype = DT_E4M3;
+    int64_t ld_srel = 0;
+    const float* s_ch = nullptr;     // [N]
+    const float* codebook = nullptr; // [16] or nullptr
+    const void* bias = nullptr;
+    int bias_dtype = DT_NONE;
+    void* y = nullptr;
+    int y_dtype = DT_F16;
+    int64_t ldy = 0;
+};
+hipError_t run_gemm_i8(const GemmI8Args& a, hipStream_t st);
+
+// ---- standalone decodes (dequant.hip) ----
+hipError_t run_dequant_gguf(int type, const uint8_t* w, int64_t total, void* out, int out_dtype, hipStream_t st);
+hipError_t run_dequant_int8(const int8_t* q, int64_t N, int64_t K, int64_t ldq, const void* scale, int scale_dtype,
+                            int64_t scale_stride, float* out, hipStream_t st);
+hipError_t run_dequant_w4a8(const uint8_t* q, int64_t N, int64_t K, int64_t ldq, int bits, int gs, const void* s_rel,
+                            int s_rel_dtype, int64_t ld_srel, const float* s_ch, const float* codebook, void* out,
+                            int out_dtype, hipStream_t st);
+
+}  // namespace qlin

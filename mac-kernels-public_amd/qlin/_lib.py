@@ -1,0 +1,111 @@
+"""ctypes binding of libqlin.so (include/qlin.h).
+
+The library is built in-tree by ``mac-kernels-public_amd/build_lib.py``.  Loading fails loudly
+when it is missing: there is no CPU or eager fallback in this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from .exceptions import NoCapableBackendError, QlinError
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqlin.so")
+
+QLIN_OK, QLIN_EUNSUPPORTED, QLIN_EINVAL, QLIN_EHIP, QLIN_EWORKSPACE = 0, 1, 2, 3, 4
+DT_F32, DT_F16, DT_BF16, DT_I8, DT_U8, DT_I32, DT_E4M3 = 0, 1, 2, 3, 4, 5, 6
+OP_INT8_LINEAR, OP_W4A8_LINEAR, OP_GGUF_LINEAR = 0, 1, 2
+
+_TORCH_DT = {
+    torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.int8: DT_I8,
+    torch.uint8: DT_U8, torch.int32: DT_I32, torch.float8_e4m3fn: DT_E4M3,
+}
+
+# Every symbol include/qlin.h declares.
+EXPORTS = (
+    "qlin_version", "qlin_status_string", "qlin_last_error", "qlin_workspace_size", "qlin_query",
+    "qlin_int8_linear", "qlin_w4a8_linear", "qlin_gguf_linear", "qlin_dequantize_gguf",
+    "qlin_dequantize_int8", "qlin_dequantize_w4a8", "qlin_quantize_act_int8",
+)
+
+
+class QlinTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 4),
+        ("stride", ctypes.c_int64 * 4),
+    ]
+
+
+_lib = None
+
+
+def load():
+    """Load libqlin.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise QlinError(f"{LIB_PATH} is missing: build it with mac-kernels-public_amd/build_lib.py "
+                        "(the HIP library is the only implementation; there is no fallback)")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, I64, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    T = ctypes.POINTER(QlinTensor)
+    sigs = {
+        "qlin_version": (I, []),
+        "qlin_status_string": (ctypes.c_char_p, [I]),
+        "qlin_last_error": (ctypes.c_char_p, []),
+        "qlin_workspace_size": (SZ, [I, I64, I64, I64, I, I]),
+        "qlin_query": (I, [I, I64, I64, I64, I, I, I]),
+        "qlin_int8_linear": (I, [T, T, T, T, T, I, P, SZ, P]),
+        "qlin_w4a8_linear": (I, [T, T, T, T, T, T, T, I, I, I, P, SZ, P]),
+        "qlin_gguf_linear": (I, [T, P, I, I64, I64, T, T, P, SZ, P]),
+        "qlin_dequantize_gguf": (I, [P, I, I64, I64, T, P]),
+        "qlin_dequantize_int8": (I, [T, T, T, I, P]),
+        "qlin_dequantize_w4a8": (I, [T, T, T, T, T, I, I, I, P]),
+        "qlin_quantize_act_int8": (I, [T, T, T, I, T, P]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def desc(t: torch.Tensor | None, dtype_override: int | None = None):
+    """qlin_tensor descriptor of a torch tensor (None -> NULL pointer)."""
+    if t is None:
+        return None
+    if t.dim() > 4:
+        raise ValueError("at most 4 dims")
+    d = QlinTensor()
+    d.data = t.data_ptr()
+    d.dtype = dtype_override if dtype_override is not None else _TORCH_DT[t.dtype]
+    d.ndim = max(t.dim(), 1)
+    if t.dim() == 0:
+        d.shape[0], d.stride[0] = 1, 1
+    for i in range(t.dim()):
+        d.shape[i] = t.shape[i]
+        d.stride[i] = t.stride(i)
+    return ctypes.byref(d)
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def check(status: int, op: str):
+    if status == QLIN_OK:
+        return
+    msg = load().qlin_last_error().decode(errors="replace")
+    if status == QLIN_EUNSUPPORTED:
+        raise NoCapableBackendError(op, {"hip": msg})
+    if status in (QLIN_EINVAL, QLIN_EWORKSPACE):
+        raise ValueError(f"{op}: {msg}")
+    raise QlinError(f"{op}: {msg}")

@@ -1,0 +1,290 @@
+"""Packed-weight linear ops on MI355X, with comfy-kitchen's names, argument order and defaults.
+
+Reference interface (roblennon/mac-kernels-public; the implementations live in un-vendored
+comfy-kitchen forks, the call sites below pin the API):
+  int8_linear       bench/bench_ck01_int8.py:57, bench/bench_lora_sidepath_kernel.py:77
+  w4a8_int8_linear  bench/bench_w4a8_linear.py:82-83, bench/bench_lora_fused_rank.py:42-44
+  gguf_linear       docs/research/2026-10-03-gguf-on-metal.md:85, bench/bench_gguf_linear.py:120
+  dequantize_*      bench/bench_ck01_int8.py:49, tests/test_training_packed.py:25-26
+
+Every op runs on the HIP library through the C ABI on the current torch stream and returns a new
+tensor.  Inputs are read-only and packed weights are never copied.  A call the kernels do not
+implement raises NoCapableBackendError (the reference registry's decline), never a silent
+approximation.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _lib
+from .exceptions import NoCapableBackendError
+from .gguf import GGUF_TYPES, gguf_type_id
+
+_FLOAT = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _disabled(op):
+    if os.environ.get("QLIN_DISABLE", "0") not in ("", "0"):
+        raise NoCapableBackendError(op, {"hip": "disabled by QLIN_DISABLE"})
+
+
+def _decline_lora(op, lora_down, lora_up, lora_scale):
+    if lora_down is not None or lora_up is not None or lora_scale is not None:
+        raise NoCapableBackendError(op, {"hip": "lora_* side path is not implemented"})
+
+
+def _check_device(op, *tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise NoCapableBackendError(op, {"hip": f"tensor on {t.device}, the kernels need a ROCm device"})
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{op}: tensors on different devices ({dev}, {t.device})")
+    return dev
+
+
+def _as_2d(x: torch.Tensor, k: int):
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} input features, the weight has {k}")
+    lead = tuple(x.shape[:-1])
+    x2 = x.reshape(-1, k)
+    if x2.shape[0] > 1 and x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    if x2.shape[0] > 1 and x2.stride(0) < k:
+        x2 = x2.contiguous()
+    if x2.data_ptr() % 16:  # storage offset that breaks 128-bit loads: take an aligned copy
+        x2 = x2.clone(memory_format=torch.contiguous_format)
+    return x2, lead
+
+
+def _out(x2, lead, n, out_dtype, x):
+    dt = out_dtype or x.dtype
+    if dt not in _FLOAT:
+        raise NoCapableBackendError("linear", {"hip": f"out_dtype {dt} unsupported"})
+    y = torch.empty((x2.shape[0], n), dtype=dt, device=x.device)
+    return y, lead + (n,)
+
+
+def _workspace(op, m, n, k, param, x2):
+    nbytes = _lib.load().qlin_workspace_size(op, m, n, k, param, _lib._TORCH_DT[x2.dtype])
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x2.device)
+
+
+def _bias(bias, n):
+    if bias is None:
+        return None
+    if bias.numel() != n:
+        raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
+    return bias.reshape(n).contiguous()
+
+
+# ------------------------------------------------------------------------------------------------
+# INT8 (+ ConvRot) weight-only
+# ------------------------------------------------------------------------------------------------
+
+def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, convrot_groupsize=256,
+                lora_down=None, lora_up=None, lora_scale=None):
+    """y = rot(x) @ (qdata * scale)^T + bias.  qdata int8 [N, K] (rotated basis when convrot),
+    scale [N] / [N, 1] / scalar (fp32 or fp16).  fp16 MFMA, fp32 accumulate."""
+    op = "int8_linear"
+    _disabled(op)
+    _decline_lora(op, lora_down, lora_up, lora_scale)
+    _check_device(op, x, qdata, scale, bias)
+    if qdata.dtype != torch.int8 or qdata.dim() != 2:
+        raise NoCapableBackendError(op, {"hip": "qdata must be a 2-D int8 tensor"})
+    if x.dtype not in _FLOAT:
+        raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
+    n, k = qdata.shape
+    x2, lead = _as_2d(x, k)
+    y, shape = _out(x2, lead, n, out_dtype, x)
+    if x2.shape[0] == 0 or n == 0:
+        return y.reshape(shape)
+    g = int(convrot_groupsize) if convrot else 0
+    s = scale.reshape(-1) if scale.numel() in (1, n) else scale
+    b = _bias(bias, n)
+    ws = _workspace(_lib.OP_INT8_LINEAR, x2.shape[0], n, k, g, x2)
+    L = _lib.load()
+    st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(y), g,
+                            ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+    _lib.check(st, op)
+    return y.reshape(shape)
+
+
+def dequantize_int8(qdata, scale):
+    """float32 q * scale[n] (the rotated basis for ConvRot weights), bit-exact."""
+    return dequantize_int8_convrot_weight(qdata, scale, 0)
+
+
+def dequantize_int8_convrot_weight(qdata, scale, convrot_groupsize=256):
+    """Original-basis float32 weight rotate(q * scale) (0 = no rotation)."""
+    op = "dequantize_int8"
+    _check_device(op, qdata, scale)
+    n, k = qdata.shape
+    out = torch.empty((n, k), dtype=torch.float32, device=qdata.device)
+    s = scale.reshape(-1) if scale.numel() in (1, n) else scale
+    st = _lib.load().qlin_dequantize_int8(_lib.desc(qdata), _lib.desc(s), _lib.desc(out), int(convrot_groupsize),
+                                          _lib.stream_of(qdata.device))
+    _lib.check(st, op)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# W4A8 / W6A8 (AsymW4A8Int8 storage), A8 int8 GEMM
+# ------------------------------------------------------------------------------------------------
+
+def _srel_desc(s_rel):
+    if s_rel.dtype == torch.float8_e4m3fn:
+        return _lib.desc(s_rel.view(torch.uint8), _lib.DT_E4M3)
+    if s_rel.dtype in (torch.float16, torch.bfloat16, torch.float32):
+        return _lib.desc(s_rel)
+    raise NoCapableBackendError("w4a8_int8_linear", {"hip": f"s_rel dtype {s_rel.dtype} unsupported"})
+
+
+def _bits_of(qdata, s_rel, group_size):
+    k = s_rel.shape[1] * group_size
+    bits = (qdata.shape[1] * 8) // k
+    if bits not in (4, 6) or qdata.shape[1] * 8 != bits * k:
+        raise ValueError(f"qdata [{qdata.shape[0]}, {qdata.shape[1]}] does not hold 4- or 6-bit codes for K={k}")
+    return bits, k
+
+
+def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None, bias=None, group_size=16,
+                     convrot_groupsize=256, out_dtype=None, *, lora_down=None, lora_up=None, lora_scale=None):
+    """A8 linear: per-token int8 activations (quantize_int8_rowwise of the rotated x), int8 MFMA
+    against the int8 weight grid, y = acc * sx[m] * s_channel[n] + bias."""
+    op = "w4a8_int8_linear"
+    _disabled(op)
+    _decline_lora(op, lora_down, lora_up, lora_scale)
+    if correction is not None:
+        raise NoCapableBackendError(op, {"hip": "the asymmetric `correction` variant is not implemented"})
+    _check_device(op, x, qdata, s_rel, s_channel, codebook, bias)
+    if x.dtype not in _FLOAT:
+        raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
+    bits, k = _bits_of(qdata, s_rel, group_size)
+    n = qdata.shape[0]
+    x2, lead = _as_2d(x, k)
+    y, shape = _out(x2, lead, n, out_dtype, x)
+    if x2.shape[0] == 0 or n == 0:
+        return y.reshape(shape)
+    q = qdata if qdata.dtype in (torch.int8, torch.uint8) else qdata.view(torch.int8)
+    cb = None if codebook is None else codebook.to(torch.float32).contiguous()
+    sch = s_channel.reshape(-1).to(torch.float32).contiguous()
+    b = _bias(bias, n)
+    ws = _workspace(_lib.OP_W4A8_LINEAR, x2.shape[0], n, k, bits, x2)
+    L = _lib.load()
+    st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
+                            _lib.desc(b), _lib.desc(y), bits, int(group_size), int(convrot_groupsize or 0),
+                            ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+    _lib.check(st, op)
+    return y.reshape(shape)
+
+
+def dequantize_w4a8_int8_weight(qdata, s_rel, s_channel, codebook=None, correction=None, group_size=16,
+                                convrot_groupsize=256, output_dtype=torch.float32):
+    """Packed storage -> weight in the original basis (rotated back per ConvRot group)."""
+    op = "dequantize_w4a8_int8_weight"
+    if correction is not None:
+        raise NoCapableBackendError(op, {"hip": "the asymmetric `correction` variant is not implemented"})
+    _check_device(op, qdata, s_rel, s_channel, codebook)
+    bits, k = _bits_of(qdata, s_rel, group_size)
+    n = qdata.shape[0]
+    out = torch.empty((n, k), dtype=torch.float32, device=qdata.device)
+    cb = None if codebook is None else codebook.to(torch.float32).contiguous()
+    sch = s_channel.reshape(-1).to(torch.float32).contiguous()
+    st = _lib.load().qlin_dequantize_w4a8(_lib.desc(qdata), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
+                                          _lib.desc(out), bits, int(group_size), int(convrot_groupsize or 0),
+                                          _lib.stream_of(qdata.device))
+    _lib.check(st, op)
+    return out if output_dtype == torch.float32 else out.to(output_dtype)
+
+
+def w4a8_int8_grid(qdata, s_rel, codebook=None, group_size=16):
+    """The int8 weight grid w8 [N, K] the A8 GEMM multiplies (bit-exact decode)."""
+    op = "w4a8_int8_grid"
+    _check_device(op, qdata, s_rel, codebook)
+    bits, k = _bits_of(qdata, s_rel, group_size)
+    n = qdata.shape[0]
+    out = torch.empty((n, k), dtype=torch.int8, device=qdata.device)
+    cb = None if codebook is None else codebook.to(torch.float32).contiguous()
+    ones = torch.ones(n, dtype=torch.float32, device=qdata.device)
+    st = _lib.load().qlin_dequantize_w4a8(_lib.desc(qdata), _srel_desc(s_rel), _lib.desc(ones), _lib.desc(cb),
+                                          _lib.desc(out), bits, int(group_size), 0, _lib.stream_of(qdata.device))
+    _lib.check(st, op)
+    return out
+
+
+def quantize_int8_rowwise(x, convrot_groupsize=0, return_rotated=False):
+    """Per-token A8 quantization on the GPU: (q int8 [M, K], scale fp32 [M, 1]) of rot(x),
+    with the reference's arithmetic in x's dtype."""
+    op = "quantize_int8_rowwise"
+    _check_device(op, x)
+    k = x.shape[-1]
+    x2, lead = _as_2d(x, k)
+    m = x2.shape[0]
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    xr = torch.empty((m, k), dtype=x.dtype, device=x.device) if return_rotated else None
+    if m:
+        st = _lib.load().qlin_quantize_act_int8(_lib.desc(x2), _lib.desc(q), _lib.desc(s), int(convrot_groupsize),
+                                                _lib.desc(xr), _lib.stream_of(x.device))
+        _lib.check(st, op)
+    q = q.reshape(lead + (k,))
+    s = s.reshape(lead + (1,))
+    if return_rotated:
+        return q, s, xr.reshape(lead + (k,))
+    return q, s
+
+
+# ------------------------------------------------------------------------------------------------
+# GGUF
+# ------------------------------------------------------------------------------------------------
+
+def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=None, lora_up=None, lora_scale=None):
+    """y = x @ W^T + bias with W [N, K] decoded from GGUF blocks of `qtype` (ggml type id or name).
+    `weight` is the tensor's raw bytes (uint8, [N, K/qk*ts] or flat)."""
+    op = "gguf_linear"
+    _disabled(op)
+    _decline_lora(op, lora_down, lora_up, lora_scale)
+    _check_device(op, x, weight, bias)
+    tid = gguf_type_id(qtype)
+    n, k = int(shape[0]), int(shape[1])
+    if weight.dtype != torch.uint8:
+        raise NoCapableBackendError(op, {"hip": "weight must be the uint8 block bytes"})
+    if not weight.is_contiguous():
+        raise NoCapableBackendError(op, {"hip": "weight bytes must be contiguous"})
+    _, qk, ts = GGUF_TYPES_BY_ID[tid]
+    if weight.numel() != n * k // qk * ts:
+        raise ValueError(f"weight has {weight.numel()} bytes, expected {n * k // qk * ts} for {shape}")
+    if x.dtype not in _FLOAT:
+        raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
+    x2, lead = _as_2d(x, k)
+    y, oshape = _out(x2, lead, n, out_dtype, x)
+    if x2.shape[0] == 0 or n == 0:
+        return y.reshape(oshape)
+    b = _bias(bias, n)
+    ws = _workspace(_lib.OP_GGUF_LINEAR, x2.shape[0], n, k, tid, x2)
+    st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(y),
+                                      ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+    _lib.check(st, op)
+    return y.reshape(oshape)
+
+
+def dequantize_gguf(weight, qtype, shape, out_dtype=torch.float32):
+    """Decode GGUF block bytes to a dense [N, K] tensor; float32 is bit-exact with gguf-py."""
+    op = "dequantize_gguf"
+    _check_device(op, weight)
+    tid = gguf_type_id(qtype)
+    n, k = int(shape[0]), int(shape[1])
+    out = torch.empty((n, k), dtype=out_dtype, device=weight.device)
+    st = _lib.load().qlin_dequantize_gguf(weight.data_ptr(), tid, n, k, _lib.desc(out), _lib.stream_of(weight.device))
+    _lib.check(st, op)
+    return out
+
+
+GGUF_TYPES_BY_ID = {v[0]: (name, v[1], v[2]) for name, v in GGUF_TYPES.items()}

@@ -1,0 +1,152 @@
+"""The C ABI library without a GPU: it loads, exports every symbol include/qlin.h declares, and
+rejects malformed or unsupported calls before launching anything."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "qlin.h")).read()
+    return sorted(set(re.findall(r"\b(qlin_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from qlin import _lib
+    L = _lib.load()
+    syms = header_symbols()
+    assert len(syms) >= 12
+    for s in syms:
+        assert hasattr(L, s), s
+    assert set(syms) == set(_lib.EXPORTS)
+    assert L.qlin_version() == 1
+    assert L.qlin_status_string(1) == b"unsupported"
+
+
+def test_query_and_workspace():
+    from qlin import _lib
+    L = _lib.load()
+    assert L.qlin_query(_lib.OP_GGUF_LINEAR, 1, 4096, 4096, 12, _lib.DT_F16, _lib.DT_F16) == 0
+    assert L.qlin_query(_lib.OP_GGUF_LINEAR, 1, 4096, 4096, 99, _lib.DT_F16, _lib.DT_F16) == 1
+    assert L.qlin_query(_lib.OP_GGUF_LINEAR, 1, 4096, 4000, 12, _lib.DT_F16, _lib.DT_F16) == 1
+    assert L.qlin_query(_lib.OP_INT8_LINEAR, 8, 64, 768, 256, _lib.DT_F16, _lib.DT_F16) == 0
+    assert L.qlin_query(_lib.OP_INT8_LINEAR, 8, 64, 768, 100, _lib.DT_F16, _lib.DT_F16) == 1
+    assert L.qlin_query(_lib.OP_W4A8_LINEAR, 8, 64, 3072, 4, _lib.DT_F16, _lib.DT_BF16) == 0
+    assert L.qlin_query(_lib.OP_W4A8_LINEAR, 8, 64, 3072, 5, _lib.DT_F16, _lib.DT_F16) == 1
+    assert b"bits" in L.qlin_last_error()
+    ws = L.qlin_workspace_size(_lib.OP_INT8_LINEAR, 256, 3072, 3072, 128, _lib.DT_F16)
+    assert ws >= 256 * 3072 * 2 + 256 * 4
+
+
+def _d(t, dt=None):
+    from qlin import _lib
+    return _lib.desc(t, dt)
+
+
+def test_malformed_calls_are_rejected_before_launch():
+    from qlin import _lib
+    L = _lib.load()
+    x = torch.zeros(4, 256, dtype=torch.float16)
+    y = torch.zeros(4, 32, dtype=torch.float16)
+    # unknown ggml type -> unsupported
+    assert L.qlin_gguf_linear(_d(x), 1, 99, 32, 256, None, _d(y), None, 0, None) == _lib.QLIN_EUNSUPPORTED
+    # K not a whole number of blocks -> unsupported (rows would straddle blocks)
+    assert L.qlin_gguf_linear(_d(x), 1, 12, 32, 250, None, _d(y), None, 0, None) == _lib.QLIN_EUNSUPPORTED
+    # y with the wrong shape -> invalid
+    yb = torch.zeros(4, 31, dtype=torch.float16)
+    assert L.qlin_gguf_linear(_d(x), 1, 8, 32, 256, None, _d(yb), None, 0, None) == _lib.QLIN_EINVAL
+    # workspace too small
+    assert L.qlin_gguf_linear(_d(x), 1, 8, 32, 256, None, _d(y), None, 0, None) == _lib.QLIN_EWORKSPACE
+    # INT8: bad ConvRot group, non-int8 weight, missing x
+    q = torch.zeros(32, 256, dtype=torch.int8)
+    s = torch.ones(32)
+    assert L.qlin_int8_linear(_d(x), _d(q), _d(s), None, _d(y), 100, None, 0, None) == _lib.QLIN_EUNSUPPORTED
+    assert L.qlin_int8_linear(_d(x), _d(q.float()), _d(s), None, _d(y), 0, None, 0, None) == _lib.QLIN_EUNSUPPORTED
+    assert L.qlin_int8_linear(None, _d(q), _d(s), None, _d(y), 0, None, 0, None) == _lib.QLIN_EINVAL
+    # scale with the wrong length
+    assert L.qlin_int8_linear(_d(x), _d(q), _d(torch.ones(7)), None, _d(y), 0, None, 0, None) == _lib.QLIN_EINVAL
+    # W4A8: 5 bits, codebook with 6 bits
+    qq = torch.zeros(32, 128, dtype=torch.int8)
+    sr = torch.ones(32, 16)
+    assert L.qlin_w4a8_linear(_d(x), _d(qq), _d(sr), _d(s), None, None, _d(y), 5, 16, 256, None, 0, None) == 1
+    q6 = torch.zeros(32, 192, dtype=torch.int8)
+    cb = torch.zeros(16)
+    assert L.qlin_w4a8_linear(_d(x), _d(q6), _d(sr), _d(s), _d(cb), None, _d(y), 6, 16, 256, None, 0, None) == 1
+    assert b"codebook" in L.qlin_last_error()
+
+
+def test_ops_decline_cpu_tensors():
+    import qlin
+    x = torch.zeros(2, 256, dtype=torch.float16)
+    with pytest.raises(qlin.NoCapableBackendError):
+        qlin.int8_linear(x, torch.zeros(8, 256, dtype=torch.int8), torch.ones(8))
+
+
+def test_registry():
+    import qlin
+    from qlin.exceptions import NoCapableBackendError
+    fn = qlin.registry.get_implementation("int8_linear")
+    assert fn is qlin.int8_linear
+    with pytest.raises(NoCapableBackendError) as e:
+        qlin.registry.get_implementation("int8_linear", kwargs={"lora_down": object()})
+    assert "hip" in e.value.reasons
+    with pytest.raises(NoCapableBackendError):
+        qlin.registry.get_implementation("scaled_mm_nvfp4")
+    os.environ["QLIN_DISABLE"] = "1"
+    try:
+        with pytest.raises(NoCapableBackendError):
+            qlin.registry.get_implementation("gguf_linear")
+        assert "gguf_linear" in qlin.registry.capabilities()
+    finally:
+        del os.environ["QLIN_DISABLE"]
+
+
+@pytest.mark.parametrize("g", [4, 8, 16, 32, 64, 128, 256])
+def test_hadamard_invariants(g):
+    import oracle as O
+    from qlin.quantize import hadamard_signs
+    h = O.hadamard(g)
+    assert np.allclose(h, h.T)
+    assert np.allclose(h @ h, np.eye(g), atol=1e-12)
+    assert np.allclose(np.abs(h), 1 / np.sqrt(g))
+    assert np.array_equal(hadamard_signs(g), np.sign(h))
+    if g in (4, 16, 64, 256):  # the reference's construction: kron powers of H4, normalized
+        h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+        r = h4
+        while r.shape[0] < g:
+            r = np.kron(r, h4)
+        assert np.array_equal(np.sign(h), r)
+    x = np.random.default_rng(0).standard_normal((3, 4 * g)).astype(np.float32)
+    rx = O.rotate(x, g)
+    assert np.allclose(rx, (x.astype(np.float64).reshape(3, 4, g) @ h.T).reshape(3, 4 * g), atol=1e-6)
+    assert np.allclose(O.rotate(rx, g), x, atol=1e-5)
+
+
+@pytest.mark.parametrize("name", ["Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K",
+                                  "IQ4_NL", "IQ4_XS"])
+def test_gguf_quantizer_round_trip(name):
+    """The packer and the oracle's decoder agree on every field's position: the decode of the
+    packed gaussian reproduces it to the format's precision (a swapped nibble, a misplaced scale
+    or a wrong high-bit index blows the error up to O(1))."""
+    import oracle as O
+    from qlin.quantize import quantize_gguf
+    bound = {"Q4_0": .1, "Q4_1": .1, "Q5_0": .05, "Q5_1": .05, "Q8_0": .007, "Q2_K": .4, "Q3_K": .2, "Q4_K": .1,
+             "Q5_K": .05, "Q6_K": .025, "IQ4_NL": .1, "IQ4_XS": .1}[name]
+    w = (np.random.default_rng(1).standard_normal((32, 512)) * 0.02).astype(np.float32)
+    raw = quantize_gguf(w, name)
+    assert raw.shape == (32, 512 // O.GGUF_TYPES[name][1] * O.GGUF_TYPES[name][2])
+    assert O.rel_fro(O.gguf_dequantize(raw, name, w.shape), w) < bound
+
+
+def test_int8_convrot_quantizer_matches_oracle():
+    import oracle as O
+    from qlin.quantize import quantize_int8_convrot_weight
+    w = (np.random.default_rng(2).standard_normal((64, 512)) * 0.02).astype(np.float32)
+    q, s = quantize_int8_convrot_weight(w, 256)
+    oq, os_ = O.quantize_int8_rowwise(O.rotate(w, 256))
+    assert np.array_equal(q, oq) and np.array_equal(s, os_.reshape(-1))

@@ -1,0 +1,365 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on the same seeded inputs.
+
+Bars: decoded weights and int8 activation quantization bit-exact; linear outputs within 1e-3
+relative Frobenius error and 2e-2 max-abs error of a float64 matmul over the same dequantized
+operands (the A8 path also bit-exact against an exact replay of its integer GEMM + epilogue).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REL_TOL, ABS_TOL = 1e-3, 2e-2
+GGUF = ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS")
+DEV = "cuda:0"
+
+
+def qlin():
+    import qlin as Q
+    return Q
+
+
+def qz():
+    from qlin import quantize as QZ
+    return QZ
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def check_linear(got, want, what=""):
+    got = got.float().cpu().numpy().astype(np.float64)
+    rel = O.rel_fro(got, want)
+    mx = float(np.abs(got - want).max()) if want.size else 0.0
+    assert np.isfinite(got).all(), what
+    assert rel < REL_TOL and mx < ABS_TOL, f"{what}: rel_fro={rel:.3e} max_abs={mx:.3e}"
+    return rel, mx
+
+
+def x_fp16(m, k, seed=1, outliers=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g)
+    if outliers:
+        mask = torch.rand(m, k, generator=g) < 0.01
+        x = torch.where(mask, 20.0 * torch.sign(x), x)
+    return x.half()
+
+
+# ------------------------------------------------------------------------------------------------
+# GGUF decode
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", GGUF)
+def test_dequantize_gguf_bit_exact(name):
+    n, k = 40, 1024
+    for seed, raw in ((0, qz().random_gguf_blocks(name, n, k, seed=3)),
+                      (1, qz().quantize_gguf(np.random.default_rng(4).standard_normal((n, k)).astype(np.float32) * 0.02, name))):
+        want = O.gguf_dequantize(raw, name, (n, k))
+        w = torch.from_numpy(np.ascontiguousarray(raw)).to(DEV)
+        got = qlin().dequantize_gguf(w, name, (n, k)).cpu().numpy()
+        assert got.view(np.uint32).tobytes() == want.view(np.uint32).tobytes(), f"{name} seed {seed}"
+        got16 = qlin().dequantize_gguf(w, name, (n, k), out_dtype=torch.float16).cpu().numpy().view(np.uint16)
+        want16 = want.astype(np.float16).view(np.uint16)
+        bad = np.flatnonzero(got16 != want16)
+        assert bad.size == 0, (f"{name}: {bad.size} fp16 mismatches; first: f32 {want.reshape(-1)[bad[:4]]!r} "
+                               f"got {got16.reshape(-1)[bad[:4]]} want {want16.reshape(-1)[bad[:4]]}")
+
+
+@pytest.mark.parametrize("case", ["gauss_96x1024", "heavy_96x1024"])
+@pytest.mark.parametrize("fmt,name", [("gguf_q8_0", "Q8_0"), ("gguf_q4_k", "Q4_K")])
+def test_dequantize_gguf_golden(case, fmt, name):
+    raw = np.load(os.path.join(HERE, "golden", "selftest_raw.npz"))[f"{case}/{fmt}/q"]
+    meta = json.load(open(os.path.join(HERE, "golden", "selftest_sha256.json")))
+    got = qlin().dequantize_gguf(torch.from_numpy(raw.copy()).to(DEV), name, (96, 1024)).cpu().numpy()
+    assert sha(got) == meta["cases"][case]["formats"][fmt]["deq"]
+
+
+@pytest.mark.parametrize("name", ["Q8_0", "Q4_K", "Q6_K", "Q4_0", "IQ4_XS"])
+def test_dequantize_gguf_special_scales(name):
+    """fp16 scale fields of 0, +-65504 and subnormals decode exactly."""
+    _, qk, ts = O.GGUF_TYPES[name]
+    raw = qz().random_gguf_blocks(name, 8, 512, seed=9).reshape(-1, ts)
+    specials = np.array([0.0, 65504.0, -65504.0, 6e-8, -3e-6, 2 ** -24, 1.0, -0.0], dtype=np.float16).view(np.uint8)
+    offs = {"Q8_0": [0], "Q4_K": [0, 2], "Q6_K": [208], "Q4_0": [0], "IQ4_XS": [0]}[name]
+    for i in range(raw.shape[0]):
+        for off in offs:
+            raw[i, off:off + 2] = specials[2 * (i % 8): 2 * (i % 8) + 2]
+    want = O.gguf_dequantize(raw, name)
+    got = qlin().dequantize_gguf(torch.from_numpy(raw.reshape(8, -1).copy()).to(DEV), name, (8, 512)).cpu().numpy()
+    assert got.reshape(-1).view(np.uint32).tobytes() == want.view(np.uint32).tobytes()
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q8_0", "Q6_K"])
+def test_dequantize_gguf_straddling_rows(name):
+    """Rows that start mid-block (flat indexing, gguf-on-metal.md:38): N*K is a whole number of
+    blocks but K is not."""
+    _, qk, ts = O.GGUF_TYPES[name]
+    n, k = 32, qk * 3 // 2 if qk == 256 else 48
+    raw = qz().random_gguf_blocks(name, 1, n * k, seed=2).reshape(-1)
+    want = O.gguf_dequantize(raw, name).reshape(n, k)
+    got = qlin().dequantize_gguf(torch.from_numpy(raw.copy()).to(DEV), name, (n, k)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------------------------------------
+# GGUF linear
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", GGUF)
+@pytest.mark.parametrize("m", [1, 8, 64, 100])
+def test_gguf_linear(name, m):
+    n, k = 80, 1024
+    raw = qz().random_gguf_blocks(name, n, k, seed=11)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = x_fp16(m, k, seed=m)
+    want = O.linear_ref(x.float().numpy(), w)
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k))
+    assert got.dtype == torch.float16 and got.shape == (m, n)
+    check_linear(got, want, f"{name} M={m}")
+
+
+@pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                     (torch.float32, torch.float32), (torch.float16, torch.float32)])
+@pytest.mark.parametrize("m", [3, 200])
+def test_gguf_linear_dtypes_and_bias(xdt, odt, m):
+    name, n, k = "Q4_K", 96, 512
+    raw = qz().random_gguf_blocks(name, n, k, seed=5)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(3)).to(xdt)
+    b = torch.randn(n, generator=torch.Generator().manual_seed(4)) * 0.1
+    want = O.linear_ref(x.float().numpy(), w, b.numpy())
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), 12, (n, k), bias=b.to(DEV), out_dtype=odt)
+    assert got.dtype == odt
+    if odt == torch.bfloat16:
+        # bf16 output rounding alone is ~1.1e-3 rel RMS: compare with the reference rounded to bf16
+        want_b = torch.from_numpy(want).to(torch.bfloat16).double().numpy()
+        assert O.rel_fro(got.double().cpu().numpy(), want_b) < 1e-3
+        assert O.rel_fro(got.double().cpu().numpy(), want) < 4e-3
+    else:
+        check_linear(got, want, f"x {xdt} out {odt}")
+
+
+def test_gguf_linear_large_activations_near_max_scales():
+    """|x| ~ 3e4 against near-max fp16 block scales: fp32 accumulation, no overflow."""
+    name, n, k = "Q8_0", 32, 256
+    raw = qz().random_gguf_blocks(name, n, k, seed=6).reshape(-1, 34)
+    raw[:, :2] = np.array([60000.0], dtype=np.float16).view(np.uint8)
+    raw = raw.reshape(n, -1)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = (torch.randn(2, k, generator=torch.Generator().manual_seed(1)) * 1e4).clamp(-6e4, 6e4).half()
+    x[:, :4] = 3e4
+    want = O.linear_ref(x.float().numpy(), w)
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), out_dtype=torch.float32)
+    rel = O.rel_fro(got.cpu().numpy(), want)
+    assert np.isfinite(got.cpu().numpy()).all() and rel < REL_TOL
+
+
+def test_gguf_linear_shapes_and_empty():
+    Q = qlin()
+    name, n, k = "Q4_0", 48, 256
+    raw = torch.from_numpy(qz().random_gguf_blocks(name, n, k, seed=1)).to(DEV)
+    x = torch.randn(2, 3, k, device=DEV).half()
+    y = Q.gguf_linear(x, raw, name, (n, k))
+    assert y.shape == (2, 3, n)
+    y1 = Q.gguf_linear(x[0, 0], raw, name, (n, k))
+    assert y1.shape == (n,)
+    torch.testing.assert_close(y1, y[0, 0], rtol=0, atol=0)
+    e = Q.gguf_linear(torch.empty(0, k, device=DEV).half(), raw, name, (n, k))
+    assert e.shape == (0, n)
+    xs = torch.randn(5, k + 8, device=DEV).half()[:, 8:]  # strided rows with a storage offset
+    torch.testing.assert_close(Q.gguf_linear(xs, raw, name, (n, k)), Q.gguf_linear(xs.contiguous(), raw, name, (n, k)),
+                               rtol=0, atol=0)
+    with pytest.raises(Q.NoCapableBackendError):
+        Q.gguf_linear(x, raw, name, (n, k), lora_down=torch.zeros(1, k, device=DEV))
+
+
+# ------------------------------------------------------------------------------------------------
+# INT8 ConvRot weight-only
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("g", [0, 128, 256])
+@pytest.mark.parametrize("m", [1, 33, 256])
+def test_int8_linear(g, m):
+    n, k = 192, 1024
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    q, s = qz().quantize_int8_convrot_weight(w, g) if g else qz().quantize_int8_rowwise(w)
+    x = x_fp16(m, k, seed=m)
+    xr = O.rotate(x.float().numpy(), g) if g else x.float().numpy()
+    want = O.linear_ref(xr, O.dequantize_int8(q, s))
+    got = qlin().int8_linear(x.to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV),
+                             convrot=bool(g), convrot_groupsize=g or 256)
+    check_linear(got, want, f"G={g} M={m}")
+    # the original-basis weight gives the same product on the unrotated activation
+    if g:
+        want2 = O.linear_ref(x.float().numpy(), O.dequantize_int8_convrot(q, s, g))
+        assert O.rel_fro(want2, want) < 1e-5
+
+
+def test_int8_linear_scales_bias_bf16():
+    n, k, m = 64, 512, 70
+    rng = np.random.default_rng(8)
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (np.abs(rng.standard_normal(n)) * 1e-3).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(2)).bfloat16()
+    xr = O.rotate(x.float().numpy(), 256)
+    want = O.linear_ref(xr, O.dequantize_int8(q, s), b)
+    got = qlin().int8_linear(x.to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).half().to(DEV),
+                             torch.from_numpy(b).to(DEV), torch.float32, convrot=True)
+    want16 = O.linear_ref(xr, O.dequantize_int8(q, s.astype(np.float16).astype(np.float32)), b)
+    check_linear(got, want16, "fp16 scale + bias")
+    assert O.rel_fro(want16, want) < 1e-3
+
+
+def test_int8_linear_extremes():
+    """Edge cases of bench/probe_small_m.py:84-101: tiny inputs, huge/zero scales, rotation growth."""
+    Q = qlin()
+    h = O.hadamard(256)
+    onehot = np.zeros((4, 256), np.int8)
+    onehot[:, 0] = 1
+    cases = [
+        ("tiny_input", np.full((1, 256), 2.0 ** -26, np.float32), np.ones((4, 256), np.int8), np.ones(4, np.float32), 0),
+        ("large_scale", np.full((1, 256), 0.001 / 256, np.float32), np.ones((4, 256), np.int8),
+         np.array([1e5, 3e7, 1e-30, -1e5], np.float32), 0),
+        ("zero_scale", np.ones((1, 256), np.float32), np.ones((4, 256), np.int8), np.zeros(4, np.float32), 256),
+        ("rotation_growth", (10000 * np.sign(h[:, 0])).reshape(1, -1).astype(np.float32), onehot,
+         np.full(4, 0.001, np.float32), 256),
+    ]
+    for name, x, q, s, g in cases:
+        xt = torch.from_numpy(x).to(DEV)
+        got = Q.int8_linear(xt, torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), None, torch.float32,
+                            convrot=bool(g), convrot_groupsize=g or 256).cpu().numpy()
+        xr = O.rotate(x, g) if g else x
+        want = O.linear_ref(xr, O.dequantize_int8(q, s))
+        den = max(np.abs(want).max(), 1e-30)
+        assert np.isfinite(got).all(), name
+        assert np.abs(got - want).max() / den < 2e-3, f"{name}: {got} vs {want}"
+
+
+def test_dequantize_int8_bit_exact_and_rotation():
+    n, k = 64, 512
+    rng = np.random.default_rng(1)
+    q = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
+    s = (np.abs(rng.standard_normal(n)) * 1e-3).astype(np.float32)
+    qt, st = torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV)
+    got = qlin().dequantize_int8(qt, st).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), O.dequantize_int8(q, s).view(np.uint32))
+    rot = qlin().dequantize_int8_convrot_weight(qt, st, 256).cpu().numpy()
+    assert O.rel_fro(rot, O.dequantize_int8_convrot(q, s, 256)) < 1e-6
+
+
+# ------------------------------------------------------------------------------------------------
+# A8 activation quantization and W4A8 / W6A8
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_quantize_act_int8_bit_exact(dt):
+    m, k = 37, 768
+    x = x_fp16(m, k, seed=5, outliers=True).float()
+    x[3] = 0.0                       # zero row: scale clamps to 1e-30, dtype scale -> tiny
+    x[4] = x[4] * 1e-6               # tiny row
+    x = x.to(dt)
+    q, s = qlin().quantize_int8_rowwise(x.to(DEV))
+    if dt == torch.bfloat16:
+        wq, ws = O.quantize_int8_rowwise(x.view(torch.int16).numpy().view(np.uint16), bf16=True)
+    else:
+        wq, ws = O.quantize_int8_rowwise(x.numpy())
+    assert np.array_equal(q.cpu().numpy(), wq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+
+
+@pytest.mark.parametrize("g", [128, 256])
+def test_quantize_act_rotated(g):
+    """With ConvRot: the rotation is fp32 (within one fp16 ulp of the exact rotation, rarely off),
+    and the int8 quantization of the rotated row is bit-exact."""
+    m, k = 64, 1024
+    x = x_fp16(m, k, seed=6, outliers=True)
+    q, s, xr = qlin().quantize_int8_rowwise(x.to(DEV), g, return_rotated=True)
+    xr = xr.cpu().numpy()
+    exact = O.rotate(x.numpy(), g)
+    diff = np.abs(xr.view(np.uint16).astype(np.int32) - exact.view(np.uint16).astype(np.int32))
+    assert diff.max() <= 1 and (diff > 0).mean() < 1e-2
+    wq, ws = O.quantize_int8_rowwise(xr)
+    assert np.array_equal(q.cpu().numpy(), wq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+
+
+W4A8_CASES = [
+    (4, 16, "auto", torch.float8_e4m3fn),
+    (4, 128, None, torch.float16),
+    (6, 16, None, torch.float8_e4m3fn),
+    (6, 64, None, torch.float16),
+]
+
+
+@pytest.mark.parametrize("bits,gs,cb,srdt", W4A8_CASES)
+@pytest.mark.parametrize("m", [1, 130])
+def test_w4a8_linear(bits, gs, cb, srdt, m):
+    n, k, g = 160, 1024, 256
+    rng = np.random.default_rng(10 + bits)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    q, s_rel, s_ch, book = qz().quantize_w4a8_int8_weight(w, bits=bits, group_size=gs, convrot_groupsize=g,
+                                                          codebook=cb, s_rel_dtype=srdt)
+    x = x_fp16(m, k, seed=m, outliers=True)
+    b = torch.randn(n, generator=torch.Generator().manual_seed(9)) * 0.1
+    dev = lambda t: None if t is None else t.to(DEV)
+    Q = qlin()
+    y = Q.w4a8_int8_linear(x.to(DEV), dev(q), dev(s_rel), dev(s_ch), dev(book), None, None, gs, g)
+    # (1) the weight grid is bit-exact with the oracle's decode
+    sr32 = s_rel.float().numpy()
+    w8 = O.w4a8_int8_grid(q.numpy(), sr32, None if book is None else book.numpy(), k, bits, gs)
+    assert np.array_equal(Q.w4a8_int8_grid(dev(q), dev(s_rel), dev(book), gs).cpu().numpy(), w8)
+    # (2) exact replay of the int8 GEMM + epilogue on the activations the GPU quantized
+    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), g)
+    xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
+    acc = O.int8_gemm_i64(xq, w8)
+    replay = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * s_ch.numpy()[None, :]).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), replay.astype(np.float16).view(np.uint16))
+    # (3) tolerance against a float64 matmul over the dequantized operands
+    want = O.linear_ref(xq.astype(np.float32) * sx[:, None], w8.astype(np.float32) * s_ch.numpy()[:, None])
+    check_linear(y, want, f"bits={bits} gs={gs} M={m}")
+    # bias joins after the rescale
+    yb = Q.w4a8_int8_linear(x.to(DEV), dev(q), dev(s_rel), dev(s_ch), dev(book), None, dev(b), gs, g)
+    check_linear(yb, want + b.numpy()[None, :].astype(np.float64), "bias")
+
+
+@pytest.mark.parametrize("case", ["gauss_96x1024", "heavy_96x1024"])
+@pytest.mark.parametrize("fmt,bits", [("w4a8", 4), ("w6a8", 6)])
+def test_dequantize_w4a8_golden(case, fmt, bits):
+    """The reference's stored W4A8/W6A8 tensors decode on the GPU to its error figures."""
+    from inputs import selftest_inputs
+    raw = np.load(os.path.join(HERE, "golden", "selftest_raw.npz"))
+    meta = json.load(open(os.path.join(HERE, "golden", "selftest_sha256.json")))["cases"][case]["formats"][fmt]
+    w = selftest_inputs((case,))[case]
+    q = torch.from_numpy(raw[f"{case}/{fmt}/q"].reshape(96, -1).copy()).to(DEV)
+    sr = torch.from_numpy(raw[f"{case}/{fmt}/s_rel"].reshape(96, -1).copy()).view(torch.float8_e4m3fn).to(DEV)
+    sc = torch.from_numpy(raw[f"{case}/{fmt}/s_channel"].copy().view(np.float32)).to(DEV)
+    key = f"{case}/{fmt}/codebook"
+    cb = torch.from_numpy(raw[key].copy().view(np.float32)).to(DEV) if key in raw.files else None
+    deq = qlin().dequantize_w4a8_int8_weight(q, sr, sc, cb, None, 16, 256).cpu().numpy()
+    d = deq.astype(np.float64) - w
+    rel = float(np.sqrt((d ** 2).sum() / (w.astype(np.float64) ** 2).sum()))
+    assert rel == pytest.approx(meta["rel_fro"], rel=1e-6)
+    assert float(np.abs(d).max()) == pytest.approx(meta["max_abs"], rel=1e-5)
+
+
+def test_w4a8_declines():
+    Q = qlin()
+    q = torch.zeros(16, 128, dtype=torch.int8, device=DEV)
+    sr = torch.ones(16, 16, device=DEV)
+    sc = torch.ones(16, device=DEV)
+    x = torch.randn(2, 256, device=DEV).half()
+    with pytest.raises(Q.NoCapableBackendError):
+        Q.w4a8_int8_linear(x, q, sr, sc, None, torch.zeros(16, 16, device=DEV))
+    with pytest.raises(Q.NoCapableBackendError):
+        Q.w4a8_int8_linear(x, q, sr, sc, lora_up=torch.zeros(16, 1, device=DEV))
