@@ -45,9 +45,8 @@ def make_gguf_weights(name, n, k, copies, seed=0):
     import numpy as np
     import torch
     from qlin.quantize import quantize_gguf
-    rng = np.random.default_rng(seed)
     out = []
-    base = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    base = (torch.randn(n, k, generator=torch.Generator().manual_seed(seed)) * 0.02).numpy()
     raw = torch.from_numpy(quantize_gguf(base, name))
     for c in range(copies):
         # distinct bytes per copy: permute the block rows (still valid blocks) so no two copies alias
@@ -179,13 +178,15 @@ def cpu_baseline_gguf(n=4096, k=4096, ms=(1, 8, 64), rows=None):
 
 
 def other_suites(which, steps, warmup):
-    """INT8-ConvRot, W4A8, W6A8 and the DiT stack at their BASELINE shapes (stderr JSON lines)."""
-    import numpy as np
+    """INT8-ConvRot, W4A8, W6A8 and the DiT layer stack at their benchmark shapes (stderr JSON lines)."""
     import torch
     import qlin
     from qlin.quantize import quantize_int8_convrot_weight, quantize_w4a8_int8_weight
     out = []
-    rng = np.random.default_rng(0)
+    gen = torch.Generator().manual_seed(0)
+
+    def weight(n, k):
+        return (torch.randn(n, k, generator=gen) * 0.02).numpy()
 
     def timed(name, fn, flops, nbytes, peak, unit):
         msr, _ = time_graph(fn, steps, warmup)
@@ -198,16 +199,16 @@ def other_suites(which, steps, warmup):
 
     if which in ("int8", "all"):
         m, n, k = 256, 3072, 3072
-        q, s = quantize_int8_convrot_weight((rng.standard_normal((n, k)) * 0.02).astype(np.float32), 128)
+        q, s = quantize_int8_convrot_weight(weight(n, k), 128)
         qd, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).half().cuda()
         x = torch.randn(m, k).half().cuda()
         timed("int8_convrot M256 K3072 N3072", lambda: qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=128),
               2 * m * n * k, n * k + n * 2 + m * k * 2 + m * n * 2, FP16_PEAK_TFLOPS, "TFLOPs")
     if which in ("w4a8", "all"):
         m, n, k = 4096, 12288, 3072
-        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
-        q, sr, sc, cb = quantize_w4a8_int8_weight(w, bits=4, group_size=128, convrot_groupsize=128, codebook=None,
-                                                  s_rel_dtype=torch.float16)
+        log("[w4a8] quantizing 12288x3072 ...")
+        q, sr, sc, cb = quantize_w4a8_int8_weight(weight(n, k), bits=4, group_size=128, convrot_groupsize=128,
+                                                  codebook=None, s_rel_dtype=torch.float16)
         qd, srd, scd = q.cuda(), sr.cuda(), sc.cuda()
         g = torch.Generator().manual_seed(2)
         x = torch.randn(m, k, generator=g)
@@ -215,11 +216,14 @@ def other_suites(which, steps, warmup):
         timed("w4a8 M4096 K3072 N12288", lambda: qlin.w4a8_int8_linear(x, qd, srd, scd, None, None, None, 128, 128),
               2 * m * n * k, q.numel() + sr.numel() * 2 + n * 4 + m * k * 2 + m * n * 2, INT8_PEAK_TOPS, "TOPs")
     if which in ("w6a8", "all"):
+        packed = {}
+        for (n, k) in ((13824, 5120), (5120, 13824)):
+            log(f"[w6a8] quantizing {n}x{k} ...")
+            q, sr, sc, cb = quantize_w4a8_int8_weight(weight(n, k), bits=6, group_size=64, convrot_groupsize=256,
+                                                      codebook=None, s_rel_dtype=torch.float16)
+            packed[(n, k)] = (q, sr, sc)
         for m in (1024, 9504):
-            for (n, k) in ((13824, 5120), (5120, 13824)):
-                w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
-                q, sr, sc, cb = quantize_w4a8_int8_weight(w, bits=6, group_size=64, convrot_groupsize=256,
-                                                          codebook=None, s_rel_dtype=torch.float16)
+            for (n, k), (q, sr, sc) in packed.items():
                 qd, srd, scd = q.cuda(), sr.cuda(), sc.cuda()
                 x = torch.randn(m, k).half().cuda()
                 timed(f"w6a8 M{m} K{k} N{n}", lambda: qlin.w4a8_int8_linear(x, qd, srd, scd, None, None, None, 64, 256),
@@ -229,7 +233,7 @@ def other_suites(which, steps, warmup):
         shapes = [(9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288)]
         layer = []
         for (n, k) in shapes:
-            q, s = quantize_int8_convrot_weight((rng.standard_normal((n, k)) * 0.02).astype(np.float32), 128)
+            q, s = quantize_int8_convrot_weight(weight(n, k), 128)
             layer.append((torch.from_numpy(q).cuda(), torch.from_numpy(s).half().cuda(),
                           torch.randn(m, k).half().cuda()))
         dense = [(torch.randn(n, k).half().cuda() * 0.02, torch.randn(m, k).half().cuda()) for (n, k) in shapes]

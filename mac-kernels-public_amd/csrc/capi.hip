@@ -267,6 +267,22 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
     const bool aligned = ((uintptr_t)weight % 4) == 0;
+    if (M == 1 && aligned) {
+        const f16* xo;
+        int64_t ldx;
+        const int32_t* eo;
+        Carver probe = ws;
+        // the activation row must be fp16 and 16-byte aligned: use x itself or the prologue's row
+        if ((s = wo_activations(X, 0, probe, st, xo, ldx, eo))) return s;
+        if (gguf_gemv_supported(ggml_type, 1, K, row_bytes, weight, xo)) {
+            GgufGemvArgs g;
+            g.type = ggml_type; g.x = xo; g.xexp = eo; g.w = (const uint8_t*)weight; g.row_bytes = row_bytes;
+            g.N = (int)N; g.K = (int)K;
+            g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
+            g.y = Y.data; g.y_dtype = Y.dtype;
+            return hip_status(run_gguf_gemv(g, st), "gguf gemv");
+        }
+    }
     if (aligned && gguf_smallm_supported(ggml_type, M, K, row_bytes)) {
         GgufSmallMArgs a;
         a.type = ggml_type;

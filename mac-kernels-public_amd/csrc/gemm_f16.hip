@@ -116,7 +116,7 @@ __device__ __forceinline__ void store_tile(f16* As, f16* Bs, int tid, const Tile
     }
 }
 
-template <int WK, int GT, typename TOut, typename TBias, typename TScale>
+template <int WK, int GT>
 __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
     __shared__ __attribute__((aligned(16))) f16 smem[2][2][BM * LDK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -169,17 +169,15 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
     }
 
     // Epilogue.  acc[i][j][v] = D[m = wm*64 + 16i + 4g + v][n = wn*64 + 16j + r16].
-    TOut* y = (TOut*)a.y;
-    const TBias* bias = (const TBias*)a.bias;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t n = n0 + wn * 64 + 16 * j + r16;
         if (n >= a.N) continue;
         float cs;
         int ce = 0;
-        if constexpr (WK == WO_INT8) cs = load_f((const TScale*)a.scale + n * a.scale_stride);
+        if constexpr (WK == WO_INT8) cs = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
         else { cs = 1.0f; ce = a.wexp[n]; }
-        const float bv = bias ? load_f(bias + n) : 0.0f;
+        const float bv = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -190,42 +188,17 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
                 float val = __builtin_ldexpf(acc[i][j][v], e);
                 if constexpr (WK == WO_INT8) val *= cs;
                 val += bv;
-                store_out(y + m * a.ldy + n, val);
+                store_rt(a.y, a.y_dtype, m * a.ldy + n, val);
             }
-    }
-}
-
-template <int WK, int GT, typename TOut, typename TBias>
-hipError_t launch3(const GemmF16Args& a, hipStream_t st) {
-    dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);
-    if constexpr (WK == WO_INT8) {
-        if (a.scale_dtype == DT_F32) hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, float>), grid, block, 0, st, a);
-        else if (a.scale_dtype == DT_F16) hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, f16>), grid, block, 0, st, a);
-        else if (a.scale_dtype == DT_BF16) hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, bf16_t>), grid, block, 0, st, a);
-        else return hipErrorInvalidValue;
-    } else {
-        hipLaunchKernelGGL((gemm_f16_kernel<WK, GT, TOut, TBias, float>), grid, block, 0, st, a);
-    }
-    return hipGetLastError();
-}
-
-template <int WK, int GT, typename TOut>
-hipError_t launch2(const GemmF16Args& a, hipStream_t st) {
-    switch (a.bias_dtype) {
-        case DT_F16: return launch3<WK, GT, TOut, f16>(a, st);
-        case DT_BF16: return launch3<WK, GT, TOut, bf16_t>(a, st);
-        default: return launch3<WK, GT, TOut, float>(a, st);
     }
 }
 
 template <int WK, int GT>
 hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
-    switch (a.y_dtype) {
-        case DT_F32: return launch2<WK, GT, float>(a, st);
-        case DT_F16: return launch2<WK, GT, f16>(a, st);
-        case DT_BF16: return launch2<WK, GT, bf16_t>(a, st);
-    }
-    return hipErrorInvalidValue;
+    if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);
+    hipLaunchKernelGGL((gemm_f16_kernel<WK, GT>), grid, block, 0, st, a);
+    return hipGetLastError();
 }
 
 template <int T>

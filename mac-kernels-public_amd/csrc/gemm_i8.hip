@@ -120,7 +120,7 @@ __device__ __forceinline__ void store_regs(uint8_t* As, uint8_t* Bs, int tid, co
     }
 }
 
-template <int BITS, bool CB, typename TSrel, typename TOut, typename TBias>
+template <int BITS, bool CB, typename TSrel>
 __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][BM * LDB];
     __shared__ float cb_s[16];
@@ -169,8 +169,6 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
         __syncthreads();
     }
 
-    TOut* y = (TOut*)p.y;
-    const TBias* bias = (const TBias*)p.bias;
     // Epilogue rounds each operation separately (no fused multiply-add), so the output is exactly
     // fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]).
     {
@@ -180,7 +178,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
         const int64_t n = n0 + wn * 64 + 16 * j + r16;
         if (n >= p.N) continue;
         const float sc = p.s_ch[n];
-        const float bv = bias ? load_f(bias + n) : 0.0f;
+        const float bv = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -189,32 +187,19 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
                 if (m >= p.M) continue;
                 float val = (float)acc[i][j][v] * p.sx[m];
                 val = val * sc;
-                if (bias) val = val + bv;
-                store_out(y + m * p.ldy + n, val);
+                if (p.bias) val = val + bv;
+                store_rt(p.y, p.y_dtype, m * p.ldy + n, val);
             }
     }
     }
 }
 
-template <int BITS, bool CB, typename TSrel, typename TOut>
-hipError_t launch_b(const GemmI8Args& p, hipStream_t st) {
-    dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM)), block(256);
-    switch (p.bias_dtype) {
-        case DT_F16: hipLaunchKernelGGL((gemm_i8_kernel<BITS, CB, TSrel, TOut, f16>), grid, block, 0, st, p); break;
-        case DT_BF16: hipLaunchKernelGGL((gemm_i8_kernel<BITS, CB, TSrel, TOut, bf16_t>), grid, block, 0, st, p); break;
-        default: hipLaunchKernelGGL((gemm_i8_kernel<BITS, CB, TSrel, TOut, float>), grid, block, 0, st, p); break;
-    }
-    return hipGetLastError();
-}
-
 template <int BITS, bool CB, typename TSrel>
 hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
-    switch (p.y_dtype) {
-        case DT_F32: return launch_b<BITS, CB, TSrel, float>(p, st);
-        case DT_F16: return launch_b<BITS, CB, TSrel, f16>(p, st);
-        case DT_BF16: return launch_b<BITS, CB, TSrel, bf16_t>(p, st);
-    }
-    return hipErrorInvalidValue;
+    if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM)), block(256);
+    hipLaunchKernelGGL((gemm_i8_kernel<BITS, CB, TSrel>), grid, block, 0, st, p);
+    return hipGetLastError();
 }
 
 template <int BITS, bool CB>

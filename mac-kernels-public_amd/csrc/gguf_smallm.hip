@@ -1,16 +1,24 @@
 // GGUF linear for small M (1..64 activation rows): the weight-streaming (HBM-bound) regime.
 //
-// Grid: one 512-thread workgroup (8 waves) per 16 weight rows n; the K range is split across
-// the 8 waves in stages of 256 values, and the partial sums are reduced through LDS at the end.
-// Per stage a wave copies the 16 rows' packed blocks for those 256 values into its own LDS
-// region with coalesced dword loads (prefetching the next stage into registers while it
-// computes), then for every scale group (unit) decodes exact small-integer codes for the MFMA B
-// operand (lane = row n, lane/16 = k slice), multiplies with the fp16 activations on
-// v_mfma_f32_16x16x{32,16}_f16 and applies the unit's fp32 scale and offset to the 4 outputs it
-// holds:  y[m,n] += a[n,u] * sum_k x[m,k] q[n,k] + b[n,u] * sum_k x[m,k].
-// Accumulation is fp32 throughout; no fp16 weight rounding and no range normalization are needed.
+// Grid: one 512-thread workgroup (8 waves) per 16 weight rows n; the K range is split across the
+// 8 waves in stages (256 values, or 512 for the 210/110-byte K-quant blocks), and the partial sums
+// are reduced through LDS at the end.  Each wave issues the loads of its whole K slice up front
+// (16-, 8- or 4-byte units as the block size allows), parks them in registers, and per stage
+// copies them into its own LDS region.  From there every lane decodes the MFMA B operand for
+// (row n = lane % 16, k slice lane / 16) as EXACT small integers in fp16 -- nibbles become
+// 1024 + q through v_perm_b32 with 0x64 exponent bytes -- and runs v_mfma_f32_16x16x{32,16}_f16
+// against the fp16 activations.  Scales stay in fp32:
+//   * per-block formats (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL) and Q6_K / IQ4_XS (whose scaled
+//     codes exceed fp16's exact-integer range): y += a_unit * C (+ b_unit * sum x),
+//   * K-quants with small sub-scales (Q2_K, Q3_K, Q4_K, Q5_K): the 6-bit (4-bit) sub-scale is
+//     folded into the operand exactly (|sc * q| <= 1953, computed by one fp16 FMA), the sub-block
+//     minimum rides in a second MFMA, both accumulate over the 256-value block inside the MFMA
+//     accumulators, and the fp16 block scales d, dmin are applied once per block.
+// No fp16 weight rounding and no range normalization: every product is formed in fp32.
+#include <type_traits>
+
 #include "qlin_internal.h"
-#include "gguf_codes.h"
+#include "gguf_exact.h"
 
 namespace qlin {
 
@@ -20,15 +28,245 @@ constexpr int SM_WAVES = 8;
 constexpr int SM_THREADS = SM_WAVES * 64;
 
 template <int VPL> struct FragT;
-template <> struct FragT<8> { typedef f16x8 type; };
-template <> struct FragT<4> { typedef f16x4 type; };
+template <> struct FragT<8> { typedef f16x8 type; typedef u32x4 bits; };
+template <> struct FragT<4> { typedef f16x4 type; typedef u32x2 bits; };
 
 template <int VPL>
-__device__ __forceinline__ f32x4 mfma16(typename FragT<VPL>::type a, typename FragT<VPL>::type b) {
-    f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (VPL == 8) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, z, 0, 0, 0);
-    else return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, z, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma16(typename FragT<VPL>::type a, typename FragT<VPL>::type b, f32x4 c) {
+    if constexpr (VPL == 8) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
+
+// --------------------------------------------------------------------------------------------
+// Byte -> fp16 helpers.  `t` holds four bytes b0..b3 (each < 1024 - 1024 offset fits 10 bits);
+// perm64 pairs them with 0x64 high bytes: fp16 (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3).
+// --------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t perm64_lo(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04010400u); }
+__device__ __forceinline__ uint32_t perm64_hi(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04030402u); }
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ uint32_t as_u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// 8 bytes (< 256 each, as two dwords) -> 8 fp16 (1024 + byte) + off, exactly.
+__device__ __forceinline__ f16x8 bytes_to_f16x8(uint32_t t0, uint32_t t1, f16 off) {
+    const f16x2 o = {off, off};
+    u32x4 r;
+    r.x = as_u(as_h2(perm64_lo(t0)) + o);
+    r.y = as_u(as_h2(perm64_hi(t0)) + o);
+    r.z = as_u(as_h2(perm64_lo(t1)) + o);
+    r.w = as_u(as_h2(perm64_hi(t1)) + o);
+    return __builtin_bit_cast(f16x8, r);
+}
+// Same, scaled: ((1024 + byte) * s - 1024 * s) = byte * s with one fp16 rounding of an exact
+// integer result (callers keep |byte * s| <= 2048).
+__device__ __forceinline__ f16x8 bytes_to_f16x8_scaled(uint32_t t0, uint32_t t1, f16 s, f16 off) {
+    const f16x2 sv = {s, s}, o = {off, off};
+    u32x4 r;
+    r.x = as_u(__builtin_elementwise_fma(as_h2(perm64_lo(t0)), sv, o));
+    r.y = as_u(__builtin_elementwise_fma(as_h2(perm64_hi(t0)), sv, o));
+    r.z = as_u(__builtin_elementwise_fma(as_h2(perm64_lo(t1)), sv, o));
+    r.w = as_u(__builtin_elementwise_fma(as_h2(perm64_hi(t1)), sv, o));
+    return __builtin_bit_cast(f16x8, r);
+}
+__device__ __forceinline__ f16x4 bytes_to_f16x4(uint32_t t, f16 off) {
+    const f16x2 o = {off, off};
+    u32x2 r;
+    r.x = as_u(as_h2(perm64_lo(t)) + o);
+    r.y = as_u(as_h2(perm64_hi(t)) + o);
+    return __builtin_bit_cast(f16x4, r);
+}
+__device__ __forceinline__ f16x4 bytes_to_f16x4_scaled(uint32_t t, f16 s, f16 off) {
+    const f16x2 sv = {s, s}, o = {off, off};
+    u32x2 r;
+    r.x = as_u(__builtin_elementwise_fma(as_h2(perm64_lo(t)), sv, o));
+    r.y = as_u(__builtin_elementwise_fma(as_h2(perm64_hi(t)), sv, o));
+    return __builtin_bit_cast(f16x4, r);
+}
+
+// Spread bits 0..3 of x to bit 0 of bytes 0..3.
+__device__ __forceinline__ uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
+
+// IQ4_NL levels + 128 as bytes: lut(i) for 4 nibble bytes at once (two 8-entry v_perm lookups and
+// a byte select on bit 3).
+__device__ __forceinline__ uint32_t iq4_lut4(uint32_t idx) {
+    const uint32_t L0 = 0x3F2D1801u;  // -127..-65 + 128:  1, 24, 45, 63
+    const uint32_t L1 = 0x766A5D4Fu;  // -49..-10 + 128:  79, 93, 106, 118
+    const uint32_t L2 = 0xA6998D81u;  // 1..38 + 128:   129, 141, 153, 166
+    const uint32_t L3 = 0xF1D9C5B5u;  // 53..113 + 128: 181, 197, 217, 241
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(L1, L0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(L3, L2, sel);
+    const uint32_t m8 = idx & 0x08080808u;
+    const uint32_t mask = (m8 << 5) - (m8 >> 3);
+    return (hi & mask) | (lo & ~mask);
+}
+
+// --------------------------------------------------------------------------------------------
+// Format policies.  KIND 0: one fp32 scale (and offset) per unit; KIND 1: sub-scales folded,
+// fp32 d (dmin) per block.  get() decodes this lane's VPL values of the unit starting at value v0
+// of the block at byte offset o of the LDS stage row s.
+// --------------------------------------------------------------------------------------------
+template <int T> struct SM;
+
+__device__ __forceinline__ float lds_f16(const uint8_t* s, int off) { return f16_bits_to_f32(ld_u16(s, off)); }
+
+template <> struct SM<gguf::Q8_0> {
+    static constexpr int QK = 32, TS = 34, UNIT = 32, SBLK = 8, KIND = 0;
+    static constexpr bool MIN = false;
+    __device__ static f16x8 get(const uint8_t* s, int o, int v0, float& a, float& b) {
+        a = lds_f16(s, o);
+        b = 0.0f;
+        const uint32_t w0 = ld_u32(s, o + 2 + v0) ^ 0x80808080u, w1 = ld_u32(s, o + 6 + v0) ^ 0x80808080u;
+        return bytes_to_f16x8(w0, w1, (f16)-1152.0f);
+    }
+};
+
+template <int T> struct SMNib32 {
+    static constexpr int QK = 32, TS = (T == gguf::Q4_1) ? 20 : 18, UNIT = 32, SBLK = 8, KIND = 0;
+    static constexpr bool MIN = (T == gguf::Q4_1);
+    __device__ static f16x8 get(const uint8_t* s, int o, int v0, float& a, float& b) {
+        constexpr int qo = (T == gguf::Q4_1) ? 4 : 2;
+        a = lds_f16(s, o);
+        b = MIN ? lds_f16(s, o + 2) : 0.0f;
+        const int sh = (v0 >> 4) * 4;
+        uint32_t t0 = (ld_u32(s, o + qo + (v0 & 15)) >> sh) & 0x0F0F0F0Fu;
+        uint32_t t1 = (ld_u32(s, o + qo + (v0 & 15) + 4) >> sh) & 0x0F0F0F0Fu;
+        if constexpr (T == gguf::IQ4_NL) {
+            t0 = iq4_lut4(t0);
+            t1 = iq4_lut4(t1);
+            return bytes_to_f16x8(t0, t1, (f16)-1152.0f);
+        }
+        return bytes_to_f16x8(t0, t1, (f16)((T == gguf::Q4_0) ? -1032.0f : -1024.0f));
+    }
+};
+template <> struct SM<gguf::Q4_0> : SMNib32<gguf::Q4_0> {};
+template <> struct SM<gguf::Q4_1> : SMNib32<gguf::Q4_1> {};
+template <> struct SM<gguf::IQ4_NL> : SMNib32<gguf::IQ4_NL> {};
+
+template <int T> struct SMQ5 {
+    static constexpr int QK = 32, TS = (T == gguf::Q5_0) ? 22 : 24, UNIT = 32, SBLK = 8, KIND = 0;
+    static constexpr bool MIN = (T == gguf::Q5_1);
+    __device__ static f16x8 get(const uint8_t* s, int o, int v0, float& a, float& b) {
+        constexpr int ho = (T == gguf::Q5_0) ? 2 : 4;
+        a = lds_f16(s, o);
+        b = MIN ? lds_f16(s, o + 2) : 0.0f;
+        const uint32_t qh = ld_u32(s, o + ho) >> v0;  // bits of values v0..v0+7
+        const int sh = (v0 >> 4) * 4;
+        const uint32_t t0 = ((ld_u32(s, o + ho + 4 + (v0 & 15)) >> sh) & 0x0F0F0F0Fu) | (spread4(qh) << 4);
+        const uint32_t t1 = ((ld_u32(s, o + ho + 8 + (v0 & 15)) >> sh) & 0x0F0F0F0Fu) | (spread4(qh >> 4) << 4);
+        return bytes_to_f16x8(t0, t1, (f16)((T == gguf::Q5_0) ? -1040.0f : -1024.0f));
+    }
+};
+template <> struct SM<gguf::Q5_0> : SMQ5<gguf::Q5_0> {};
+template <> struct SM<gguf::Q5_1> : SMQ5<gguf::Q5_1> {};
+
+template <> struct SM<gguf::IQ4_XS> {
+    static constexpr int QK = 256, TS = 136, UNIT = 32, SBLK = 1, KIND = 0;
+    static constexpr bool MIN = false;
+    __device__ static f16x8 get(const uint8_t* s, int o, int v0, float& a, float& b) {
+        const int sb = v0 >> 5;
+        const uint32_t hdr = ld_u32(s, o), sl = ld_u32(s, o + 4);
+        const int ls = ((sl >> (8 * (sb >> 1) + 4 * (sb & 1))) & 0xF) | (int)(((hdr >> (16 + 2 * sb)) & 3u) << 4);
+        a = f16_bits_to_f32((uint16_t)(hdr & 0xFFFFu)) * (float)(ls - 32);
+        b = 0.0f;
+        const int i = v0 & 31, sh = (i >> 4) * 4;
+        const uint32_t t0 = iq4_lut4((ld_u32(s, o + 8 + 16 * sb + (i & 15)) >> sh) & 0x0F0F0F0Fu);
+        const uint32_t t1 = iq4_lut4((ld_u32(s, o + 12 + 16 * sb + (i & 15)) >> sh) & 0x0F0F0F0Fu);
+        return bytes_to_f16x8(t0, t1, (f16)-1152.0f);
+    }
+};
+
+template <> struct SM<gguf::Q6_K> {
+    static constexpr int QK = 256, TS = 210, UNIT = 16, SBLK = 2, KIND = 0;
+    static constexpr bool MIN = false;
+    __device__ static f16x4 get(const uint8_t* s, int o, int v0, float& a, float& b) {
+        a = lds_f16(s, o + 208) * (float)(int)(int8_t)(ld_u32(s, o + 192 + (v0 >> 4)) & 0xFFu);
+        b = 0.0f;
+        const int h = v0 >> 7, r = v0 & 127;
+        const uint32_t lo = (ld_u32(s, o + 64 * h + (r & 63)) >> (4 * (r >> 6))) & 0x0F0F0F0Fu;
+        const uint32_t hi = (ld_u32(s, o + 128 + 32 * h + (r & 31)) >> (2 * (r >> 5))) & 0x03030303u;
+        return bytes_to_f16x4(lo | (hi << 4), (f16)-1056.0f);
+    }
+};
+
+// K-quants with folded sub-scales.  get() returns the operand sc*q for this lane and the
+// sub-block minimum (fp16, exact) for the second MFMA; block() returns the fp32 d, dmin.
+template <int T> struct SMK45 {
+    static constexpr int QK = 256, TS = (T == gguf::Q4_K) ? 144 : 176, UNIT = 32, SBLK = 1, KIND = 1;
+    static constexpr bool MIN = true;
+    __device__ static void block(const uint8_t* s, int o, float& d, float& dmin) {
+        const uint32_t h = ld_u32(s, o);
+        d = f16_bits_to_f32((uint16_t)(h & 0xFFFFu));
+        dmin = f16_bits_to_f32((uint16_t)(h >> 16));
+    }
+    __device__ static f16x8 get(const uint8_t* s, int o, int v0, f16& mv) {
+        const int sb = v0 >> 5;
+        const uint32_t s0 = ld_u32(s, o + 4), s1 = ld_u32(s, o + 8), s2 = ld_u32(s, o + 12);
+        int sc, mn;
+        if (sb < 4) {
+            sc = (s0 >> (8 * sb)) & 63;
+            mn = (s1 >> (8 * sb)) & 63;
+        } else {
+            const int j = sb - 4;
+            sc = ((s2 >> (8 * j)) & 0xF) | (((s0 >> (8 * j + 6)) & 3) << 4);
+            mn = ((s2 >> (8 * j + 4)) & 0xF) | (((s1 >> (8 * j + 6)) & 3) << 4);
+        }
+        mv = (f16)(float)mn;
+        constexpr int qs = (T == gguf::Q4_K) ? 16 : 48;
+        const int i = v0 & 31, sh = (sb & 1) * 4;
+        uint32_t t0 = (ld_u32(s, o + qs + 32 * (sb >> 1) + i) >> sh) & 0x0F0F0F0Fu;
+        uint32_t t1 = (ld_u32(s, o + qs + 32 * (sb >> 1) + i + 4) >> sh) & 0x0F0F0F0Fu;
+        if constexpr (T == gguf::Q5_K) {
+            t0 |= ((ld_u32(s, o + 16 + i) >> sb) & 0x01010101u) << 4;
+            t1 |= ((ld_u32(s, o + 20 + i) >> sb) & 0x01010101u) << 4;
+        }
+        const f16 scv = (f16)(float)sc;
+        return bytes_to_f16x8_scaled(t0, t1, scv, (f16)(-1024.0f * (float)sc));
+    }
+};
+template <> struct SM<gguf::Q4_K> : SMK45<gguf::Q4_K> {};
+template <> struct SM<gguf::Q5_K> : SMK45<gguf::Q5_K> {};
+
+template <> struct SM<gguf::Q2_K> {
+    static constexpr int QK = 256, TS = 84, UNIT = 16, SBLK = 1, KIND = 1;
+    static constexpr bool MIN = true;
+    __device__ static void block(const uint8_t* s, int o, float& d, float& dmin) {
+        const uint32_t h = ld_u32(s, o + 80);
+        d = f16_bits_to_f32((uint16_t)(h & 0xFFFFu));
+        dmin = f16_bits_to_f32((uint16_t)(h >> 16));
+    }
+    __device__ static f16x4 get(const uint8_t* s, int o, int v0, f16& mv) {
+        const uint32_t scb = ld_u32(s, o + (v0 >> 4)) & 0xFFu;
+        mv = (f16)(float)(scb >> 4);
+        const int sc = scb & 0xF;
+        const int h = v0 >> 7, t2 = (v0 >> 5) & 3, i0 = v0 & 31;
+        const uint32_t t = (ld_u32(s, o + 16 + 32 * h + i0) >> (2 * t2)) & 0x03030303u;
+        return bytes_to_f16x4_scaled(t, (f16)(float)sc, (f16)(-1024.0f * (float)sc));
+    }
+};
+
+template <> struct SM<gguf::Q3_K> {
+    // value = (d * s6) * q with q = q2 - 4 * (1 - hbit) in -4..3.  The operand carries t = q + 4
+    // (0..7) scaled by s6 exactly, and the second MFMA removes 4 * s6 (dmin = d).
+    static constexpr int QK = 256, TS = 110, UNIT = 16, SBLK = 2, KIND = 1;
+    static constexpr bool MIN = true;
+    __device__ static void block(const uint8_t* s, int o, float& d, float& dmin) {
+        d = lds_f16(s, o + 108);
+        dmin = d;
+    }
+    __device__ static f16x4 get(const uint8_t* s, int o, int v0, f16& mv) {
+        const int si = v0 >> 4;
+        const int lo = (ld_u32(s, o + 96 + (si & 7)) >> (4 * (si >> 3))) & 0xF;
+        const int hs = (ld_u32(s, o + 104 + (si & 3)) >> (2 * (si >> 2))) & 3;
+        const int s6 = (lo | (hs << 4)) - 32;
+        mv = (f16)(float)(4 * s6);
+        const int h = v0 >> 7, t2 = (v0 >> 5) & 3, i0 = v0 & 31, hb = v0 >> 5;
+        const uint32_t q2 = (ld_u32(s, o + 32 + 32 * h + i0) >> (2 * t2)) & 0x03030303u;
+        const uint32_t hm = (ld_u32(s, o + i0) >> hb) & 0x01010101u;
+        const uint32_t t = q2 | (hm << 2);  // q + 4
+        return bytes_to_f16x4_scaled(t, (f16)(float)s6, (f16)(-1024.0f * (float)s6));
+    }
+};
 
 template <int VPL>
 __device__ __forceinline__ typename FragT<VPL>::type load_x(const f16* __restrict__ x, int64_t ldx, int m, int M,
@@ -38,21 +276,26 @@ __device__ __forceinline__ typename FragT<VPL>::type load_x(const f16* __restric
     return *reinterpret_cast<const V*>(x + (int64_t)m * ldx + k);
 }
 
-template <int T, int MT, typename TOut, typename TBias>
+// --------------------------------------------------------------------------------------------
+template <int T, int MT, int W>
 __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
     const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K,
-    const TBias* __restrict__ bias, TOut* __restrict__ y, int64_t ldy) {
-    using C = gguf::Codes<T>;
-    constexpr int QK = C::QK, TS = C::TS, UNIT = C::UNIT, VPL = UNIT / 4;
-    constexpr int SBLK = 256 / QK;                 // blocks per row per stage
-    constexpr int RSB = SBLK * TS;                 // stage bytes per row
-    constexpr int RS = ((RSB + 15) / 16) * 16 + 16; // LDS row stride (padded for over-reads)
-    constexpr int WORDS = 16 * RSB / 4;            // dwords per stage (RSB is even; x16 rows)
-    static_assert((16 * RSB) % 4 == 0, "stage must be whole dwords");
-    constexpr int NPF = (WORDS + 63) / 64;          // prefetch dwords per lane
-    constexpr int UPS = 256 / UNIT;                 // units per stage
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy) {
+    using F = SM<T>;
+    constexpr int QK = F::QK, TS = F::TS, UNIT = F::UNIT, VPL = UNIT / 4, SBLK = F::SBLK;
+    constexpr int SV = SBLK * QK;                    // values per stage
+    constexpr int RSB = SBLK * TS;                   // stage bytes per row
+    constexpr int RS = ((RSB + 15) / 16) * 16 + 16;  // LDS row stride (padded for over-reads)
+    static_assert(RSB % W == 0, "stage bytes must be whole load units");
+    constexpr int UPR = RSB / W;                     // load units per row
+    constexpr int UNITS = 16 * UPR;                  // load units per stage
+    constexpr int NPF = (UNITS + 63) / 64;           // load units per lane per stage
+    // stages held in registers: two when a stage is small, else one (register pressure)
+    constexpr int PF = (NPF <= 12 && MT <= 2) ? 2 : 1;
+    constexpr int UPS = SV / UNIT;                   // scale units per stage
     typedef typename FragT<VPL>::type V;
+    typedef typename std::conditional<W == 16, u32x4, typename std::conditional<W == 8, u32x2, uint32_t>::type>::type LU;
 
     constexpr int STAGE_BYTES = SM_WAVES * 16 * RS;
     constexpr int RED_BYTES = SM_WAVES * MT * 4 * 64 * 4;
@@ -62,76 +305,39 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 16;
     const int nl = lane & 15, g = lane >> 4;
-    const int stages = K / 256;
+    const int stages = K / SV;
     const int st0 = (stages * wave) / SM_WAVES, st1 = (stages * (wave + 1)) / SM_WAVES;
     uint8_t* my = smem + wave * 16 * RS;
+    // rows of the 4 outputs this lane holds per m-tile: 4*g + i; skip FMAs for rows past M when M <= 4
+    const int ilim = (MT == 1 && M < 4) ? M : 4;
 
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // dword u of the stage: row r = u / (RSB/4) when RSB % 4 == 0; RSB may be 2 mod 4 (Q6_K
-    // with one block), so the copy runs over 16-bit halves in that case.
-    uint32_t pf[NPF];
-    auto issue = [&](int st) {
-        if constexpr (RSB % 4 == 0) {
+    LU pf[PF][NPF];
+    auto issue = [&](int st, LU* buf) {
 #pragma unroll
-            for (int i = 0; i < NPF; ++i) {
-                const int u = lane + 64 * i;
-                uint32_t v = 0;
-                if (u < WORDS) {
-                    const int r = u / (RSB / 4);
-                    const int off = (u - r * (RSB / 4)) * 4;
-                    if (n0 + r < N)
-                        v = *reinterpret_cast<const uint32_t*>(w + (int64_t)(n0 + r) * row_bytes +
-                                                               (int64_t)st * RSB + off);
-                }
-                pf[i] = v;
+        for (int i = 0; i < NPF; ++i) {
+            const int u = lane + 64 * i;
+            LU v{};
+            if (u < UNITS) {
+                const int r = u / UPR;
+                const int off = (u - r * UPR) * W;
+                if (n0 + r < N)
+                    v = *reinterpret_cast<const LU*>(w + (int64_t)(n0 + r) * row_bytes + (int64_t)st * RSB + off);
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < NPF; ++i) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int u = 2 * (lane + 64 * i) + hh;  // 16-bit unit index
-                    if (u < 2 * WORDS) {
-                        const int r = u / (RSB / 2);
-                        const int off = (u - r * (RSB / 2)) * 2;
-                        if (n0 + r < N) {
-                            const uint16_t h = *reinterpret_cast<const uint16_t*>(
-                                w + (int64_t)(n0 + r) * row_bytes + (int64_t)st * RSB + off);
-                            v |= (uint32_t)h << (16 * hh);
-                        }
-                    }
-                }
-                pf[i] = v;
-            }
+            buf[i] = v;
         }
     };
-    auto commit = [&]() {
-        if constexpr (RSB % 4 == 0) {
+    auto commit = [&](const LU* buf) {
 #pragma unroll
-            for (int i = 0; i < NPF; ++i) {
-                const int u = lane + 64 * i;
-                if (u < WORDS) {
-                    const int r = u / (RSB / 4);
-                    const int off = (u - r * (RSB / 4)) * 4;
-                    *reinterpret_cast<uint32_t*>(my + r * RS + off) = pf[i];
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < NPF; ++i) {
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int u = 2 * (lane + 64 * i) + hh;
-                    if (u < 2 * WORDS) {
-                        const int r = u / (RSB / 2);
-                        const int off = (u - r * (RSB / 2)) * 2;
-                        *reinterpret_cast<uint16_t*>(my + r * RS + off) = (uint16_t)(pf[i] >> (16 * hh));
-                    }
-                }
+        for (int i = 0; i < NPF; ++i) {
+            const int u = lane + 64 * i;
+            if (u < UNITS) {
+                const int r = u / UPR;
+                const int off = (u - r * UPR) * W;
+                *reinterpret_cast<LU*>(my + r * RS + off) = buf[i];
             }
         }
     };
@@ -140,38 +346,88 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
 #pragma unroll
     for (int i = 0; i < VPL; ++i) ones[i] = (f16)1.0f;
 
-    if (st0 < st1) issue(st0);
-    for (int st = st0; st < st1; ++st) {
-        __builtin_amdgcn_wave_barrier();
-        commit();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (st + 1 < st1) issue(st + 1);
-        const uint8_t* srow = my + nl * RS;
-        const int64_t kst = (int64_t)st * 256;
+    for (int c0 = st0; c0 < st1; c0 += PF) {
 #pragma unroll
-        for (int u = 0; u < UPS; ++u) {
-            const int blk = (u * UNIT) / QK;
-            const int v0 = (u * UNIT) % QK + VPL * g;
-            int q[VPL];
-            float a, b;
-            C::get(srow, blk * TS, v0, q, a, b);
-            V bf;
+        for (int j = 0; j < PF; ++j)
+            if (c0 + j < st1) issue(c0 + j, pf[j]);
 #pragma unroll
-            for (int i = 0; i < VPL; ++i) bf[i] = (f16)(float)q[i];
-            const int64_t k = kst + u * UNIT + VPL * g;
+        for (int j = 0; j < PF; ++j) {
+            const int st = c0 + j;
+            if (st >= st1) break;
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            commit(pf[j]);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint8_t* srow = my + nl * RS;
+            const int64_t kst = (int64_t)st * SV;
+            if constexpr (F::KIND == 0) {
+                auto unit = [&](int u) {
+                    const int blk = (u * UNIT) / QK;
+                    const int v0 = (u * UNIT) % QK + VPL * g;
+                    float a, b;
+                    const V bf = F::get(srow, blk * TS, v0, a, b);
+                    const int64_t k = kst + u * UNIT + VPL * g;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const V af = load_x<VPL>(x, ldx, mt * 16 + nl, M, k);
-                const f32x4 c = mfma16<VPL>(af, bf);
-                if constexpr (C::MIN) {
-                    const f32x4 c1 = mfma16<VPL>(af, ones);
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const V af = load_x<VPL>(x, ldx, mt * 16 + nl, M, k);
+                        const f32x4 c = mfma16<VPL>(af, bf, f32x4{0.f, 0.f, 0.f, 0.f});
+                        if constexpr (F::MIN) {
+                            const f32x4 c1 = mfma16<VPL>(af, ones, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[mt][i] += a * c[i] + b * c1[i];
+                            for (int i = 0; i < 4; ++i)
+                                if (i < ilim) acc[mt][i] += a * c[i] + b * c1[i];
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                if (i < ilim) acc[mt][i] += a * c[i];
+                        }
+                    }
+                };
+                if constexpr (MT == 1) {
+#pragma unroll
+                    for (int u = 0; u < UPS; ++u) unit(u);
                 } else {
+#pragma unroll 2
+                    for (int u = 0; u < UPS; ++u) unit(u);
+                }
+            } else {
+                constexpr int UPB = QK / UNIT;  // units per block
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[mt][i] += a * c[i];
+                for (int blk = 0; blk < SBLK; ++blk) {
+                    f32x4 c1[MT], c2[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        c1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                        c2[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+#pragma unroll
+                    for (int ub = 0; ub < UPB; ++ub) {
+                        const int v0 = ub * UNIT + VPL * g;
+                        f16 mv;
+                        const V bf = F::get(srow, blk * TS, v0, mv);
+                        V bm;
+#pragma unroll
+                        for (int i = 0; i < VPL; ++i) bm[i] = mv;
+                        const int64_t k = kst + blk * QK + v0;
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            const V af = load_x<VPL>(x, ldx, mt * 16 + nl, M, k);
+                            c1[mt] = mfma16<VPL>(af, bf, c1[mt]);
+                            if constexpr (F::MIN) c2[mt] = mfma16<VPL>(af, bm, c2[mt]);
+                        }
+                    }
+                    float d, dmin;
+                    F::block(srow, blk * TS, d, dmin);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (i < ilim) {
+                                acc[mt][i] += d * c1[mt][i];
+                                if constexpr (F::MIN) acc[mt][i] -= dmin * c2[mt][i];
+                            }
                 }
             }
         }
@@ -186,74 +442,67 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     // 16 x 16 outputs per m-tile; thread e handles element (i = e/64, source lane = e%64).
     for (int e = tid; e < MT * 256; e += SM_THREADS) {
         const int mt = e >> 8, rem = e & 255, i = rem >> 6, sl = rem & 63;
-        float sum = 0.0f;
-#pragma unroll
-        for (int wv = 0; wv < SM_WAVES; ++wv) sum += red[wv][mt][i][sl];
         const int m = mt * 16 + 4 * (sl >> 4) + i;
         const int n = n0 + (sl & 15);
         if (m < M && n < N) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < SM_WAVES; ++wv) sum += red[wv][mt][i][sl];
             float v = xexp ? __builtin_ldexpf(sum, xexp[m]) : sum;
-            if (bias) v += load_f(bias + n);
-            store_out(y + (int64_t)m * ldy + n, v);
+            if (bias) v += load_rt(bias, bias_dt, n);
+            store_rt(y, y_dt, (int64_t)m * ldy + n, v);
         }
     }
 }
 
-template <int T, typename TOut, typename TBias>
+// Widest load unit dividing the stage row (16, 8 or 4 bytes).
+template <int T>
+constexpr int best_width() {
+    constexpr int RSB = SM<T>::SBLK * SM<T>::TS;
+    return RSB % 16 == 0 ? 16 : (RSB % 8 == 0 ? 8 : 4);
+}
+
+template <int T>
 hipError_t launch_t(const GgufSmallMArgs& a, hipStream_t st) {
     dim3 grid((unsigned)((a.N + 15) / 16)), block(SM_THREADS);
     const int mt = (a.M + 15) / 16;
-#define QLIN_SM_LAUNCH(MTV)                                                                          \
-    hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV, TOut, TBias>), grid, block, 0, st, a.x, a.ldx, a.M, \
-                       a.xexp, a.w, a.row_bytes, a.N, a.K, (const TBias*)a.bias, (TOut*)a.y, a.ldy)
+    constexpr int WB = best_width<T>();
+    const bool wide = (a.row_bytes % WB == 0) && ((uintptr_t)a.w % WB == 0);
+#define QLIN_SM_LAUNCH(MTV, WV)                                                                             \
+    hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV, WV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
+                       a.row_bytes, a.N, a.K, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy)
+#define QLIN_SM_W(MTV)                \
+    if (wide) QLIN_SM_LAUNCH(MTV, WB); \
+    else QLIN_SM_LAUNCH(MTV, 4);
     switch (mt) {
-        case 1: QLIN_SM_LAUNCH(1); break;
-        case 2: QLIN_SM_LAUNCH(2); break;
-        case 3: QLIN_SM_LAUNCH(3); break;
-        case 4: QLIN_SM_LAUNCH(4); break;
+        case 1: QLIN_SM_W(1); break;
+        case 2: QLIN_SM_W(2); break;
+        case 3: QLIN_SM_W(3); break;
+        case 4: QLIN_SM_W(4); break;
         default: return hipErrorInvalidValue;
     }
+#undef QLIN_SM_W
 #undef QLIN_SM_LAUNCH
     return hipGetLastError();
-}
-
-template <typename TOut, typename TBias>
-hipError_t launch_bias(const GgufSmallMArgs& a, hipStream_t st) {
-    hipError_t err = hipErrorInvalidValue;
-    bool ok = gguf::dispatch_type(a.type, [&]<int T>() { err = launch_t<T, TOut, TBias>(a, st); });
-    return ok ? err : hipErrorInvalidValue;
-}
-
-template <typename TOut>
-hipError_t launch_out(const GgufSmallMArgs& a, hipStream_t st) {
-    switch (a.bias_dtype) {
-        case DT_F32: return launch_bias<TOut, float>(a, st);
-        case DT_F16: return launch_bias<TOut, f16>(a, st);
-        case DT_BF16: return launch_bias<TOut, bf16_t>(a, st);
-        default: return launch_bias<TOut, float>(a, st);  // bias == nullptr
-    }
 }
 
 }  // namespace
 
 bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes) {
-    int qk, ts;
-    if (!gguf::type_info(type, qk, ts)) return false;
-    if (M < 1 || M > 64 || K % 256 != 0) return false;
-    const int rsb = (256 / qk) * ts;
-    if (rsb % 2) return false;
-    // dword copies need every stage start 4-aligned; half-word copies 2-aligned.
-    if (rsb % 4 == 0) return row_bytes % 4 == 0;
-    return row_bytes % 2 == 0;
+    if (M < 1 || M > 64) return false;
+    bool ok = false;
+    gguf::dispatch_type(type, [&]<int T>() {
+        constexpr int SV = SM<T>::SBLK * SM<T>::QK, RSB = SM<T>::SBLK * SM<T>::TS;
+        ok = (K % SV == 0) && (RSB % 4 == 0) && (row_bytes % 4 == 0);
+    });
+    return ok;
 }
 
 hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st) {
-    switch (a.y_dtype) {
-        case DT_F32: return launch_out<float>(a, st);
-        case DT_F16: return launch_out<f16>(a, st);
-        case DT_BF16: return launch_out<bf16_t>(a, st);
-    }
-    return hipErrorInvalidValue;
+    if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    hipError_t err = hipErrorInvalidValue;
+    bool ok = gguf::dispatch_type(a.type, [&]<int T>() { err = launch_t<T>(a, st); });
+    return ok ? err : hipErrorInvalidValue;
 }
 
 }  // namespace qlin

@@ -150,6 +150,19 @@ __device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
 __device__ __forceinline__ void store_out(f16* p, float v) { *p = (f16)v; }
 __device__ __forceinline__ void store_out(bf16_t* p, float v) { p->bits = f32_to_bf16_bits(v); }
 
+// Runtime-typed output store / bias load (the dtype is uniform across the launch, so the branch
+// costs one scalar compare).
+__device__ __forceinline__ void store_rt(void* base, int dtype, int64_t idx, float v) {
+    if (dtype == 0) reinterpret_cast<float*>(base)[idx] = v;
+    else if (dtype == 1) reinterpret_cast<f16*>(base)[idx] = (f16)v;
+    else reinterpret_cast<uint16_t*>(base)[idx] = f32_to_bf16_bits(v);
+}
+__device__ __forceinline__ float load_rt(const void* base, int dtype, int64_t idx) {
+    if (dtype == 0) return reinterpret_cast<const float*>(base)[idx];
+    if (dtype == 1) return (float)reinterpret_cast<const f16*>(base)[idx];
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[idx]);
+}
+
 __device__ __forceinline__ float load_f(const float* p) { return *p; }
 __device__ __forceinline__ float load_f(const f16* p) { return (float)*p; }
 __device__ __forceinline__ float load_f(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }

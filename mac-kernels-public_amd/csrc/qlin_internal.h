@@ -49,6 +49,22 @@ struct GgufSmallMArgs {
 bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes);
 hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st);
 
+// ---- GGUF single-row linear (gguf_gemv.hip) ----
+struct GgufGemvArgs {
+    int type = 0;
+    const f16* x = nullptr;          // one fp16 activation row (16-byte aligned)
+    const int32_t* xexp = nullptr;   // its exponent to restore (nullptr = 0)
+    const uint8_t* w = nullptr;
+    int64_t row_bytes = 0;
+    int N = 0, K = 0;
+    const void* bias = nullptr;
+    int bias_dtype = DT_NONE;
+    void* y = nullptr;
+    int y_dtype = DT_F16;
+};
+bool gguf_gemv_supported(int type, int64_t M, int64_t K, int64_t row_bytes, const void* w, const void* x);
+hipError_t run_gguf_gemv(const GgufGemvArgs& a, hipStream_t st);
+
 // ---- weight-only fp16 MFMA tile GEMM (gemm_f16.hip) ----
 enum { WO_INT8 = 0, WO_GGUF = 1 };
 struct GemmF16Args {
