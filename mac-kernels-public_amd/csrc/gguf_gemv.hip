@@ -5,9 +5,11 @@
 //   * each lane owns one contiguous "chunk" of a weight row (64 or 128 values: a run of whole
 //     32-value blocks, or part of a 256-value super-block) and loads it with 16-byte global loads
 //     (only 4-byte alignment is needed); a row is covered by 16..64 lanes, a wave covers 1..4 rows;
-//   * the activation row is staged once per workgroup in LDS; each lane keeps the fp16 pairs for
-//     its chunk in registers, permuted to match the decode order, plus fp32 sums over each scale
-//     group (needed by the offsets below);
+//   * the activation row is read once per workgroup with coalesced loads and staged in LDS in a
+//     swizzled order (a lane's own chunk, read with a 256-byte lane stride straight from global
+//     memory, would touch a different cache line per lane and per load); each lane keeps its
+//     chunk in registers as fp16 pairs permuted to match the decode order, plus fp32 sums over
+//     each scale group (needed by the offsets below);
 //   * 4-bit codes: nibble pairs become fp16 (1024 + q) with one v_and_or_b32 ("0x6400 | nibble");
 //     the 1024 (and any format offset) is removed in fp32 through the group sums:
 //         sum_k x_k * (a * q_k + b) = a * (S - 1024 * sum x) + b * sum x,  S = sum x_k (1024 + q_k);
@@ -34,6 +36,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 constexpr int GV_THREADS = 256;
+constexpr int GV_MAX_K = 8192;
 
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 
@@ -174,7 +177,7 @@ template <> struct GV<gguf::Q5_K> : GVK45<gguf::Q5_K> {};
 
 // Q8_0: chunk = 2 blocks (68 bytes, 64 values).
 template <> struct GV<gguf::Q8_0> {
-    static constexpr int QK = 32, TS = 34, VC = 64, XP = 32, NG = 2, LD = 17;
+    static constexpr int VC = 64, XP = 32, NG = 2, LD = 17;
     static constexpr bool LUT = false;
     __device__ static void load(const uint8_t* row, int c, uint32_t* r) { load_dwords<17>(row + (int64_t)c * 68, r); }
     __device__ static void prep_x(const uint32_t* xn, uint32_t* xp, float* xs) {
@@ -261,7 +264,7 @@ template <> struct GV<gguf::IQ4_NL> : GVTab32<gguf::IQ4_NL> {};
 
 // IQ4_XS: chunk = half super-block (sub-blocks 4h..4h+3, 128 values).
 template <> struct GV<gguf::IQ4_XS> {
-    static constexpr int QK = 256, TS = 136, VC = 128, XP = 64, NG = 4, LD = 18;
+    static constexpr int TS = 136, VC = 128, XP = 64, NG = 4, LD = 18;
     static constexpr bool LUT = true;
     __device__ static void load(const uint8_t* row, int c, uint32_t* r) {
         const uint8_t* b = row + (int64_t)(c >> 1) * TS;
@@ -298,8 +301,10 @@ template <> struct GV<gguf::IQ4_XS> {
 // Blocks are 210 bytes, so a block may start 2 bytes off a dword boundary; each region is loaded
 // from the dword below it and realigned with v_alignbyte.
 template <> struct GV<gguf::Q6_K> {
-    static constexpr int QK = 256, TS = 210, VC = 128, XP = 64, NG = 8, LD = 17 + 9 + 3 + 1;
+    static constexpr int TS = 210, VC = 128, XP = 64, NG = 8, LD = 17 + 9 + 3 + 1 + 1;
     static constexpr bool LUT = false;
+    // raw dwords as loaded (realigned in dot(), so that no loaded value is used before the
+    // activation staging); r[30] = the block's byte offset from a dword boundary (0 or 2)
     __device__ static void load(const uint8_t* row, int c, uint32_t* r) {
         const int h = c & 1;
         const uint8_t* b = row + (int64_t)(c >> 1) * TS;
@@ -308,22 +313,25 @@ template <> struct GV<gguf::Q6_K> {
         // ql and qh halves end at least 14 bytes before the block end: the extra dword stays inside
         load_dwords<17>(a + 64 * h, r);            // ql half
         load_dwords<9>(a + 128 + 32 * h, r + 17);  // qh half
-        // scales and d sit at the end of the block: read exactly the bytes needed
-        if (sh) {
-            load_dwords<3>(a + 192 + 8 * h, r + 26);
-        } else {
-            load_dwords<2>(b + 192 + 8 * h, r + 26);
-            r[28] = 0;
-        }
+        // scales and d sit at the end of the block: read no byte past it.  The third scale dword
+        // is needed only when sh = 2; with sh = 0 it re-reads the second (and is shifted out).
+        const uint32_t* sc = reinterpret_cast<const uint32_t*>(a + 192 + 8 * h);
+        r[26] = sc[0];
+        r[27] = sc[1];
+        r[28] = sc[sh ? 2 : 1];
         r[29] = *reinterpret_cast<const uint16_t*>(b + 208);
-        if (sh) {
+        r[30] = (uint32_t)sh;
+    }
+    // alignbyte with shift 0 returns its low operand: the same code serves both alignments
+    __device__ static void realign(const uint32_t* r, uint32_t* q) {
+        const uint32_t sh = r[30];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) r[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], sh);
+        for (int i = 0; i < 16; ++i) q[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], sh);
 #pragma unroll
-            for (int i = 17; i < 25; ++i) r[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], sh);
-            r[26] = __builtin_amdgcn_alignbyte(r[27], r[26], sh);
-            r[27] = __builtin_amdgcn_alignbyte(r[28], r[27], sh);
-        }
+        for (int i = 17; i < 25; ++i) q[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], sh);
+        q[26] = __builtin_amdgcn_alignbyte(r[27], r[26], sh);
+        q[27] = __builtin_amdgcn_alignbyte(r[28], r[27], sh);
+        q[29] = r[29];
     }
     // ql dword j: low nibbles -> values 4j..4j+3, high nibbles -> 64 + 4j..; natural pairing (x0,x2),(x1,x3)
     __device__ static void prep_x(const uint32_t* xn, uint32_t* xp, float* xs) {
@@ -346,7 +354,9 @@ template <> struct GV<gguf::Q6_K> {
             xs[g] = s;
         }
     }
-    __device__ static float dot(const uint32_t* r, int, const uint32_t* xp, const float* xs) {
+    __device__ static float dot(const uint32_t* raw, int, const uint32_t* xp, const float* xs) {
+        uint32_t r[30];
+        realign(raw, r);
         const float d = f16_bits_to_f32((uint16_t)(r[29] & 0xFFFFu));
         float S[8];
 #pragma unroll
@@ -388,7 +398,12 @@ __device__ __forceinline__ uint32_t table_entry(int b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (f16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (f16)hi) << 16);
 }
 
-// LPR lanes per row (a power of two <= 64); RPW rows per wave.
+// LPR lanes per row (a power of two <= 64); RPP = 64 / LPR rows per pass of a wave.
+// Order of work: the activation row (coalesced), then each wave's weight chunks for two passes --
+// so every load is in flight before the first wait -- then the LDS staging of the activations
+// (and the table, for formats with one) and the prep of the activation pairs while the weights
+// arrive.  No load sits behind a lane-dependent branch: rows past N re-read row N - 1 and are
+// not stored.
 template <int T, int LPR>
 __global__ __launch_bounds__(GV_THREADS) void gguf_gemv_kernel(const f16* __restrict__ x, const int32_t* __restrict__ xexp,
                                                                const uint8_t* __restrict__ w,
@@ -398,53 +413,89 @@ __global__ __launch_bounds__(GV_THREADS) void gguf_gemv_kernel(const f16* __rest
     using F = GV<T>;
     constexpr int VC = F::VC;
     constexpr int RPP = 64 / LPR;  // rows per pass of a wave
-    __shared__ __attribute__((aligned(16))) uint32_t xs_lds[8192 / 2];
-    __shared__ uint32_t tab[256];
+    constexpr int NU = VC / 8;     // 16-byte activation units per chunk
+    __shared__ uint32_t tab_all[F::LUT ? GV_THREADS / 64 : 1][F::LUT ? 256 : 1];
+    __shared__ __attribute__((aligned(16))) u32x4 xs_lds[GV_MAX_K / 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if constexpr (F::LUT) tab[tid] = table_entry<T>(tid);
-    // stage x (K fp16) in LDS
-    for (int i = tid; i < K / 8; i += GV_THREADS)
-        reinterpret_cast<u32x4*>(xs_lds)[i] = reinterpret_cast<const u32x4*>(x)[i];
-    __syncthreads();
     const int c = lane % LPR, rp = lane / LPR;
+
+    const int waves_total = gridDim.x * (GV_THREADS / 64);
+    const int gw = blockIdx.x * (GV_THREADS / 64) + wave;
+    const int passes = (N + RPP - 1) / RPP;
+    const int KU = K / 8;
+
+    // 1. the activation row, with fully coalesced loads (consecutive lanes, consecutive 16 bytes).
+    //    Without branches: units past the row re-read (and below re-write) its last unit.
+    u32x4 xst[GV_MAX_K / 8 / GV_THREADS];
+#pragma unroll
+    for (int j = 0; j < GV_MAX_K / 8 / GV_THREADS; ++j)
+        xst[j] = reinterpret_cast<const u32x4*>(x)[min(tid + GV_THREADS * j, KU - 1)];
+    // 2. the weight chunks of this wave's first two passes (rows past N re-read row N - 1)
+    auto row_of = [&](int p) { return min(p * RPP + rp, N - 1); };
+    int p = gw;
+    uint32_t r0[F::LD], r1[F::LD];
+    __builtin_amdgcn_sched_barrier(0);
+    F::load(w + (int64_t)row_of(p) * row_bytes, c, r0);
+    F::load(w + (int64_t)row_of(p + waves_total) * row_bytes, c, r1);
+    // epilogue operands, fetched now rather than after the reduction
+    const int xe = xexp ? xexp[0] : 0;
+    uint32_t bv0 = 0, bv1 = 0;  // raw bits (0 reads as +0 in every dtype)
+    if (bias) {
+        bv0 = load_bits_rt(bias, bias_dt, row_of(p));
+        bv1 = load_bits_rt(bias, bias_dt, row_of(p + waves_total));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. activations into LDS: unit i of chunk c at i * LPR + (c ^ i), so that the per-lane reads
+    //    below (fixed i, consecutive c) and these writes both spread over the banks.  The fences
+    //    order LDS only: the weight loads stay in flight across the barrier.
+#pragma unroll
+    for (int j = 0; j < GV_MAX_K / 8 / GV_THREADS; ++j) {
+        const int u = min(tid + GV_THREADS * j, KU - 1);
+        const int cc = u / NU, i = u % NU;
+        xs_lds[i * LPR + (cc ^ i)] = xst[j];
+    }
+    uint32_t* tab = tab_all[F::LUT ? wave : 0];
+    if constexpr (F::LUT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tab[lane + 64 * i] = table_entry<T>(lane + 64 * i);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_sched_barrier(0);  // nothing that needs a weight value moves above this point
     uint32_t xn[VC / 2];
 #pragma unroll
-    for (int i = 0; i < VC / 8; ++i) {
-        const u32x4 v = reinterpret_cast<const u32x4*>(xs_lds)[(c * VC) / 8 + i];
+    for (int i = 0; i < NU; ++i) {
+        const u32x4 v = xs_lds[i * LPR + (c ^ i)];
         xn[4 * i] = v.x; xn[4 * i + 1] = v.y; xn[4 * i + 2] = v.z; xn[4 * i + 3] = v.w;
     }
     uint32_t xp[F::XP];
     float xsum[F::NG];
     F::prep_x(xn, xp, xsum);
 
-    const int waves_total = gridDim.x * (GV_THREADS / 64);
-    const int gw = blockIdx.x * (GV_THREADS / 64) + wave;
-    const int passes = (N + RPP - 1) / RPP;
-    // each wave takes passes gw, gw + W, gw + 2W, ... (W = waves in the grid), two at a time:
-    // both passes' loads are issued before either is computed
-    auto finish = [&](const uint32_t* r, int p) {
-        const int n = p * RPP + rp;
-        float v = 0.0f;
-        if (n < N) {
-            if constexpr (F::LUT) v = F::dot(r, c, xp, xsum, tab);
-            else v = F::dot(r, c, xp, xsum);
-        }
+    auto finish = [&](const uint32_t* r, int pp, uint32_t bv) {
+        const int n = pp * RPP + rp;
+        float v;
+        if constexpr (F::LUT) v = F::dot(r, c, xp, xsum, tab);
+        else v = F::dot(r, c, xp, xsum);
 #pragma unroll
         for (int m = 1; m < LPR; m <<= 1) v += __shfl_xor(v, m, 64);
-        if (c == 0 && n < N) {
-            if (xexp) v = __builtin_ldexpf(v, xexp[0]);
-            if (bias) v += load_rt(bias, bias_dt, n);
-            store_rt(y, y_dt, n, v);
-        }
+        if (c == 0 && n < N) store_rt(y, y_dt, n, __builtin_ldexpf(v, xe) + bits_to_f32_rt(bv, bias_dt));
     };
-    for (int p = gw; p < passes; p += 2 * waves_total) {
-        const int p2 = p + waves_total;
-        uint32_t r0[F::LD], r1[F::LD];
-        const int n0 = p * RPP + rp, n1 = p2 * RPP + rp;
-        if (n0 < N) F::load(w + (int64_t)n0 * row_bytes, c, r0);
-        if (p2 < passes && n1 < N) F::load(w + (int64_t)n1 * row_bytes, c, r1);
-        finish(r0, p);
-        if (p2 < passes) finish(r1, p2);
+    // The first two passes are computed unconditionally (their stores are guarded), so their
+    // loads are not moved into a branch behind the barrier; the launch normally sizes the grid so
+    // that they are all there is.
+    for (;;) {
+        finish(r0, p, bv0);
+        finish(r1, p + waves_total, bv1);
+        p += 2 * waves_total;
+        if (p >= passes) break;
+        F::load(w + (int64_t)row_of(p) * row_bytes, c, r0);
+        F::load(w + (int64_t)row_of(p + waves_total) * row_bytes, c, r1);
+        if (bias) {
+            bv0 = load_bits_rt(bias, bias_dt, row_of(p));
+            bv1 = load_bits_rt(bias, bias_dt, row_of(p + waves_total));
+        }
     }
 }
 
@@ -489,7 +540,7 @@ bool dispatch_gemv(int t, Fn&& f) {
 }  // namespace
 
 bool gguf_gemv_supported(int type, int64_t M, int64_t K, int64_t row_bytes, const void* w, const void* x) {
-    if (M != 1 || K > 8192 || (uintptr_t)w % 4 || (uintptr_t)x % 16 || row_bytes % 4) return false;
+    if (M != 1 || K > GV_MAX_K || (uintptr_t)w % 4 || (uintptr_t)x % 16 || row_bytes % 4) return false;
     bool ok = false;
     dispatch_gemv(type, [&]<int T>() {
         const int64_t vc = GV<T>::VC;

@@ -2,9 +2,11 @@
 //
 // Grid: one 512-thread workgroup (8 waves) per 16 weight rows n; the K range is split across the
 // 8 waves in stages (256 values, or 512 for the 210/110-byte K-quant blocks), and the partial sums
-// are reduced through LDS at the end.  Each wave issues the loads of its whole K slice up front
-// (16-, 8- or 4-byte units as the block size allows), parks them in registers, and per stage
-// copies them into its own LDS region.  From there every lane decodes the MFMA B operand for
+// are reduced through LDS at the end.  Each wave keeps one or two stages of weight loads in
+// flight (16-, 8- or 4-byte units as the block size allows) and, separately, the activation
+// fragments of the next D scale units; no load sits behind a lane-dependent branch, so the
+// memory latencies overlap instead of adding up.  Per stage a wave copies its weight registers
+// into its own LDS region and refills them with the stage PF ahead.  From there every lane decodes the MFMA B operand for
 // (row n = lane % 16, k slice lane / 16) as EXACT small integers in fp16 -- nibbles become
 // 1024 + q through v_perm_b32 with 0x64 exponent bytes -- and runs v_mfma_f32_16x16x{32,16}_f16
 // against the fp16 activations.  Scales stay in fp32:
@@ -268,16 +270,10 @@ template <> struct SM<gguf::Q3_K> {
     }
 };
 
-template <int VPL>
-__device__ __forceinline__ typename FragT<VPL>::type load_x(const f16* __restrict__ x, int64_t ldx, int m, int M,
-                                                            int64_t k) {
-    typedef typename FragT<VPL>::type V;
-    if (m >= M) return V{};
-    return *reinterpret_cast<const V*>(x + (int64_t)m * ldx + k);
-}
+constexpr int pow2_floor(int v) { return v >= 2 ? 2 * pow2_floor(v / 2) : 1; }
 
 // --------------------------------------------------------------------------------------------
-template <int T, int MT, int W>
+template <int T, int MT>
 __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
     const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K,
@@ -287,15 +283,22 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     constexpr int SV = SBLK * QK;                    // values per stage
     constexpr int RSB = SBLK * TS;                   // stage bytes per row
     constexpr int RS = ((RSB + 15) / 16) * 16 + 16;  // LDS row stride (padded for over-reads)
-    static_assert(RSB % W == 0, "stage bytes must be whole load units");
-    constexpr int UPR = RSB / W;                     // load units per row
+    static_assert(RSB % 4 == 0 && RSB >= 16, "stage rows must be whole dwords");
+    // 16-byte load units (dword alignment suffices); a row's last unit ends at the row's last
+    // byte and may overlap the one before it
+    constexpr int UPR = (RSB + 15) / 16;             // load units per row
     constexpr int UNITS = 16 * UPR;                  // load units per stage
     constexpr int NPF = (UNITS + 63) / 64;           // load units per lane per stage
     // stages held in registers: two when a stage is small, else one (register pressure)
     constexpr int PF = (NPF <= 12 && MT <= 2) ? 2 : 1;
     constexpr int UPS = SV / UNIT;                   // scale units per stage
+    constexpr int UPB = QK / UNIT;                   // scale units per block
+    // activation fragments in flight: D units ahead of the MFMAs (at most 64 VGPRs of them)
+    constexpr int XV = MT * VPL / 2;
+    constexpr int D = (UPS * XV <= 64) ? UPS : pow2_floor(64 / XV);
+    static_assert(D >= 1 && UPS % D == 0, "x prefetch depth must divide the stage");
     typedef typename FragT<VPL>::type V;
-    typedef typename std::conditional<W == 16, u32x4, typename std::conditional<W == 8, u32x2, uint32_t>::type>::type LU;
+    typedef uint32_t LU __attribute__((ext_vector_type(4), aligned(4)));
 
     constexpr int STAGE_BYTES = SM_WAVES * 16 * RS;
     constexpr int RED_BYTES = SM_WAVES * MT * 4 * 64 * 4;
@@ -311,23 +314,27 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     // rows of the 4 outputs this lane holds per m-tile: 4*g + i; skip FMAs for rows past M when M <= 4
     const int ilim = (MT == 1 && M < 4) ? M : 4;
 
+    // No load below branches on the lane: activation rows past M re-read row M - 1 and weight rows
+    // past N re-read row N - 1 (their results are never stored); stages past this wave's range
+    // re-read its last stage (never committed).
+    const f16* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = x + (int64_t)min(mt * 16 + nl, M - 1) * ldx + VPL * g;
+    const int last = st1 - 1;
+
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     LU pf[PF][NPF];
     auto issue = [&](int st, LU* buf) {
+        st = min(st, last);
 #pragma unroll
         for (int i = 0; i < NPF; ++i) {
-            const int u = lane + 64 * i;
-            LU v{};
-            if (u < UNITS) {
-                const int r = u / UPR;
-                const int off = (u - r * UPR) * W;
-                if (n0 + r < N)
-                    v = *reinterpret_cast<const LU*>(w + (int64_t)(n0 + r) * row_bytes + (int64_t)st * RSB + off);
-            }
-            buf[i] = v;
+            const int u = (UNITS % 64 == 0) ? lane + 64 * i : min(lane + 64 * i, UNITS - 1);
+            const int r = u / UPR;
+            const int off = min((u - r * UPR) * 16, RSB - 16);
+            buf[i] = *reinterpret_cast<const LU*>(w + (int64_t)min(n0 + r, N - 1) * row_bytes + (int64_t)st * RSB + off);
         }
     };
     auto commit = [&](const LU* buf) {
@@ -336,98 +343,109 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
             const int u = lane + 64 * i;
             if (u < UNITS) {
                 const int r = u / UPR;
-                const int off = (u - r * UPR) * W;
+                const int off = min((u - r * UPR) * 16, RSB - 16);
                 *reinterpret_cast<LU*>(my + r * RS + off) = buf[i];
             }
         }
+    };
+    V xr[D][MT];
+    auto load_xu = [&](int st, int u, V* dst) {
+        const int64_t k = (int64_t)min(st, last) * SV + u * UNIT;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) dst[mt] = *reinterpret_cast<const V*>(xrow[mt] + k);
     };
 
     V ones;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) ones[i] = (f16)1.0f;
 
-    for (int c0 = st0; c0 < st1; c0 += PF) {
+    if (st0 < st1) {
+        // first stage's weights, its first D activation units, then the other prefetched stages
+        issue(st0, pf[0]);
 #pragma unroll
-        for (int j = 0; j < PF; ++j)
-            if (c0 + j < st1) issue(c0 + j, pf[j]);
+        for (int d = 0; d < D; ++d) load_xu(st0, d, xr[d]);
 #pragma unroll
-        for (int j = 0; j < PF; ++j) {
-            const int st = c0 + j;
-            if (st >= st1) break;
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            commit(pf[j]);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const uint8_t* srow = my + nl * RS;
-            const int64_t kst = (int64_t)st * SV;
-            if constexpr (F::KIND == 0) {
-                auto unit = [&](int u) {
-                    const int blk = (u * UNIT) / QK;
-                    const int v0 = (u * UNIT) % QK + VPL * g;
-                    float a, b;
-                    const V bf = F::get(srow, blk * TS, v0, a, b);
-                    const int64_t k = kst + u * UNIT + VPL * g;
+        for (int j = 1; j < PF; ++j) issue(st0 + j, pf[j]);
+
+        for (int c0 = st0; c0 < st1; c0 += PF) {
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const V af = load_x<VPL>(x, ldx, mt * 16 + nl, M, k);
-                        const f32x4 c = mfma16<VPL>(af, bf, f32x4{0.f, 0.f, 0.f, 0.f});
-                        if constexpr (F::MIN) {
-                            const f32x4 c1 = mfma16<VPL>(af, ones, f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                if (i < ilim) acc[mt][i] += a * c[i] + b * c1[i];
-                        } else {
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                if (i < ilim) acc[mt][i] += a * c[i];
-                        }
-                    }
+            for (int j = 0; j < PF; ++j) {
+                const int st = c0 + j;
+                if (st >= st1) break;
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                commit(pf[j]);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                issue(st + PF, pf[j]);  // refill the freed registers with the stage PF ahead
+                const uint8_t* srow = my + nl * RS;
+                // unit u's activations sit in xr[u % D]; once used, the slot takes unit u + D
+                auto next_x = [&](int u) {
+                    if (u + D < UPS) load_xu(st, u + D, xr[u % D]);
+                    else load_xu(st + 1, u + D - UPS, xr[u % D]);
                 };
-                if constexpr (MT == 1) {
+                if constexpr (F::KIND == 0) {
 #pragma unroll
-                    for (int u = 0; u < UPS; ++u) unit(u);
-                } else {
-#pragma unroll 2
-                    for (int u = 0; u < UPS; ++u) unit(u);
-                }
-            } else {
-                constexpr int UPB = QK / UNIT;  // units per block
-#pragma unroll
-                for (int blk = 0; blk < SBLK; ++blk) {
-                    f32x4 c1[MT], c2[MT];
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        c1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                        c2[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    }
-#pragma unroll
-                    for (int ub = 0; ub < UPB; ++ub) {
-                        const int v0 = ub * UNIT + VPL * g;
-                        f16 mv;
-                        const V bf = F::get(srow, blk * TS, v0, mv);
-                        V bm;
-#pragma unroll
-                        for (int i = 0; i < VPL; ++i) bm[i] = mv;
-                        const int64_t k = kst + blk * QK + v0;
+                    for (int u = 0; u < UPS; ++u) {
+                        const int blk = (u * UNIT) / QK;
+                        const int v0 = (u * UNIT) % QK + VPL * g;
+                        float a, b;
+                        const V bf = F::get(srow, blk * TS, v0, a, b);
 #pragma unroll
                         for (int mt = 0; mt < MT; ++mt) {
-                            const V af = load_x<VPL>(x, ldx, mt * 16 + nl, M, k);
-                            c1[mt] = mfma16<VPL>(af, bf, c1[mt]);
-                            if constexpr (F::MIN) c2[mt] = mfma16<VPL>(af, bm, c2[mt]);
-                        }
-                    }
-                    float d, dmin;
-                    F::block(srow, blk * TS, d, dmin);
+                            const V af = xr[u % D][mt];
+                            const f32x4 c = mfma16<VPL>(af, bf, f32x4{0.f, 0.f, 0.f, 0.f});
+                            if constexpr (F::MIN) {
+                                const f32x4 c1 = mfma16<VPL>(af, ones, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
+                                for (int i = 0; i < 4; ++i)
+                                    if (i < ilim) acc[mt][i] += a * c[i] + b * c1[i];
+                            } else {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (i < ilim) {
-                                acc[mt][i] += d * c1[mt][i];
-                                if constexpr (F::MIN) acc[mt][i] -= dmin * c2[mt][i];
+                                for (int i = 0; i < 4; ++i)
+                                    if (i < ilim) acc[mt][i] += a * c[i];
                             }
+                        }
+                        next_x(u);
+                    }
+                } else {
+#pragma unroll
+                    for (int blk = 0; blk < SBLK; ++blk) {
+                        f32x4 c1[MT], c2[MT];
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            c1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                            c2[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                        }
+#pragma unroll
+                        for (int ub = 0; ub < UPB; ++ub) {
+                            const int u = blk * UPB + ub;
+                            const int v0 = ub * UNIT + VPL * g;
+                            f16 mv;
+                            const V bf = F::get(srow, blk * TS, v0, mv);
+                            V bm;
+#pragma unroll
+                            for (int i = 0; i < VPL; ++i) bm[i] = mv;
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) {
+                                const V af = xr[u % D][mt];
+                                c1[mt] = mfma16<VPL>(af, bf, c1[mt]);
+                                if constexpr (F::MIN) c2[mt] = mfma16<VPL>(af, bm, c2[mt]);
+                            }
+                            next_x(u);
+                        }
+                        float d, dmin;
+                        F::block(srow, blk * TS, d, dmin);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                if (i < ilim) {
+                                    acc[mt][i] += d * c1[mt][i];
+                                    if constexpr (F::MIN) acc[mt][i] -= dmin * c2[mt][i];
+                                }
+                    }
                 }
             }
         }
@@ -455,33 +473,19 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     }
 }
 
-// Widest load unit dividing the stage row (16, 8 or 4 bytes).
-template <int T>
-constexpr int best_width() {
-    constexpr int RSB = SM<T>::SBLK * SM<T>::TS;
-    return RSB % 16 == 0 ? 16 : (RSB % 8 == 0 ? 8 : 4);
-}
-
 template <int T>
 hipError_t launch_t(const GgufSmallMArgs& a, hipStream_t st) {
     dim3 grid((unsigned)((a.N + 15) / 16)), block(SM_THREADS);
-    const int mt = (a.M + 15) / 16;
-    constexpr int WB = best_width<T>();
-    const bool wide = (a.row_bytes % WB == 0) && ((uintptr_t)a.w % WB == 0);
-#define QLIN_SM_LAUNCH(MTV, WV)                                                                             \
-    hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV, WV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
+#define QLIN_SM_LAUNCH(MTV)                                                                               \
+    hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
                        a.row_bytes, a.N, a.K, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy)
-#define QLIN_SM_W(MTV)                \
-    if (wide) QLIN_SM_LAUNCH(MTV, WB); \
-    else QLIN_SM_LAUNCH(MTV, 4);
-    switch (mt) {
-        case 1: QLIN_SM_W(1); break;
-        case 2: QLIN_SM_W(2); break;
-        case 3: QLIN_SM_W(3); break;
-        case 4: QLIN_SM_W(4); break;
+    switch ((a.M + 15) / 16) {
+        case 1: QLIN_SM_LAUNCH(1); break;
+        case 2: QLIN_SM_LAUNCH(2); break;
+        case 3: QLIN_SM_LAUNCH(3); break;
+        case 4: QLIN_SM_LAUNCH(4); break;
         default: return hipErrorInvalidValue;
     }
-#undef QLIN_SM_W
 #undef QLIN_SM_LAUNCH
     return hipGetLastError();
 }

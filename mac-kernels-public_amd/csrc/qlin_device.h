@@ -163,6 +163,18 @@ __device__ __forceinline__ float load_rt(const void* base, int dtype, int64_t id
     return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[idx]);
 }
 
+// Raw bits of element idx (for an early load whose conversion happens at the point of use:
+// keeps the load from waiting on everything issued before it).
+__device__ __forceinline__ uint32_t load_bits_rt(const void* base, int dtype, int64_t idx) {
+    if (dtype == 0) return reinterpret_cast<const uint32_t*>(base)[idx];
+    return reinterpret_cast<const uint16_t*>(base)[idx];
+}
+__device__ __forceinline__ float bits_to_f32_rt(uint32_t bits, int dtype) {
+    if (dtype == 0) return __uint_as_float(bits);
+    if (dtype == 1) return f16_bits_to_f32((uint16_t)bits);
+    return bf16_bits_to_f32((uint16_t)bits);
+}
+
 __device__ __forceinline__ float load_f(const float* p) { return *p; }
 __device__ __forceinline__ float load_f(const f16* p) { return (float)*p; }
 __device__ __forceinline__ float load_f(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
