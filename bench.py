@@ -8,7 +8,9 @@ weight from a pool of >= 1 GiB (4x the 256 MiB Infinity Cache) so the bytes come
 steps are captured once in a HIP graph and replayed, so launch overhead from Python is not timed.
 
 value = whole-step algorithmic bytes (packed weights + fp16 x + fp16 y) / step time, in GB/s.
-roofline: the same per launch against the 8 TB/s HBM peak.
+roofline: the kernel with the largest share of the step (by time), its algorithmic bytes per launch over
+its average launch duration (HIP events around graph replays of that call alone), against the 8 TB/s
+HBM peak; `traffic` is its measured HBM bytes per launch from the committed counter summary.
 cpu_baseline: the oracle's dequantize-then-matmul on the host (C decode, fp32 BLAS matmul).
 
 Other suites (--suite int8|w4a8|w6a8|dit|all) print their own JSON lines to stderr.
@@ -40,14 +42,21 @@ def gguf_bytes(name, n, k):
     return n * (k // qk) * ts
 
 
-def make_gguf_weights(name, n, k, copies, seed=0):
+def quantized_base(name, n, k, seed=0):
+    """One N(0, 0.02) weight quantized on the host to GGUF `name` (uint8 [n, row_bytes])."""
+    import torch
+    from qlin.quantize import quantize_gguf
+    base = (torch.randn(n, k, generator=torch.Generator().manual_seed(seed)) * 0.02).numpy()
+    return torch.from_numpy(quantize_gguf(base, name))
+
+
+def make_gguf_weights(name, n, k, copies, seed=0, raw=None):
     """`copies` independent weights of one type (quantized on the host, then resident on the GPU)."""
     import numpy as np
     import torch
-    from qlin.quantize import quantize_gguf
     out = []
-    base = (torch.randn(n, k, generator=torch.Generator().manual_seed(seed)) * 0.02).numpy()
-    raw = torch.from_numpy(quantize_gguf(base, name))
+    if raw is None:
+        raw = quantized_base(name, n, k, seed)
     for c in range(copies):
         # distinct bytes per copy: permute the block rows (still valid blocks) so no two copies alias
         perm = torch.from_numpy(np.random.default_rng(seed + 100 + c).permutation(n))
@@ -88,7 +97,8 @@ def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
     per_step_bytes = sum(gguf_bytes(t, n, k) for t in GGUF_SUITE) * len(ms)
     copies = max(1, -(-POOL_BYTES // per_step_bytes))
     log(f"[gguf] building pool: {copies} copies x {per_step_bytes / 2**20:.0f} MiB per step")
-    weights = {t: make_gguf_weights(t, n, k, copies * len(ms), seed=i) for i, t in enumerate(GGUF_SUITE)}
+    bases = {t: quantized_base(t, n, k, seed=i) for i, t in enumerate(GGUF_SUITE)}
+    weights = {t: make_gguf_weights(t, n, k, copies * len(ms), seed=i, raw=bases[t]) for i, t in enumerate(GGUF_SUITE)}
     g = torch.Generator().manual_seed(1)
     xs = {m: torch.randn(m, k, generator=g).half().cuda() for m in ms}
     calls = []
@@ -109,20 +119,22 @@ def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
     flops = sum(2 * m * n * k for _ in GGUF_SUITE for m in ms)
     gbs = alg_bytes / (ms_step * 1e-3) / 1e9
 
-    # per (type, M): graph of the same call over `copies` pool copies
+    # per (type, M): a graph of the same call over its own >= 1 GiB pool of that weight, so that
+    # every launch reads HBM (a few copies would sit in the 256 MiB Infinity Cache)
+    del weights
     detail = {}
-    for t in GGUF_SUITE:
+    for i, t in enumerate(GGUF_SUITE):
+        nc = -(-POOL_BYTES // gguf_bytes(t, n, k))
+        ws = make_gguf_weights(t, n, k, nc, seed=i, raw=bases[t])
         for j, m in enumerate(ms):
-            ws = [weights[t][c * len(ms) + j] for c in range(copies)]
-
             def one(ws=ws, m=m, t=t):
                 for w in ws:
                     qlin.gguf_linear(xs[m], w, tid[t], (n, k))
 
-            msr, _ = time_graph(one, 20, 3)
-            us = msr / copies * 1e3
+            msr, _ = time_graph(one, 10, 2)
+            us = msr / nc * 1e3
             b = gguf_bytes(t, n, k) + m * k * 2 + m * n * 2
-            detail[f"{t}/M{m}"] = {"us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+            detail[f"{t}/M{m}"] = {"us": round(us, 2), "bytes": b, "GBps": round(b / (us * 1e-6) / 1e9, 1),
                                    "TFLOPs": round(2 * m * n * k / (us * 1e-6) / 1e12, 2)}
             log(f"[gguf] {t:7s} M={m:3d}: {us:7.2f} us  {detail[f'{t}/M{m}']['GBps']:8.1f} GB/s")
     return {
@@ -175,6 +187,65 @@ def cpu_baseline_gguf(n=4096, k=4096, ms=(1, 8, 64), rows=None):
         "decode_ms": round(dec_s * 1e3, 1), "matmul_ms": round(mm_s * 1e3, 1), "cpu_model": cpu_model,
         "decode_threads": 1,
     }
+
+
+def kernel_of(m):
+    """Kernel that serves a K=N=4096 GGUF call with M activation rows (the dispatch in the C ABI)."""
+    return "gguf_gemv_kernel" if m == 1 else "gguf_smallm_kernel"
+
+
+def kernel_breakdown(detail):
+    """Per kernel: launches, algorithmic bytes per launch and the average launch duration, from the
+    per-(type, M) graph timings (HIP events on the replay stream)."""
+    out = {}
+    for key, d in detail.items():
+        t, m = key.split("/M")
+        k = kernel_of(int(m))
+        e = out.setdefault(k, {"launches": 0, "bytes": 0, "us_total": 0.0})
+        e["launches"] += 1
+        e["bytes"] += d["bytes"]
+        e["us_total"] += d["us"]
+    for k, e in out.items():
+        e["bytes_per_launch"] = round(e["bytes"] / e["launches"])
+        e["us_per_launch"] = round(e["us_total"] / e["launches"], 3)
+        e["GBps"] = round(e["bytes"] / (e["us_total"] * 1e-6) / 1e9, 1)
+        e["us_total"] = round(e["us_total"], 2)
+        del e["bytes"]
+    return out
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary
+    (counter runs cannot happen inside the timed process); None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", "gguf_linear_k4096_counters.md")
+    try:
+        for line in open(path):
+            if line.startswith(f"traffic {kernel} "):
+                return int(line.split()[2])
+    except OSError:
+        pass
+    return None
+
+
+def profile_pass(n=4096, k=4096, ms=(1, 8, 64), reps=3):
+    """Eager launches for counter collection (each dispatch is profiled on its own)."""
+    import torch
+    import qlin
+    weights = {t: make_gguf_weights(t, n, k, reps * len(ms), seed=i) for i, t in enumerate(GGUF_SUITE)}
+    g = torch.Generator().manual_seed(1)
+    xs = {m: torch.randn(m, k, generator=g).half().cuda() for m in ms}
+    for t in GGUF_SUITE:
+        tid = qlin.GGUF_TYPES[t][0]
+        for j, m in enumerate(ms):
+            for r in range(reps):
+                qlin.gguf_linear(xs[m], weights[t][r * len(ms) + j], tid, (n, k))
+    # reference kernel of known traffic: an elementwise pass reading and writing 64 MiB each
+    src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    log("[profile] done")
 
 
 def other_suites(which, steps, warmup):
@@ -261,10 +332,14 @@ def main():
     ap.add_argument("--suite", default="gguf", choices=["gguf", "int8", "w4a8", "w6a8", "dit", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=1024, help="weight rows decoded per call for the CPU baseline")
+    ap.add_argument("--profile", action="store_true",
+                    help="eager launches for rocprofv3 counter runs (no timing, no JSON): each GGUF call three "
+                         "times on distinct weights, then a 64 MiB device copy as the byte-counter reference")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
-              "(the path shards by weight rows with no exchange, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported: the linear shards by weight "
+              "rows with no exchange between GPUs, so one GPU's throughput is the figure of merit",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     import qlin  # noqa: F401
@@ -272,14 +347,17 @@ def main():
     _lib.load()
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
 
+    if a.profile:
+        profile_pass()
+        return
     if a.suite != "gguf":
         other_suites(a.suite, a.steps, a.warmup)
         if a.suite != "all":
             return
     r = suite_gguf(a.steps, a.warmup)
-    per_launch_bytes = r["alg_bytes"] / r["launches"]
-    per_launch_s = r["ms_per_step"] * 1e-3 / r["launches"]
-    achieved = per_launch_bytes / per_launch_s / 1e9
+    kernels = kernel_breakdown(r["detail"])
+    dom = max(kernels, key=lambda k: kernels[k]["us_total"])
+    dk = kernels[dom]
     line = {
         "metric": METRIC,
         "value": round(r["value"], 1),
@@ -300,11 +378,13 @@ def main():
             "tflops_step": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 3),
         },
         "roofline": {
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gguf_smallm_kernel (all 21 launches of the step, averaged)",
-            "bytes_per_launch": round(per_launch_bytes), "us_per_launch": round(per_launch_s * 1e6, 3),
+            "bound": "hbm", "achieved": dk["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dk["GBps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
+            "kernel": dom, "launches": dk["launches"],
+            "bytes_per_launch": dk["bytes_per_launch"], "us_per_launch": dk["us_per_launch"],
+            "step_GBps": round(r["value"], 1),
         },
+        "kernels": kernels,
         "detail": r["detail"],
     }
     if not a.no_cpu:

@@ -4,8 +4,9 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``b
 import this package.  It restates the reference's codecs (roblennon/mac-kernels-public,
 ``modal/weight_error_app.py:88-339``, ``modal/modal_app.py:30-50``,
 ``docs/research/2026-10-03-gguf-on-metal.md:18-36``) in plain C (``qlin_oracle.c``, built by
-``oracle/Makefile`` into ``liboracle_qlin.so``) with numpy wrappers, plus numpy quantizers that
-generate packed inputs (``quantizers.py``).
+``oracle/Makefile`` into ``liboracle_qlin.so``) with numpy wrappers.  The quantizers that make packed
+test inputs live in the product's host layer (``qlin/quantize.py``) and are pinned by the same golden
+vectors.
 
 Parity pins (checked in tests/test_oracle_*.py):
   * GGUF Q8_0 / Q4_K decode ........ reference golden deq sha256 (bit-exact)
