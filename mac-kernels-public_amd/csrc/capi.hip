@@ -5,7 +5,7 @@
 #include <cstring>
 #include <string>
 
-#include "../../include/qlin.h"
+#include "qlin.h"
 #include "hadamard.h"
 #include "gguf_exact.h"
 #include "qlin_internal.h"
@@ -245,6 +245,9 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     return hip_status(run_gemm_f16(a, st), "int8 gemm");
 }
 
+// Largest M of the small-M GGUF kernel (the single-row VALU kernel takes M = 1 when it applies)
+constexpr int64_t GGUF_SMALLM_MAX_M = 64;
+
 qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                              const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
                              void* stream) {
@@ -283,7 +286,7 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
             return hip_status(run_gguf_gemv(g, st), "gguf gemv");
         }
     }
-    if (aligned && gguf_smallm_supported(ggml_type, M, K, row_bytes)) {
+    if (aligned && M <= GGUF_SMALLM_MAX_M && gguf_smallm_supported(ggml_type, M, K, row_bytes)) {
         GgufSmallMArgs a;
         a.type = ggml_type;
         int64_t ldx;

@@ -115,7 +115,7 @@ def test_dequantize_gguf_straddling_rows(name):
 # ------------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("name", GGUF)
-@pytest.mark.parametrize("m", [1, 8, 64, 100])
+@pytest.mark.parametrize("m", [1, 8, 16, 17, 64, 100, 128, 129])  # every kernel and each switch point
 def test_gguf_linear(name, m):
     n, k = 80, 1024
     raw = qz().random_gguf_blocks(name, n, k, seed=11)
@@ -129,7 +129,7 @@ def test_gguf_linear(name, m):
 
 @pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                      (torch.float32, torch.float32), (torch.float16, torch.float32)])
-@pytest.mark.parametrize("m", [3, 200])
+@pytest.mark.parametrize("m", [3, 40, 200])
 def test_gguf_linear_dtypes_and_bias(xdt, odt, m):
     name, n, k = "Q4_K", 96, 512
     raw = qz().random_gguf_blocks(name, n, k, seed=5)
