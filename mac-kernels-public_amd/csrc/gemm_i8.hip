@@ -22,6 +22,21 @@ struct Regs {
     u32x4 b[4];  // 64 decoded int8 of one weight row half
 };
 
+// Raw bits of s_rel[i] (converted at the point of use, so the load does not force an early wait)
+template <typename TSrel>
+__device__ __forceinline__ uint32_t srel_bits(const void* s, int64_t i) {
+    if constexpr (sizeof(TSrel) == 1) return ((const uint8_t*)s)[i];
+    else if constexpr (sizeof(TSrel) == 2) return ((const uint16_t*)s)[i];
+    else return ((const uint32_t*)s)[i];
+}
+template <typename TSrel>
+__device__ __forceinline__ float srel_from_bits(uint32_t b) {
+    if constexpr (sizeof(TSrel) == 1) return e4m3_to_f32((uint8_t)b);
+    else if constexpr (sizeof(TSrel) == 4) return __uint_as_float(b);
+    else if constexpr (__is_same(TSrel, bf16_t)) return bf16_bits_to_f32((uint16_t)b);
+    else return f16_bits_to_f32((uint16_t)b);
+}
+
 template <typename TSrel>
 __device__ __forceinline__ float srel_at(const void* s, int64_t i) {
     if constexpr (sizeof(TSrel) == 1) return e4m3_to_f32(((const uint8_t*)s)[i]);
@@ -194,9 +209,247 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
     }
 }
 
+
+// ------------------------------------------------------------------------------------------------
+// Large-tile A8 kernel: 512 threads, tile 256 x 256 x 128 (int8), waves 4 x 2 of 64 x 128 (two
+// waves per SIMD, so one wave's MFMAs cover the other's memory waits).
+// Each decoded weight value feeds 2 * BM MFMA ops, so the decode must stay near 2-4 VALU per value:
+//   * 4-bit codes (uniform or codebook): per weight row and k-tile one 16-entry int8 table
+//     T[c] = clamp(rne(level[c] * s), -127, 127), built by the two threads that decode the row,
+//     then two v_perm lookups (the low and high eight entries) and a byte select on bit 3 per four
+//     codes -- the same int8 grid as decode8_i8;
+//   * 6-bit codes: (c - 32) * s is exact in fp32 for fp16 / e4m3 / bf16 scales (a 6-bit integer
+//     times an 11-bit significand), so rint + one med3 clamp gives the grid value directly.
+// The next k-tile's loads are issued before the current tile's MFMAs and decoded after them in the
+// same basic block.  Requires K % 128 == 0 and group_size % 64 == 0 (one scale per 64-value half).
+// ------------------------------------------------------------------------------------------------
+
+// Byte-wise lookup of four 4-bit indices (one per byte) in a 16-byte table t0..t3.
+__device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t1, t0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t3, t2, sel);
+    const uint32_t m8 = idx & 0x08080808u;
+    const uint32_t mask = (m8 << 5) - (m8 >> 3);  // 0xFF in every byte whose index has bit 3
+    return (hi & mask) | (lo & ~mask);
+}
+
+__device__ __forceinline__ uint32_t grid_byte(float level, float s) {
+    const float t = __builtin_amdgcn_fmed3f(__builtin_rintf(level * s), -127.0f, 127.0f);
+    return (uint32_t)((int)t & 0xFF);
+}
+
+// 64 codes of one weight row (nibble dwords nib[0..7], 2-bit plane hi2[0..3] for 6-bit) -> 64
+// int8 grid values in out[0..15].  4-bit: a 16-entry table per scale.  When the thread pair that
+// shares the row also shares the scale (`pair`, wave-uniform), each builds half of it (entries
+// 8h .. 8h+7) and the halves are swapped with one lane shuffle; otherwise each builds all 16.
+template <int BITS, bool CB>
+__device__ __forceinline__ void decode64(const uint32_t* nib, const uint32_t* hi2, float s, const float* cb, int h,
+                                         bool pair, uint32_t* out) {
+#pragma clang fp contract(off)
+    if constexpr (BITS == 4) {
+        auto entries = [&](int c0) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int c = c0 + b;
+                const float level = CB ? cb[c] : (float)(c - 8);
+                v |= grid_byte(level, s) << (8 * b);
+            }
+            return v;
+        };
+        uint32_t t0, t1, t2, t3;
+        if (pair) {
+            const uint32_t mine0 = entries(8 * h), mine1 = entries(8 * h + 4);
+            const uint32_t other0 = (uint32_t)__shfl_xor((int)mine0, 1, 64);
+            const uint32_t other1 = (uint32_t)__shfl_xor((int)mine1, 1, 64);
+            t0 = h ? other0 : mine0; t1 = h ? other1 : mine1;
+            t2 = h ? mine0 : other0; t3 = h ? mine1 : other1;
+        } else {
+            t0 = entries(0); t1 = entries(4); t2 = entries(8); t3 = entries(12);
+        }
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {  // nibble dword d: codes 8d .. 8d+7
+            const uint32_t w = nib[d];
+            const uint32_t ev = lut16(w & 0x0F0F0F0Fu, t0, t1, t2, t3);         // codes 0, 2, 4, 6
+            const uint32_t od = lut16((w >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);  // codes 1, 3, 5, 7
+            out[2 * d] = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+            out[2 * d + 1] = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+        }
+    } else {
+        (void)h;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const uint32_t w = nib[d];
+            const uint32_t h16 = (hi2[d >> 1] >> (16 * (d & 1))) & 0xFFFFu;  // 2 bits per code
+            uint32_t o0 = 0, o1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int code = (int)(((w >> (4 * i)) & 0xFu) | (((h16 >> (2 * i)) & 3u) << 4));
+                const uint32_t bb = grid_byte((float)(code - 32), s);
+                if (i < 4) o0 |= bb << (8 * i);
+                else o1 |= bb << (8 * (i - 4));
+            }
+            out[2 * d] = o0;
+            out[2 * d + 1] = o1;
+        }
+    }
+}
+
+// Tile order for an 8-XCD part: block b runs on XCD b % 8, so each XCD is given a contiguous run
+// of the tile sequence, and the sequence walks groups of 4 M-tiles across all N-tiles.  Tiles
+// resident at the same time on one XCD then share activation and weight panels in its L2.
+__device__ __forceinline__ void xcd_tile(int b, int nblocks, int n_m, int n_n, int& mt, int& nt) {
+    constexpr int XCD = 8, GROUP_M = 4;
+    const int per = nblocks / XCD;  // the last nblocks % 8 blocks keep the plain order
+    const int t = b < XCD * per ? (b % XCD) * per + b / XCD : b;
+    const int group = t / (GROUP_M * n_n);
+    const int first_m = group * GROUP_M;
+    const int gm = min(n_m - first_m, GROUP_M);
+    mt = first_m + (t % (GROUP_M * n_n)) % gm;
+    nt = (t % (GROUP_M * n_n)) / gm;
+}
+
+// 512 threads = 8 waves, 4 (M) x 2 (N) of 64 x 128; tile 256 x 256 x 128 (int8).
+constexpr int BKA = 128, LDAA = BKA + 16;  // k-tile and LDS row stride (bytes)
+
+template <int BITS, bool CB, typename TSrel>
+__global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
+    constexpr int BMT = 256, BNT = 256, NT = 512;
+    constexpr int WM = 64, WN = 128, TI = WM / 16, TJ = WN / 16;
+    constexpr int NA = BMT * (BKA / 16) / NT;  // 16-byte activation units per thread and k-tile
+    constexpr int UA = BKA / 16;              // ... per activation row
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][BMT * LDAA];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BNT * LDAA];
+    __shared__ float cb_s[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, g = lane >> 4;
+    int mt, nt;
+    xcd_tile(blockIdx.x, (int)gridDim.x, (int)((p.M + BMT - 1) / BMT), (int)((p.N + BNT - 1) / BNT), mt, nt);
+    const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
+    const int ktiles = (int)(p.K / BKA);
+    if constexpr (CB) {
+        if (tid < 16) cb_s[tid] = p.codebook[tid];
+        __syncthreads();
+    }
+    const float* cb = CB ? cb_s : nullptr;
+
+    // weight row r = tid / 2 of the tile, codes 64h .. 64h+63 of each k-tile (rows past N re-read
+    // row N - 1 and are never stored)
+    const int br = tid >> 1, bh = tid & 1;
+    const int64_t nrow = min(n0 + br, p.N - 1);
+    const uint8_t* wrow = p.q + nrow * p.ldq;
+    // activation row pointers and the scale row do not change along K
+    const int8_t* arow[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int u = tid + NT * i;
+        arow[i] = p.xq + min(m0 + u / UA, p.M - 1) * p.ldx + 16 * (u % UA);
+    }
+    const int gsh = p.group_size / 64;  // 64-value halves per scale group
+    const void* srow = nullptr;
+    if constexpr (sizeof(TSrel) == 1) srow = (const uint8_t*)p.s_rel + nrow * p.ld_srel;
+    else srow = (const TSrel*)p.s_rel + nrow * p.ld_srel;
+
+    u32x4 ra[NA];
+    uint32_t rn[8], rh[4], rs;
+    auto fetch = [&](int kt) {
+        kt = min(kt, ktiles - 1);
+        const int k0 = kt * BKA;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
+        const uint8_t* pn = wrow + k0 / 2 + 32 * bh;
+        const u32x4 n_0 = *reinterpret_cast<const u32x4*>(pn), n_1 = *reinterpret_cast<const u32x4*>(pn + 16);
+        rn[0] = n_0.x; rn[1] = n_0.y; rn[2] = n_0.z; rn[3] = n_0.w;
+        rn[4] = n_1.x; rn[5] = n_1.y; rn[6] = n_1.z; rn[7] = n_1.w;
+        if constexpr (BITS == 6) {
+            const u32x4 hv = *reinterpret_cast<const u32x4*>(wrow + p.K / 2 + k0 / 4 + 16 * bh);
+            rh[0] = hv.x; rh[1] = hv.y; rh[2] = hv.z; rh[3] = hv.w;
+        }
+        rs = srel_bits<TSrel>(srow, (unsigned)(2 * kt + bh) / (unsigned)gsh);
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int u = tid + NT * i;
+            *reinterpret_cast<u32x4*>(&As[buf][(u / UA) * LDAA + 16 * (u % UA)]) = ra[i];
+        }
+        uint32_t o[16];
+        decode64<BITS, CB>(rn, rh, srel_from_bits<TSrel>(rs), cb, bh, gsh >= 2, o);
+        u32x4* pb = reinterpret_cast<u32x4*>(&Bs[buf][br * LDAA + 64 * bh]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pb[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+    };
+
+    i32x4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int buf = kt & 1;
+        fetch(kt + 1);  // clamped past the end: re-reads the last tile (staged into an unread buffer)
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
+        const uint8_t* as = &As[buf][(wm * WM + r16) * LDAA + 16 * g];
+        const uint8_t* bs = &Bs[buf][(wn * WN + r16) * LDAA + 16 * g];
+#pragma unroll
+        for (int kk = 0; kk < BKA / 64; ++kk) {
+            i32x4 bf[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bs + 16 * j * LDAA + 64 * kk);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const i32x4 af = *reinterpret_cast<const i32x4*>(as + 16 * i * LDAA + 64 * kk);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        // unconditional: a conditional use lets the compiler sink the loads above past the MFMAs;
+        // and after them: staging waits for those loads, so it must not move ahead of the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int64_t n = n0 + wn * WN + 16 * j + r16;
+        if (n >= p.N) continue;
+        const float sc = p.s_ch[n];
+        const float bv = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t m = m0 + wm * WM + 16 * i + 4 * g + v;
+                if (m >= p.M) continue;
+                float val = (float)acc[i][j][v] * p.sx[m];
+                val = val * sc;
+                if (p.bias) val = val + bv;
+                store_rt(p.y, p.y_dtype, m * p.ldy + n, val);
+            }
+    }
+    }
+}
+
 template <int BITS, bool CB, typename TSrel>
 hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    // large tiles when the grid still fills the GPU and one scale covers each row's k-tile
+    const int64_t big_tiles = ((p.N + 255) / 256) * ((p.M + 255) / 256);
+    if (p.group_size % 64 == 0 && p.K % BKA == 0 && p.ldq % 16 == 0 && big_tiles >= 192) {
+        dim3 grid((unsigned)big_tiles), block(512);
+        hipLaunchKernelGGL((gemm_a8_kernel<BITS, CB, TSrel>), grid, block, 0, st, p);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM)), block(256);
     hipLaunchKernelGGL((gemm_i8_kernel<BITS, CB, TSrel>), grid, block, 0, st, p);
     return hipGetLastError();

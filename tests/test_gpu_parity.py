@@ -333,6 +333,37 @@ def test_w4a8_linear(bits, gs, cb, srdt, m):
     check_linear(yb, want + b.numpy()[None, :].astype(np.float64), "bias")
 
 
+@pytest.mark.parametrize("bits,cb,srdt,gs,k", [(4, None, torch.float16, 128, 256), (4, None, torch.float16, 64, 128),
+                                                (4, "auto", torch.float8_e4m3fn, 64, 128),
+                                                (6, None, torch.float8_e4m3fn, 64, 256)])
+def test_w4a8_linear_large_tiles(bits, cb, srdt, gs, k):
+    """Shapes that take the 256 x 256 tile kernel (>= 192 tiles), ragged in M and N; group size 128
+    shares one scale table per thread pair, 64 does not.  9 x 23 = 207 tiles (not a multiple of the
+    8 XCDs) for the 4-bit uniform group-64 case, 8 x 24 otherwise."""
+    m, n, g = (2303, 5880, 128) if (bits, cb, gs) == (4, None, 64) else (2047, 6136, 128)
+    rng = np.random.default_rng(20 + bits)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if cb == "auto":  # heavy tails (the quantizer fits a codebook), rescaled to the same spread
+        w = w * np.exp(rng.standard_normal((n, k)))
+        w = (w * (0.02 / w.std())).astype(np.float32)
+    q, s_rel, s_ch, book = qz().quantize_w4a8_int8_weight(w, bits=bits, group_size=gs, convrot_groupsize=g,
+                                                          codebook=cb, s_rel_dtype=srdt)
+    x = x_fp16(m, k, seed=3, outliers=True)
+    dev = lambda t: None if t is None else t.to(DEV)
+    Q = qlin()
+    y = Q.w4a8_int8_linear(x.to(DEV), dev(q), dev(s_rel), dev(s_ch), dev(book), None, None, gs, g)
+    w8 = O.w4a8_int8_grid(q.numpy(), s_rel.float().numpy(), None if book is None else book.numpy(), k, bits, gs)
+    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), g)
+    xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
+    acc = O.int8_gemm_i64(xq, w8)
+    replay = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * s_ch.numpy()[None, :]).astype(np.float32)
+    got = y.cpu().numpy()
+    bad = got.view(np.uint16) != replay.astype(np.float16).view(np.uint16)
+    assert not bad.any(), f"{int(bad.sum())} mismatches, first at {np.argwhere(bad)[:3].tolist()}"
+    want = O.linear_ref(xq.astype(np.float32) * sx[:, None], w8.astype(np.float32) * s_ch.numpy()[:, None])
+    check_linear(y, want, f"bits={bits} large tiles")
+
+
 @pytest.mark.parametrize("case", ["gauss_96x1024", "heavy_96x1024"])
 @pytest.mark.parametrize("fmt,bits", [("w4a8", 4), ("w6a8", 6)])
 def test_dequantize_w4a8_golden(case, fmt, bits):
