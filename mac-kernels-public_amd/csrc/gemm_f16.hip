@@ -193,9 +193,157 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
     }
 }
 
+
+// ------------------------------------------------------------------------------------------------
+// Large-tile INT8 weight-only kernel: 512 threads = 8 waves (4 M x 2 N of 64 x 128), tile
+// 256 x 256 x 64, LDS double buffer (2 x 72 KiB).  Two waves per SIMD, so one wave's MFMAs cover
+// the other's memory waits.  The int8 tile is converted exactly in the load stage with byte
+// permutes: fp16 bits 0x6400 | (q + 128) = 1024 + q + 128, minus 1152, two values per packed add.
+// The next k-tile's loads are issued before the current tile's MFMAs and staged after them.
+// ------------------------------------------------------------------------------------------------
+constexpr int WBK = 64, WLDK = WBK + 8;  // k-tile and LDS row stride (halves)
+
+// Tile order for an 8-XCD part (block b runs on XCD b % 8): each XCD takes a contiguous run of the
+// tile sequence, which walks groups of 4 M-tiles across all N-tiles, so tiles resident at the same
+// time on one XCD share activation and weight panels in its L2.
+__device__ __forceinline__ void xcd_tile_f16(int b, int nblocks, int n_m, int n_n, int& mt, int& nt) {
+    constexpr int XCD = 8, GROUP_M = 4;
+    const int per = nblocks / XCD;  // the last nblocks % 8 blocks keep the plain order
+    const int t = b < XCD * per ? (b % XCD) * per + b / XCD : b;
+    const int group = t / (GROUP_M * n_n);
+    const int first_m = group * GROUP_M;
+    const int gm = min(n_m - first_m, GROUP_M);
+    mt = first_m + (t % (GROUP_M * n_n)) % gm;
+    nt = (t % (GROUP_M * n_n)) / gm;
+}
+
+// 4 int8 (one dword) -> 4 exact fp16 (two dwords)
+__device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;  // q + 128 as unsigned bytes
+    const f16x2 off = {(f16)-1152.0f, (f16)-1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off);
+}
+
+__global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
+    constexpr int BMT = 256, BNT = 256, NT = 512;
+    constexpr int WM = 64, WN = 128, TI = WM / 16, TJ = WN / 16;
+    constexpr int NA = BMT * (WBK / 8) / NT;  // 16-byte activation units per thread and k-tile (4)
+    constexpr int UA = WBK / 8;               // ... per activation row (8)
+    __shared__ __attribute__((aligned(16))) f16 As[2][BMT * WLDK];
+    __shared__ __attribute__((aligned(16))) f16 Bs[2][BNT * WLDK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, g = lane >> 4;
+    int mt, nt;
+    xcd_tile_f16(blockIdx.x, (int)gridDim.x, (int)((a.M + BMT - 1) / BMT), (int)((a.N + BNT - 1) / BNT), mt, nt);
+    const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
+    const int ktiles = (int)(a.K / WBK);
+
+    // rows past M or N re-read the last row (never stored); pointers fixed along K
+    const f16* arow[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int u = tid + NT * i;
+        arow[i] = a.x + min(m0 + u / UA, a.M - 1) * a.ldx + 8 * (u % UA);
+    }
+    const int br = tid >> 1, bh = tid & 1;  // weight row br, values 32 bh .. 32 bh + 31 of a k-tile
+    const int8_t* wrow = (const int8_t*)a.w + min(n0 + br, a.N - 1) * a.ldw + 32 * bh;
+
+    u32x4 ra[NA], rb[2];
+    auto fetch = [&](int kt) {
+        const int k0 = min(kt, ktiles - 1) * WBK;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
+        rb[0] = *reinterpret_cast<const u32x4*>(wrow + k0);
+        rb[1] = *reinterpret_cast<const u32x4*>(wrow + k0 + 16);
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int u = tid + NT * i;
+            *reinterpret_cast<u32x4*>(&As[buf][(u / UA) * WLDK + 8 * (u % UA)]) = ra[i];
+        }
+        u32x4* pb = reinterpret_cast<u32x4*>(&Bs[buf][br * WLDK + 32 * bh]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t o[8];
+            i8x4_to_f16(rb[h].x, o[0], o[1]);
+            i8x4_to_f16(rb[h].y, o[2], o[3]);
+            i8x4_to_f16(rb[h].z, o[4], o[5]);
+            i8x4_to_f16(rb[h].w, o[6], o[7]);
+            pb[2 * h] = u32x4{o[0], o[1], o[2], o[3]};
+            pb[2 * h + 1] = u32x4{o[4], o[5], o[6], o[7]};
+        }
+    };
+
+    f32x4 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int buf = kt & 1;
+        fetch(kt + 1);  // clamped past the end: re-reads the last tile (staged into an unread buffer)
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
+        const f16* as = &As[buf][(wm * WM + r16) * WLDK + 8 * g];
+        const f16* bs = &Bs[buf][(wn * WN + r16) * WLDK + 8 * g];
+#pragma unroll
+        for (int kk = 0; kk < WBK / 32; ++kk) {
+            f16x8 bf[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + 16 * j * WLDK + 32 * kk);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const f16x8 af = *reinterpret_cast<const f16x8*>(as + 16 * i * WLDK + 32 * kk);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        // unconditional (a conditional use lets the compiler sink the loads past the MFMAs), and
+        // after the MFMAs (staging waits for those loads)
+        __builtin_amdgcn_sched_barrier(0);
+        stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    // acc[i][j][v] = D[m = wm*64 + 16i + 4g + v][n = wn*128 + 16j + r16]
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int64_t n = n0 + wn * WN + 16 * j + r16;
+        if (n >= a.N) continue;
+        const float cs = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+        const float bv = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t m = m0 + wm * WM + 16 * i + 4 * g + v;
+                if (m >= a.M) continue;
+                float val = a.xexp ? __builtin_ldexpf(acc[i][j][v], a.xexp[m]) : acc[i][j][v];
+                store_rt(a.y, a.y_dtype, m * a.ldy + n, val * cs + bv);
+            }
+    }
+}
+
 template <int WK, int GT>
 hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
     if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if constexpr (WK == WO_INT8) {
+        // large tiles when the grid still fills the GPU and the operands allow 16-byte loads
+        const int64_t big_tiles = ((a.N + 255) / 256) * ((a.M + 255) / 256);
+        const bool vec = a.K % WBK == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 16 == 0 &&
+                         (uintptr_t)a.w % 16 == 0;
+        if (vec && big_tiles >= 192) {
+            hipLaunchKernelGGL(gemm_wo_i8_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a);
+            return hipGetLastError();
+        }
+    }
     dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);
     hipLaunchKernelGGL((gemm_f16_kernel<WK, GT>), grid, block, 0, st, a);
     return hipGetLastError();

@@ -205,6 +205,31 @@ def test_int8_linear(g, m):
         assert O.rel_fro(want2, want) < 1e-5
 
 
+@pytest.mark.parametrize("g,m,n,xdt,odt", [(0, 2047, 6136, torch.float16, torch.float16),
+                                           (128, 2303, 5880, torch.bfloat16, torch.bfloat16)])
+def test_int8_linear_large_tiles(g, m, n, xdt, odt):
+    """Shapes that take the 256 x 256 tile kernel (>= 192 tiles, ragged M and N, 192 and 207 tiles),
+    with fp16 scales and a bias."""
+    k = 256
+    rng = np.random.default_rng(17)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    q, s = qz().quantize_int8_convrot_weight(w, g) if g else qz().quantize_int8_rowwise(w)
+    s16 = s.astype(np.float16)
+    b = rng.standard_normal(n).astype(np.float32)
+    x = x_fp16(m, k, seed=5).to(xdt)
+    xr = O.rotate(x.float().numpy(), g) if g else x.float().numpy()
+    want = O.linear_ref(xr, O.dequantize_int8(q, s16.astype(np.float32)), b)
+    got = qlin().int8_linear(x.to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s16).to(DEV),
+                             torch.from_numpy(b).to(DEV), odt, convrot=bool(g), convrot_groupsize=g or 256)
+    assert got.dtype == odt
+    if odt == torch.bfloat16:  # one bf16 rounding of the output
+        rb = torch.from_numpy(want.astype(np.float32)).bfloat16().double().numpy()
+        assert O.rel_fro(got.double().cpu().numpy(), rb) < 1e-3
+        assert O.rel_fro(got.double().cpu().numpy(), want) < 4e-3
+    else:
+        check_linear(got, want, f"G={g} large tiles")
+
+
 def test_int8_linear_scales_bias_bf16():
     n, k, m = 64, 512, 70
     rng = np.random.default_rng(8)
