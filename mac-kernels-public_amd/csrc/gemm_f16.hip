@@ -26,6 +26,14 @@ __device__ __forceinline__ uint32_t pack2(f16 lo, f16 hi) {
     return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
 }
 
+// 4 int8 (one dword) -> 4 exact fp16 (two dwords)
+__device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;  // q + 128 as unsigned bytes
+    const f16x2 off = {(f16)-1152.0f, (f16)-1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off);
+}
+
 // A: row r = tid/2 of the tile, 32 halves from column 32*(tid%2).
 __device__ __forceinline__ void load_a(const f16* __restrict__ x, int64_t ldx, int64_t M, int64_t K, int64_t m0,
                                        int64_t k0, int tid, bool vec_ok, TileRegs& R) {
@@ -54,22 +62,26 @@ __device__ __forceinline__ void load_b_int8(const int8_t* __restrict__ w, int64_
                                             int64_t n0, int64_t k0, int tid, bool vec_ok, TileRegs& R) {
     const int r = tid >> 1, h = tid & 1;
     const int64_t n = n0 + r, k = k0 + 32 * h;
-    int8_t v[32];
+    uint32_t ww[8];
     if (n < N && vec_ok && k + 32 <= K) {
         const u32x4* p = reinterpret_cast<const u32x4*>(w + n * ldw + k);
-        u32x4 a = p[0], b = p[1];
-        uint32_t ww[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = (int8_t)(ww[i >> 2] >> (8 * (i & 3)));
+        const u32x4 a = p[0], b = p[1];
+        ww[0] = a.x; ww[1] = a.y; ww[2] = a.z; ww[3] = a.w; ww[4] = b.x; ww[5] = b.y; ww[6] = b.z; ww[7] = b.w;
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = (n < N && k + i < K) ? w[n * ldw + k + i] : (int8_t)0;
+        for (int i = 0; i < 8; ++i) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (n < N && k + 4 * i + t < K) v |= (uint32_t)(uint8_t)w[n * ldw + k + 4 * i + t] << (8 * t);
+            ww[i] = v;
+        }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         uint32_t p[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = pack2((f16)(float)v[8 * i + 2 * j], (f16)(float)v[8 * i + 2 * j + 1]);
+        i8x4_to_f16(ww[2 * i], p[0], p[1]);
+        i8x4_to_f16(ww[2 * i + 1], p[2], p[3]);
         R.b[i] = u32x4{p[0], p[1], p[2], p[3]};
     }
 }
@@ -147,7 +159,8 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
     const int r16 = lane & 15, g = lane >> 4;
     for (int kt = 0; kt < ktiles; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < ktiles) fetch(kt + 1);
+        fetch(min(kt + 1, ktiles - 1));  // unconditional (see below); past the end: re-reads the last tile
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
         const f16* As = smem[buf][0];
         const f16* Bs = smem[buf][1];
 #pragma unroll
@@ -164,7 +177,10 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < ktiles) store_tile(smem[buf ^ 1][0], smem[buf ^ 1][1], tid, R);
+        // unconditional: a conditional use lets the compiler sink the loads past the MFMAs; the
+        // last iteration writes the unread buffer
+        __builtin_amdgcn_sched_barrier(0);
+        store_tile(smem[buf ^ 1][0], smem[buf ^ 1][1], tid, R);
         __syncthreads();
     }
 
@@ -195,8 +211,8 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
 
 
 // ------------------------------------------------------------------------------------------------
-// Large-tile INT8 weight-only kernel: 512 threads = 8 waves (4 M x 2 N of 64 x 128), tile
-// 256 x 256 x 64, LDS double buffer (2 x 72 KiB).  Two waves per SIMD, so one wave's MFMAs cover
+// INT8 weight-only kernel: 512 threads = 8 waves (4 M x 2 N), tile BM x BN x 64 with BM, BN in
+// {64, 128, 256} chosen by shape (256 x 256: LDS double buffer of 2 x 72 KiB).  Two waves per SIMD, so one wave's MFMAs cover
 // the other's memory waits.  The int8 tile is converted exactly in the load stage with byte
 // permutes: fp16 bits 0x6400 | (q + 128) = 1024 + q + 128, minus 1152, two values per packed add.
 // The next k-tile's loads are issued before the current tile's MFMAs and staged after them.
@@ -217,19 +233,16 @@ __device__ __forceinline__ void xcd_tile_f16(int b, int nblocks, int n_m, int n_
     nt = (t % (GROUP_M * n_n)) / gm;
 }
 
-// 4 int8 (one dword) -> 4 exact fp16 (two dwords)
-__device__ __forceinline__ void i8x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
-    const uint32_t u = w ^ 0x80808080u;  // q + 128 as unsigned bytes
-    const f16x2 off = {(f16)-1152.0f, (f16)-1152.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off);
-}
 
+template <int BMT, int BNT>
 __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
-    constexpr int BMT = 256, BNT = 256, NT = 512;
-    constexpr int WM = 64, WN = 128, TI = WM / 16, TJ = WN / 16;
-    constexpr int NA = BMT * (WBK / 8) / NT;  // 16-byte activation units per thread and k-tile (4)
-    constexpr int UA = WBK / 8;               // ... per activation row (8)
+    constexpr int NT = 512;
+    constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 16, TJ = WN / 16;
+    constexpr int UA = WBK / 8;                 // 16-byte activation units per row and k-tile
+    constexpr int NA = BMT * UA / NT;           // ... per thread
+    constexpr int TPR = NT / BNT;               // threads per weight row
+    constexpr int VPT = WBK / TPR;              // weight values (bytes) per thread and k-tile
+    static_assert(NA >= 1 && TI >= 1 && TJ >= 1 && VPT % 8 == 0, "tile shape");
     __shared__ __attribute__((aligned(16))) f16 As[2][BMT * WLDK];
     __shared__ __attribute__((aligned(16))) f16 Bs[2][BNT * WLDK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -247,16 +260,25 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
         const int u = tid + NT * i;
         arow[i] = a.x + min(m0 + u / UA, a.M - 1) * a.ldx + 8 * (u % UA);
     }
-    const int br = tid >> 1, bh = tid & 1;  // weight row br, values 32 bh .. 32 bh + 31 of a k-tile
-    const int8_t* wrow = (const int8_t*)a.w + min(n0 + br, a.N - 1) * a.ldw + 32 * bh;
+    const int br = tid / TPR, bh = tid % TPR;  // weight row br, values VPT*bh .. of a k-tile
+    const int8_t* wrow = (const int8_t*)a.w + min(n0 + br, a.N - 1) * a.ldw + VPT * bh;
 
-    u32x4 ra[NA], rb[2];
+    u32x4 ra[NA];
+    uint32_t rb[VPT / 4];
     auto fetch = [&](int kt) {
         const int k0 = min(kt, ktiles - 1) * WBK;
 #pragma unroll
         for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
-        rb[0] = *reinterpret_cast<const u32x4*>(wrow + k0);
-        rb[1] = *reinterpret_cast<const u32x4*>(wrow + k0 + 16);
+        if constexpr (VPT >= 16) {
+#pragma unroll
+            for (int h = 0; h < VPT / 16; ++h) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(wrow + k0 + 16 * h);
+                rb[4 * h] = v.x; rb[4 * h + 1] = v.y; rb[4 * h + 2] = v.z; rb[4 * h + 3] = v.w;
+            }
+        } else {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(wrow + k0);
+            rb[0] = v.x; rb[1] = v.y;
+        }
     };
     auto stage = [&](int buf) {
 #pragma unroll
@@ -264,16 +286,13 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
             const int u = tid + NT * i;
             *reinterpret_cast<u32x4*>(&As[buf][(u / UA) * WLDK + 8 * (u % UA)]) = ra[i];
         }
-        u32x4* pb = reinterpret_cast<u32x4*>(&Bs[buf][br * WLDK + 32 * bh]);
+        u32x4* pb = reinterpret_cast<u32x4*>(&Bs[buf][br * WLDK + VPT * bh]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint32_t o[8];
-            i8x4_to_f16(rb[h].x, o[0], o[1]);
-            i8x4_to_f16(rb[h].y, o[2], o[3]);
-            i8x4_to_f16(rb[h].z, o[4], o[5]);
-            i8x4_to_f16(rb[h].w, o[6], o[7]);
-            pb[2 * h] = u32x4{o[0], o[1], o[2], o[3]};
-            pb[2 * h + 1] = u32x4{o[4], o[5], o[6], o[7]};
+        for (int h = 0; h < VPT / 8; ++h) {
+            uint32_t o[4];
+            i8x4_to_f16(rb[2 * h], o[0], o[1]);
+            i8x4_to_f16(rb[2 * h + 1], o[2], o[3]);
+            pb[h] = u32x4{o[0], o[1], o[2], o[3]};
         }
     };
 
@@ -312,7 +331,7 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
         __syncthreads();
     }
 
-    // acc[i][j][v] = D[m = wm*64 + 16i + 4g + v][n = wn*128 + 16j + r16]
+    // acc[i][j][v] = D[m = wm*WM + 16i + 4g + v][n = wn*WN + 16j + r16]
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int64_t n = n0 + wn * WN + 16 * j + r16;
@@ -335,13 +354,23 @@ template <int WK, int GT>
 hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
     if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
     if constexpr (WK == WO_INT8) {
-        // large tiles when the grid still fills the GPU and the operands allow 16-byte loads
-        const int64_t big_tiles = ((a.N + 255) / 256) * ((a.M + 255) / 256);
+        // the largest tile whose grid still fills the GPU (about 160 workgroups or more), when the
+        // operands allow 16-byte loads
         const bool vec = a.K % WBK == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 16 == 0 &&
                          (uintptr_t)a.w % 16 == 0;
-        if (vec && big_tiles >= 192) {
-            hipLaunchKernelGGL(gemm_wo_i8_kernel, dim3((unsigned)big_tiles), dim3(512), 0, st, a);
-            return hipGetLastError();
+        auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
+        if (vec) {
+#define QLIN_WO(BMV, BNV)                                                                                   \
+    if (tiles(BMV, BNV) >= 160 || (BMV == 64 && BNV == 64)) {                                              \
+        hipLaunchKernelGGL((gemm_wo_i8_kernel<BMV, BNV>), dim3((unsigned)tiles(BMV, BNV)), dim3(512), 0, st, a); \
+        return hipGetLastError();                                                                           \
+    }
+            QLIN_WO(256, 256)
+            QLIN_WO(128, 256)
+            QLIN_WO(128, 128)
+            QLIN_WO(64, 128)
+            QLIN_WO(64, 64)
+#undef QLIN_WO
         }
     }
     dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);

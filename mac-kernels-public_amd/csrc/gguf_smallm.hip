@@ -49,7 +49,8 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     constexpr int UPR = (RSB + 15) / 16;             // load units per row
     constexpr int UNITS = 16 * UPR;                  // load units per stage
     constexpr int NPF = (UNITS + 63) / 64;           // load units per lane per stage
-    // stages held in registers: two when a stage is small, else one (register pressure)
+    // stages held in registers: two when a stage is small, else one (two stages in flight at
+    // MT >= 3 measured slower: the activation stream already fills the memory pipeline)
     constexpr int PF = (NPF <= 12 && MT <= 2) ? 2 : 1;
     constexpr int UPS = SV / UNIT;                   // scale units per stage
     constexpr int UPB = QK / UNIT;                   // scale units per block
@@ -97,15 +98,16 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
             buf[i] = *reinterpret_cast<const LU*>(w + (int64_t)min(n0 + r, N - 1) * row_bytes + (int64_t)st * RSB + off);
         }
     };
+    // Unconditional: lanes past the last unit re-write its bytes (issue() loaded that same unit
+    // for them).  A guarded store would let the compiler sink the guarded lanes' load into the
+    // guard, behind a wait for every load in flight.
     auto commit = [&](const LU* buf) {
 #pragma unroll
         for (int i = 0; i < NPF; ++i) {
-            const int u = lane + 64 * i;
-            if (u < UNITS) {
-                const int r = u / UPR;
-                const int off = min((u - r * UPR) * 16, RSB - 16);
-                *reinterpret_cast<LU*>(my + r * RS + off) = buf[i];
-            }
+            const int u = (UNITS % 64 == 0) ? lane + 64 * i : min(lane + 64 * i, UNITS - 1);
+            const int r = u / UPR;
+            const int off = min((u - r * UPR) * 16, RSB - 16);
+            *reinterpret_cast<LU*>(my + r * RS + off) = buf[i];
         }
     };
     V xr[D][MT];

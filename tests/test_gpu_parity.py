@@ -206,10 +206,11 @@ def test_int8_linear(g, m):
 
 
 @pytest.mark.parametrize("g,m,n,xdt,odt", [(0, 2047, 6136, torch.float16, torch.float16),
-                                           (128, 2303, 5880, torch.bfloat16, torch.bfloat16)])
+                                           (128, 2303, 5880, torch.bfloat16, torch.bfloat16),
+                                           (128, 640, 4000, torch.float16, torch.float32)])
 def test_int8_linear_large_tiles(g, m, n, xdt, odt):
-    """Shapes that take the 256 x 256 tile kernel (>= 192 tiles, ragged M and N, 192 and 207 tiles),
-    with fp16 scales and a bias."""
+    """Shapes that take the 256 x 256 tile (192 and 207 tiles, ragged M and N) and the 128 x 128 tile
+    (640 x 4000: 160 tiles), with fp16 scales and a bias."""
     k = 256
     rng = np.random.default_rng(17)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
