@@ -234,7 +234,9 @@ __device__ __forceinline__ void xcd_tile_f16(int b, int nblocks, int n_m, int n_
 }
 
 
-template <int BMT, int BNT>
+// DEEP: two register sets, so each k-tile's loads are issued two k-tiles before they are staged
+// (requires an even number of k-tiles); otherwise one.
+template <int BMT, int BNT, bool DEEP>
 __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     constexpr int NT = 512;
     constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 16, TJ = WN / 16;
@@ -263,35 +265,37 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     const int br = tid / TPR, bh = tid % TPR;  // weight row br, values VPT*bh .. of a k-tile
     const int8_t* wrow = (const int8_t*)a.w + min(n0 + br, a.N - 1) * a.ldw + VPT * bh;
 
-    u32x4 ra[NA];
-    uint32_t rb[VPT / 4];
-    auto fetch = [&](int kt) {
-        const int k0 = min(kt, ktiles - 1) * WBK;
+    struct Regs {
+        u32x4 a[NA];
+        uint32_t b[VPT / 4];
+    };
+    auto fetch = [&](int kt, Regs& R) {
+        const int k0 = min(kt, ktiles - 1) * WBK;  // past the end: re-reads the last tile
 #pragma unroll
-        for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
+        for (int i = 0; i < NA; ++i) R.a[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
         if constexpr (VPT >= 16) {
 #pragma unroll
             for (int h = 0; h < VPT / 16; ++h) {
                 const u32x4 v = *reinterpret_cast<const u32x4*>(wrow + k0 + 16 * h);
-                rb[4 * h] = v.x; rb[4 * h + 1] = v.y; rb[4 * h + 2] = v.z; rb[4 * h + 3] = v.w;
+                R.b[4 * h] = v.x; R.b[4 * h + 1] = v.y; R.b[4 * h + 2] = v.z; R.b[4 * h + 3] = v.w;
             }
         } else {
             const u32x2 v = *reinterpret_cast<const u32x2*>(wrow + k0);
-            rb[0] = v.x; rb[1] = v.y;
+            R.b[0] = v.x; R.b[1] = v.y;
         }
     };
-    auto stage = [&](int buf) {
+    auto stage = [&](int buf, const Regs& R) {
 #pragma unroll
         for (int i = 0; i < NA; ++i) {
             const int u = tid + NT * i;
-            *reinterpret_cast<u32x4*>(&As[buf][(u / UA) * WLDK + 8 * (u % UA)]) = ra[i];
+            *reinterpret_cast<u32x4*>(&As[buf][(u / UA) * WLDK + 8 * (u % UA)]) = R.a[i];
         }
         u32x4* pb = reinterpret_cast<u32x4*>(&Bs[buf][br * WLDK + VPT * bh]);
 #pragma unroll
         for (int h = 0; h < VPT / 8; ++h) {
             uint32_t o[4];
-            i8x4_to_f16(rb[2 * h], o[0], o[1]);
-            i8x4_to_f16(rb[2 * h + 1], o[2], o[3]);
+            i8x4_to_f16(R.b[2 * h], o[0], o[1]);
+            i8x4_to_f16(R.b[2 * h + 1], o[2], o[3]);
             pb[h] = u32x4{o[0], o[1], o[2], o[3]};
         }
     };
@@ -301,14 +305,7 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int buf = kt & 1;
-        fetch(kt + 1);  // clamped past the end: re-reads the last tile (staged into an unread buffer)
-        __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
+    auto compute = [&](int buf) {
         const f16* as = &As[buf][(wm * WM + r16) * WLDK + 8 * g];
         const f16* bs = &Bs[buf][(wn * WN + r16) * WLDK + 8 * g];
 #pragma unroll
@@ -324,11 +321,41 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
             }
         }
-        // unconditional (a conditional use lets the compiler sink the loads past the MFMAs), and
-        // after the MFMAs (staging waits for those loads)
-        __builtin_amdgcn_sched_barrier(0);
-        stage(buf ^ 1);
+    };
+    // Each step: loads for a later tile go out first (sched_barrier), then this tile's MFMAs, then
+    // (after another sched_barrier: staging waits for loads) the next tile is staged.  Every load
+    // is used unconditionally: a conditional use lets the compiler sink it past the MFMAs.
+    Regs R0, R1;
+    fetch(0, R0);
+    stage(0, R0);
+    if constexpr (DEEP) {
+        fetch(1, R1);
         __syncthreads();
+        for (int kt = 0; kt < ktiles; kt += 2) {
+            fetch(kt + 2, R0);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(1, R1);
+            __syncthreads();
+            fetch(kt + 3, R1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(0, R0);
+            __syncthreads();
+        }
+    } else {
+        __syncthreads();
+        for (int kt = 0; kt < ktiles; ++kt) {
+            const int buf = kt & 1;
+            fetch(kt + 1, R0);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(buf);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(buf ^ 1, R0);
+            __syncthreads();
+        }
     }
 
     // acc[i][j][v] = D[m = wm*WM + 16i + 4g + v][n = wn*WN + 16j + r16]
@@ -360,10 +387,15 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
                          (uintptr_t)a.w % 16 == 0;
         auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
         if (vec) {
-#define QLIN_WO(BMV, BNV)                                                                                   \
-    if (tiles(BMV, BNV) >= 160 || (BMV == 64 && BNV == 64)) {                                              \
-        hipLaunchKernelGGL((gemm_wo_i8_kernel<BMV, BNV>), dim3((unsigned)tiles(BMV, BNV)), dim3(512), 0, st, a); \
-        return hipGetLastError();                                                                           \
+        // two-deep prefetch for the smaller tiles (at 256 x 256 it spills and measured slower)
+        const bool deep = (a.K / WBK) % 2 == 0;
+#define QLIN_WO(BMV, BNV)                                                                                       \
+    if (tiles(BMV, BNV) >= 160 || (BMV == 64 && BNV == 64)) {                                                  \
+        if (deep && BMV * BNV < 256 * 256)                                                                      \
+            hipLaunchKernelGGL((gemm_wo_i8_kernel<BMV, BNV, true>), dim3((unsigned)tiles(BMV, BNV)), dim3(512), 0, st, a); \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemm_wo_i8_kernel<BMV, BNV, false>), dim3((unsigned)tiles(BMV, BNV)), dim3(512), 0, st, a); \
+        return hipGetLastError();                                                                               \
     }
             QLIN_WO(256, 256)
             QLIN_WO(128, 256)
