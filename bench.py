@@ -189,18 +189,24 @@ def cpu_baseline_gguf(n=4096, k=4096, ms=(1, 8, 64), rows=None):
     }
 
 
-def kernel_of(m):
-    """Kernel that serves a K=N=4096 GGUF call with M activation rows (the dispatch in the C ABI)."""
-    return "gguf_gemv_kernel" if m == 1 else "gguf_smallm_kernel"
+SPLIT_PATH = "gguf_split_kernel+gguf_split_reduce_kernel"
+
+
+def kernel_of(t, m):
+    """Kernel(s) that serve a K=N=4096 GGUF call of type t with M activation rows (the dispatch in
+    the C ABI).  The K-split path is two launches per call: the split kernel and its reduction."""
+    if m == 1:
+        return "gguf_gemv_kernel"
+    return SPLIT_PATH if m >= (5 if t == "Q6_K" else 17) else "gguf_smallm_kernel"
 
 
 def kernel_breakdown(detail):
-    """Per kernel: launches, algorithmic bytes per launch and the average launch duration, from the
-    per-(type, M) graph timings (HIP events on the replay stream)."""
+    """Per kernel (or two-kernel path): calls, algorithmic bytes per call and the average call
+    duration, from the per-(type, M) graph timings (HIP events on the replay stream)."""
     out = {}
     for key, d in detail.items():
         t, m = key.split("/M")
-        k = kernel_of(int(m))
+        k = kernel_of(t, int(m))
         e = out.setdefault(k, {"launches": 0, "bytes": 0, "us_total": 0.0})
         e["launches"] += 1
         e["bytes"] += d["bytes"]
@@ -215,16 +221,20 @@ def kernel_breakdown(detail):
 
 
 def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary
-    (counter runs cannot happen inside the timed process); None when no summary is present."""
+    """HBM bytes per call of `kernel` (a '+'-joined path adds its kernels) from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (counter runs cannot happen inside the timed
+    process); None when the summary has no line for one of them."""
     path = os.path.join(ROOT, "profiles", "gguf_linear_k4096_counters.md")
+    per = {}
     try:
         for line in open(path):
-            if line.startswith(f"traffic {kernel} "):
-                return int(line.split()[2])
+            if line.startswith("traffic "):
+                f = line.split()
+                per[f[1]] = int(f[2])
     except OSError:
-        pass
-    return None
+        return None
+    parts = kernel.split("+")
+    return sum(per[k] for k in parts) if all(k in per for k in parts) else None
 
 
 def profile_pass(n=4096, k=4096, ms=(1, 8, 64), reps=3):

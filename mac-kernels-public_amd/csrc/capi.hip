@@ -121,8 +121,26 @@ struct Carver {
 };
 
 size_t ws_int8(int64_t M, int64_t K) { return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4); }
-size_t ws_gguf(int64_t M, int64_t N, int64_t K) {
-    return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4);
+// GGUF paths by activation rows: one row -> the VALU GEMV; up to GGUF_SMALLM_MAX_M rows -> the
+// MFMA kernels that stream the weights once (K split across workgroups from gguf_split_min_m
+// rows on); more -> row exponents + the tiled fp16 GEMM.
+constexpr int64_t GGUF_SMALLM_MAX_M = 64;
+// Measured at K = N = 4096: the split kernel costs ~10 us at any M (two launches, partials) and
+// wins from M = 17 on, except Q6_K, whose 16-value units make the per-wave K-split kernel slower
+// (11.8 vs 13.9 us at M = 8).
+int64_t gguf_split_min_m(int type) { return type == gguf::Q6_K ? 5 : 17; }
+
+// K splits of the shared-activation kernel for this call, 0 when another kernel takes it.
+int gguf_split_for(int type, int64_t M, int64_t N, int64_t K) {
+    int qk, ts;
+    if (M < gguf_split_min_m(type) || M > GGUF_SMALLM_MAX_M || !gguf::type_info(type, qk, ts) || K % qk) return 0;
+    return gguf_split_parts(type, M, N, K, (K / qk) * ts);
+}
+
+size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
+    const int S = gguf_split_for(type, M, N, K);
+    return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
+           (S > 1 ? align_up((size_t)S * M * N * 4) : 0);
 }
 size_t ws_w4a8(int64_t M, int64_t K) { return align_up((size_t)(M * K)) + align_up((size_t)M * 4); }
 
@@ -180,7 +198,7 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
     switch (op) {
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
         case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, K);
-        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K);
+        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param);
     }
     return 0;
 }
@@ -246,8 +264,6 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
 }
 
 // Largest M of the small-M GGUF kernel (the single-row VALU kernel takes M = 1 when it applies)
-constexpr int64_t GGUF_SMALLM_MAX_M = 64;
-
 qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                              const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
                              void* stream) {
@@ -263,8 +279,8 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
     int bdt;
     if ((s = check_bias(bias, N, bdt))) return s;
     const int64_t M = X.rows;
-    if (workspace_bytes < ws_gguf(M, N, K))
-        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_gguf(M, N, K));
+    if (workspace_bytes < ws_gguf(M, N, K, ggml_type))
+        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_gguf(M, N, K, ggml_type));
     if (M == 0 || N == 0) return QLIN_OK;
     const int64_t row_bytes = (K / qk) * ts;
     hipStream_t st = (hipStream_t)stream;
@@ -285,6 +301,17 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
             g.y = Y.data; g.y_dtype = Y.dtype;
             return hip_status(run_gguf_gemv(g, st), "gguf gemv");
         }
+    }
+    if (const int S = aligned ? gguf_split_for(ggml_type, M, N, K) : 0; S > 0) {
+        GgufSplitArgs a;
+        a.type = ggml_type;
+        if ((s = wo_activations(X, 0, ws, st, a.x, a.ldx, a.xexp))) return s;
+        a.M = (int)M; a.N = (int)N; a.K = (int)K; a.S = S;
+        a.part = S > 1 ? (float*)ws.take((size_t)S * M * N * 4) : nullptr;
+        a.w = (const uint8_t*)weight; a.row_bytes = row_bytes;
+        a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
+        a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+        return hip_status(run_gguf_split(a, st), "gguf split-K");
     }
     if (aligned && M <= GGUF_SMALLM_MAX_M && gguf_smallm_supported(ggml_type, M, K, row_bytes)) {
         GgufSmallMArgs a;

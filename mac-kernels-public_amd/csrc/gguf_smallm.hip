@@ -42,7 +42,10 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     constexpr int QK = F::QK, TS = F::TS, UNIT = F::UNIT, VPL = UNIT / 4, SBLK = F::SBLK;
     constexpr int SV = SBLK * QK;                    // values per stage
     constexpr int RSB = SBLK * TS;                   // stage bytes per row
-    constexpr int RS = ((RSB + 15) / 16) * 16 + 16;  // LDS row stride (padded for over-reads)
+    // LDS row stride: padded for over-reads, and an odd number of 16-byte units so that the 16
+    // rows a fragment read touches fall in different banks
+    constexpr int RS0 = ((RSB + 15) / 16) * 16 + 16;
+    constexpr int RS = (RS0 / 16) % 2 ? RS0 : RS0 + 16;
     static_assert(RSB % 4 == 0 && RSB >= 16, "stage rows must be whole dwords");
     // 16-byte load units (dword alignment suffices); a row's last unit ends at the row's last
     // byte and may overlap the one before it

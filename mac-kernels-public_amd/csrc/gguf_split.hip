@@ -1,0 +1,400 @@
+// GGUF linear for a few dozen activation rows (M up to 64) with the activations shared in LDS and
+// K split across workgroups.
+//
+// A kernel that keeps all of K inside one workgroup of 16 weight rows makes every CU stream all
+// of x: M x K x 2 bytes (512 KiB at M = 64, K = 4096) against 36 KiB of weights, through loads
+// that each touch 16 rows.  Here:
+//   * a workgroup owns 128 weight rows (8 waves x 16), all M rows (MT m-tiles of 16) and one of S
+//     K ranges; grid = ceil(N / 128) x S, S chosen so the grid covers the GPU about once.  At
+//     K = N = 4096 (S = 8) a CU reads 64 KiB of x and 72 KiB of Q4_K weights;
+//   * per stage (SV values) the activation slice is loaded once, 16 bytes per lane with 512 or
+//     1024 contiguous bytes per row, into LDS (rows padded by 16 bytes so the fragment reads are
+//     conflict-free), and all eight waves read their MFMA A fragments from there;
+//   * each wave stages its own 16 weight rows through LDS and decodes them with the policies the
+//     small-M kernel uses (exact fp16 integers, fp32 scales), reusing each B fragment for its MT
+//     m-tiles;
+//   * the next stage's activations and weights are in flight while a stage is computed;
+//   * S > 1: each workgroup stores its fp32 partial tile to the workspace ([S][M][N]) and a second
+//     kernel adds the S partials in split order (the result does not depend on timing) and applies
+//     the epilogue; S = 1: the epilogue runs in place.
+#include "gguf_mfma_decode.h"
+
+namespace qlin {
+
+namespace {
+
+using namespace gguf_mfma;
+
+constexpr int SP_WAVES = 8;
+constexpr int SP_THREADS = SP_WAVES * 64;
+constexpr int SP_ROWS = 16 * SP_WAVES;  // weight rows per workgroup
+constexpr int SP_TARGET_BLOCKS = 256;   // one workgroup per CU
+constexpr int SP_MAX_SPLITS = 8;        // partial tiles added by the reduction kernel
+
+// Barrier for LDS only: waits for this wave's LDS operations, not for its global loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int T, int MT>
+__global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
+    const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
+    const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K, int S,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy,
+    float* __restrict__ part) {
+    using F = SM<T>;
+    constexpr int QK = F::QK, TS = F::TS, UNIT = F::UNIT, VPL = UNIT / 4, SBLK = F::SBLK;
+    constexpr int SV = SBLK * QK;                    // values per stage
+    constexpr int RSB = SBLK * TS;                   // stage bytes per weight row
+    // LDS weight row stride: padded for over-reads, and an odd number of 16-byte units so that
+    // the 16 rows a decode read touches fall in different banks
+    constexpr int RS0 = ((RSB + 15) / 16) * 16 + 16;
+    constexpr int RS = (RS0 / 16) % 2 ? RS0 : RS0 + 16;
+    static_assert(RSB % 4 == 0 && RSB >= 16, "stage rows must be whole dwords");
+    constexpr int UPR = (RSB + 15) / 16;             // 16-byte weight units per row (last one overlaps)
+    constexpr int HALF = 16 * UPR;                   // weight units each wave of a pair loads per stage
+    constexpr int NPF = (HALF + 63) / 64;            // weight units per lane
+    constexpr int UPS = SV / UNIT;                   // scale units per stage
+    constexpr int UH = UPS / 2;                      // scale units per K half
+    constexpr int UPB = QK / UNIT;                   // scale units per block
+    static_assert(UPS % 2 == 0 && (UPB % UH == 0 || UH % UPB == 0), "K halves must align with blocks");
+    constexpr int XR = MT * 16;                      // activation rows held (rows past M repeat row M - 1)
+    constexpr int XRS = SV * 2 + 16;                 // LDS activation row stride (bytes)
+    constexpr int CPR = SV / 8;                      // 16-byte activation chunks per row
+    constexpr int XPT = XR * CPR / SP_THREADS;       // activation chunks per thread and stage
+    static_assert(XR * CPR % SP_THREADS == 0, "activation stage must split evenly over the threads");
+    typedef typename FragT<VPL>::type V;
+    typedef uint32_t LU __attribute__((ext_vector_type(4), aligned(4)));
+
+    __shared__ __attribute__((aligned(16))) uint8_t xs[XR * XRS];
+    __shared__ __attribute__((aligned(16))) uint8_t wsm[SP_ROWS * RS];
+
+    // Waves 0..3 and 4..7 cover the first and second half of every stage's units; wave w % 4 of
+    // each half owns weight rows 32 (w % 4) .. + 31 of the tile (two n-tiles), so every activation
+    // fragment read from LDS feeds two MFMAs.
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int np = wave & 3, kh = wave >> 2;
+    const int n0 = blockIdx.x * SP_ROWS + np * 32;  // this wave pair's first weight row
+    const int nl = lane & 15, g = lane >> 4;
+    const int split = blockIdx.y;
+    const int stages = K / SV;
+    const int st0 = (int)((int64_t)stages * split / S), st1 = (int)((int64_t)stages * (split + 1) / S);
+    const int last = st1 - 1;  // the host keeps S <= stages, so every split has a stage
+    uint8_t* my = wsm + np * 32 * RS;
+    const int ilim = (MT == 1 && M < 4) ? M : 4;
+
+    // No load below branches on the lane: activation rows past M re-read row M - 1, weight rows
+    // past N re-read row N - 1 (their results are never stored), and each wave's last weight unit
+    // is re-read by the lanes past it.
+    // Stages held in registers ahead of LDS: a workgroup typically owns two 256-value stages, and
+    // both are requested before the first wait.
+    constexpr int PF = (SV == 256) ? 2 : 1;
+    u32x4 xq[PF][XPT];
+    auto issue_x = [&](int st, u32x4* dst) {
+        const int64_t k = (int64_t)min(st, last) * SV;
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int c = tid + SP_THREADS * j, r = c / CPR, cc = c % CPR;
+            dst[j] = *reinterpret_cast<const u32x4*>(x + (int64_t)min(r, M - 1) * ldx + k + 8 * cc);
+        }
+    };
+    auto commit_x = [&](const u32x4* src) {
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int c = tid + SP_THREADS * j, r = c / CPR, cc = c % CPR;
+            *reinterpret_cast<u32x4*>(xs + r * XRS + 16 * cc) = src[j];
+        }
+    };
+    // The pair's 32 x UPR load units: the K-half-0 wave takes the first half, the other the rest.
+    auto unit_of = [&](int i) { return kh * HALF + min(lane + 64 * i, HALF - 1); };
+    LU pf[PF][NPF];
+    auto issue_w = [&](int st, LU* dst) {
+        st = min(st, last);
+#pragma unroll
+        for (int i = 0; i < NPF; ++i) {
+            const int u = unit_of(i), r = u / UPR;
+            const int off = min((u - r * UPR) * 16, RSB - 16);
+            dst[i] = *reinterpret_cast<const LU*>(w + (int64_t)min(n0 + r, N - 1) * row_bytes + (int64_t)st * RSB + off);
+        }
+    };
+    // Unconditional: lanes past the last unit re-write its bytes (issue_w loaded that same unit).
+    auto commit_w = [&](const LU* src) {
+#pragma unroll
+        for (int i = 0; i < NPF; ++i) {
+            const int u = unit_of(i), r = u / UPR;
+            const int off = min((u - r * UPR) * 16, RSB - 16);
+            *reinterpret_cast<LU*>(my + r * RS + off) = src[i];
+        }
+    };
+
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    V ones;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) ones[i] = (f16)1.0f;
+
+    const uint8_t* srow[2] = {my + nl * RS, my + (16 + nl) * RS};
+    const uint8_t* xrow = xs + nl * XRS + 2 * VPL * g;  // A fragment: row mt * 16 + nl, values VPL*g.. of a unit
+
+    // This wave's half of a stage: units H * UH .. H * UH + UH - 1.
+    auto compute = [&]<int H>() {
+        if constexpr (F::KIND == 0) {
+#pragma unroll
+            for (int uu = 0; uu < UH; ++uu) {
+                const int u = H * UH + uu;
+                const int blk = (u * UNIT) / QK;
+                const int v0 = (u * UNIT) % QK + VPL * g;
+                float a[2], b[2];
+                V bf[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) bf[t] = F::get(srow[t], blk * TS, v0, a[t], b[t]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const V af = *reinterpret_cast<const V*>(xrow + mt * 16 * XRS + 2 * UNIT * u);
+                    f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (F::MIN) c1 = mfma16<VPL>(af, ones, c1);
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const f32x4 c = mfma16<VPL>(af, bf[t], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (i < ilim) acc[t][mt][i] += F::MIN ? a[t] * c[i] + b[t] * c1[i] : a[t] * c[i];
+                    }
+                }
+            }
+        } else {
+            constexpr int U0 = H * UH;
+#pragma unroll
+            for (int blk = U0 / UPB; blk <= (U0 + UH - 1) / UPB; ++blk) {
+                f32x4 c1[2][MT], c2[2][MT];
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        c1[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                        c2[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                const int ua = max(U0, blk * UPB), ub = min(U0 + UH, (blk + 1) * UPB);
+#pragma unroll
+                for (int u = ua; u < ub; ++u) {
+                    const int v0 = (u - blk * UPB) * UNIT + VPL * g;
+                    V bf[2], bm[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        f16 mv;
+                        bf[t] = F::get(srow[t], blk * TS, v0, mv);
+#pragma unroll
+                        for (int i = 0; i < VPL; ++i) bm[t][i] = mv;
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const V af = *reinterpret_cast<const V*>(xrow + mt * 16 * XRS + 2 * UNIT * u);
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            c1[t][mt] = mfma16<VPL>(af, bf[t], c1[t][mt]);
+                            if constexpr (F::MIN) c2[t][mt] = mfma16<VPL>(af, bm[t], c2[t][mt]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    float d, dmin;
+                    F::block(srow[t], blk * TS, d, dmin);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (i < ilim) {
+                                acc[t][mt][i] += d * c1[t][mt][i];
+                                if constexpr (F::MIN) acc[t][mt][i] -= dmin * c2[t][mt][i];
+                            }
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        issue_x(st0 + j, xq[j]);
+        issue_w(st0 + j, pf[j]);
+    }
+    for (int c0 = st0; c0 < st1; c0 += PF)
+#pragma unroll
+    for (int jp = 0; jp < PF; ++jp) {
+        const int st = c0 + jp;
+        if (st >= st1) break;
+        lds_barrier();  // every wave is done with the previous stage's LDS
+        commit_x(xq[jp]);
+        commit_w(pf[jp]);
+        if (st + PF < st1) {  // refill the freed registers with the stage PF ahead (uniform branch)
+            issue_x(st + PF, xq[jp]);
+            issue_w(st + PF, pf[jp]);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the next stages' loads stay ahead of this stage's math
+        lds_barrier();  // this stage is in LDS
+        if (kh == 0) compute.template operator()<0>();
+        else compute.template operator()<1>();
+    }
+
+    // The two K halves meet in LDS (reusing the activation buffer) in a fixed order, and the
+    // [XR x 128] tile leaves with every output row as 512 contiguous bytes.  Lane (nl, g),
+    // register i of n-tile t, m-tile mt holds row mt * 16 + 4 * g + i, column 32 np + 16 t + nl.
+    constexpr int ORS = SP_ROWS * 4 + 16;  // LDS output row stride (bytes)
+    static_assert(ORS <= XRS, "the output tile must fit in the activation buffer");
+    auto out_at = [&](int t, int mt, int i) {
+        return reinterpret_cast<float*>(xs + (mt * 16 + 4 * g + i) * ORS + 4 * (np * 32 + 16 * t + nl));
+    };
+    lds_barrier();  // every wave is done with the last stage's activations
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *out_at(t, mt, i) = acc[t][mt][i];
+    }
+    lds_barrier();
+    if (kh == 0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *out_at(t, mt, i) = acc[t][mt][i] + *out_at(t, mt, i);
+    }
+    lds_barrier();
+    const int nt0 = blockIdx.x * SP_ROWS;
+    if (part) {
+        // Partials are written through to memory (device-scope stores), so the reduction kernel
+        // reads them without an L2 write-back of the whole tile at the end of this kernel; each
+        // store instruction covers 256 contiguous bytes of a row.
+        const int c = tid % SP_ROWS, n = nt0 + c;
+#pragma unroll
+        for (int j = 0; j < XR * SP_ROWS / SP_THREADS; ++j) {
+            const int r = tid / SP_ROWS + (SP_THREADS / SP_ROWS) * j;
+            if (r < M && n < N)
+                __hip_atomic_store(part + ((int64_t)split * M + r) * N + n,
+                                   *reinterpret_cast<const float*>(xs + r * ORS + 4 * c), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < XR * (SP_ROWS / 4) / SP_THREADS; ++j) {
+        const int c = tid + SP_THREADS * j, r = c / (SP_ROWS / 4), n = nt0 + 4 * (c % (SP_ROWS / 4));
+        if (r >= M || n >= N) continue;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xs + r * ORS + 16 * (c % (SP_ROWS / 4)));
+        const int e = xexp ? xexp[r] : 0;
+        for (int q = 0; q < 4 && n + q < N; ++q)
+            store_rt(y, y_dt, (int64_t)r * ldy + n + q,
+                     __builtin_ldexpf(v[q], e) + (bias ? load_rt(bias, bias_dt, n + q) : 0.0f));
+    }
+}
+
+// y[m][n] = ldexp(sum over s in order of part[s][m][n], xexp[m]) + bias[n]; four columns per thread,
+// all S partial loads in flight at once.
+template <int S>
+__global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
+    const float* __restrict__ part, int M, int N, const int32_t* __restrict__ xexp,
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy) {
+    const int nq = (N + 3) / 4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)M * nq) return;
+    const int m = (int)(t / nq), n = (int)(t % nq) * 4;
+    const int64_t mn = (int64_t)M * N;
+    const float* p = part + (int64_t)m * N + n;
+    const int e = xexp ? xexp[m] : 0;
+    f32x4 s;
+    if (N % 4 == 0) {
+        f32x4 v[S];
+#pragma unroll
+        for (int k = 0; k < S; ++k) v[k] = *reinterpret_cast<const f32x4*>(p + k * mn);
+        s = v[0];
+#pragma unroll
+        for (int k = 1; k < S; ++k) s += v[k];
+    } else {
+        for (int q = 0; q < 4; ++q) {
+            float v[S];
+#pragma unroll
+            for (int k = 0; k < S; ++k) v[k] = n + q < N ? p[q + k * mn] : 0.0f;
+            s[q] = v[0];
+#pragma unroll
+            for (int k = 1; k < S; ++k) s[q] += v[k];
+        }
+    }
+    for (int q = 0; q < 4 && n + q < N; ++q)
+        store_rt(y, y_dt, (int64_t)m * ldy + n + q,
+                 __builtin_ldexpf(s[q], e) + (bias ? load_rt(bias, bias_dt, n + q) : 0.0f));
+}
+
+template <int T>
+constexpr int stage_values() { return SM<T>::SBLK * SM<T>::QK; }
+
+template <int T>
+hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
+    dim3 grid((unsigned)((a.N + SP_ROWS - 1) / SP_ROWS), (unsigned)a.S), block(SP_THREADS);
+    float* part = a.S > 1 ? a.part : nullptr;
+#define QLIN_SP_LAUNCH(MTV)                                                                                \
+    hipLaunchKernelGGL((gguf_split_kernel<T, MTV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w,    \
+                       a.row_bytes, a.N, a.K, a.S, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, part)
+    switch ((a.M + 15) / 16) {
+        case 1: QLIN_SP_LAUNCH(1); break;
+        case 2: QLIN_SP_LAUNCH(2); break;
+        case 3: QLIN_SP_LAUNCH(3); break;
+        case 4: QLIN_SP_LAUNCH(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef QLIN_SP_LAUNCH
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || a.S == 1) return err;
+    const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
+    const dim3 rgrid((unsigned)((threads + 255) / 256));
+#define QLIN_SP_REDUCE(SV)                                                                                    \
+    hipLaunchKernelGGL(gguf_split_reduce_kernel<SV>, rgrid, dim3(256), 0, st, a.part, a.M, a.N, a.xexp, a.bias, \
+                       a.bias_dtype, a.y, a.y_dtype, a.ldy)
+    switch (a.S) {
+        case 2: QLIN_SP_REDUCE(2); break;
+        case 3: QLIN_SP_REDUCE(3); break;
+        case 4: QLIN_SP_REDUCE(4); break;
+        case 5: QLIN_SP_REDUCE(5); break;
+        case 6: QLIN_SP_REDUCE(6); break;
+        case 7: QLIN_SP_REDUCE(7); break;
+        case 8: QLIN_SP_REDUCE(8); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef QLIN_SP_REDUCE
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes) {
+    if (M < 1 || M > 64 || N < 1) return 0;
+    int parts = 0;
+    gguf::dispatch_type(type, [&]<int T>() {
+        constexpr int SV = stage_values<T>(), RSB = SM<T>::SBLK * SM<T>::TS;
+        if (K % SV || RSB % 4 || row_bytes % 4) return;
+        const int64_t stages = K / SV, tiles = (N + SP_ROWS - 1) / SP_ROWS;
+        const int64_t s = (SP_TARGET_BLOCKS + tiles - 1) / tiles;
+        parts = (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(s, stages), SP_MAX_SPLITS));
+    });
+    return parts;
+}
+
+hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st) {
+    if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if (a.S < 1 || a.S > SP_MAX_SPLITS || (a.S > 1 && !a.part) || (a.ldx % 8) || ((uintptr_t)a.x % 16)) return hipErrorInvalidValue;
+    hipError_t err = hipErrorInvalidValue;
+    bool ok = gguf::dispatch_type(a.type, [&]<int T>() {
+        if ((a.K % stage_values<T>()) || a.S > a.K / stage_values<T>()) return;
+        err = launch_t<T>(a, st);
+    });
+    return ok ? err : hipErrorInvalidValue;
+}
+
+}  // namespace qlin

@@ -49,6 +49,28 @@ struct GgufSmallMArgs {
 bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes);
 hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st);
 
+// ---- GGUF linear with activations shared in LDS and K split across workgroups (gguf_split.hip) ----
+struct GgufSplitArgs {
+    int type = 0;
+    const f16* x = nullptr;          // fp16 activations, 16-byte aligned, ldx % 8 == 0
+    int64_t ldx = 0;
+    int M = 0;
+    const int32_t* xexp = nullptr;   // per-row exponent to restore (nullptr = 0)
+    const uint8_t* w = nullptr;
+    int64_t row_bytes = 0;
+    int N = 0, K = 0;
+    int S = 1;                       // K splits (gguf_split_parts)
+    float* part = nullptr;           // S > 1: fp32 partials [S][M][N]
+    const void* bias = nullptr;
+    int bias_dtype = DT_NONE;
+    void* y = nullptr;
+    int y_dtype = DT_F16;
+    int64_t ldy = 0;
+};
+// Number of K splits this path uses for the shape, 0 when it does not take it.
+int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes);
+hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st);
+
 // ---- GGUF single-row linear (gguf_gemv.hip) ----
 struct GgufGemvArgs {
     int type = 0;

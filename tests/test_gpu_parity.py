@@ -115,7 +115,7 @@ def test_dequantize_gguf_straddling_rows(name):
 # ------------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("name", GGUF)
-@pytest.mark.parametrize("m", [1, 8, 16, 17, 64, 100, 128, 129])  # every kernel and each switch point
+@pytest.mark.parametrize("m", [1, 4, 5, 8, 16, 17, 64, 100, 128, 129])  # every kernel and each switch point
 def test_gguf_linear(name, m):
     n, k = 80, 1024
     raw = qz().random_gguf_blocks(name, n, k, seed=11)
@@ -125,6 +125,24 @@ def test_gguf_linear(name, m):
     got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k))
     assert got.dtype == torch.float16 and got.shape == (m, n)
     check_linear(got, want, f"{name} M={m}")
+
+
+@pytest.mark.parametrize("name,m,n,k", [
+    ("Q4_K", 33, 131, 256),     # one K stage: single split, epilogue in the kernel, ragged N
+    ("Q4_0", 64, 131, 1280),    # five splits, N % 4 != 0 in the reduction
+    ("Q8_0", 20, 12800, 1280),  # 100 row tiles: three splits over five stages (uneven)
+    ("Q3_K", 64, 200, 2048),    # two-block stages, sub-block minimum MFMA
+    ("IQ4_XS", 47, 256, 4096),
+])
+def test_gguf_linear_split_k(name, m, n, k):
+    """The K-split kernel (M = 17..64): ragged N, uneven and single splits, bias."""
+    raw = qz().random_gguf_blocks(name, n, k, seed=21)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = x_fp16(m, k, seed=m + 3)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1).half()
+    want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), bias=b.to(DEV))
+    check_linear(got, want, f"{name} M={m} N={n} K={k}")
 
 
 @pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
