@@ -316,15 +316,18 @@ constexpr int BKA = 128, LDAA = BKA + 16;  // k-tile and LDS row stride (bytes)
 template <int BITS, bool CB, typename TSrel>
 __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
     constexpr int BMT = 256, BNT = 256, NT = 512;
-    constexpr int WM = 64, WN = 128, TI = WM / 16, TJ = WN / 16;
+    // v_mfma_i32_32x32x32_i8 sub-tiles (about 1.6x the throughput of the 16x16x64 form here)
+    constexpr int WM = 64, WN = 128, TI = WM / 32, TJ = WN / 32;
     constexpr int NA = BMT * (BKA / 16) / NT;  // 16-byte activation units per thread and k-tile
     constexpr int UA = BKA / 16;              // ... per activation row
-    __shared__ __attribute__((aligned(16))) uint8_t As[2][BMT * LDAA];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BNT * LDAA];
+    // one LDS block: double-buffered operands in the loop, then the output staging of the epilogue
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (BMT + BNT) * LDAA];
+    uint8_t (*As)[BMT * LDAA] = reinterpret_cast<uint8_t (*)[BMT * LDAA]>(smem);
+    uint8_t (*Bs)[BNT * LDAA] = reinterpret_cast<uint8_t (*)[BNT * LDAA]>(smem + 2 * BMT * LDAA);
     __shared__ float cb_s[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int r16 = lane & 15, g = lane >> 4;
+    const int r32 = lane & 31, h = lane >> 5;
     int mt, nt;
     xcd_tile(blockIdx.x, (int)gridDim.x, (int)((p.M + BMT - 1) / BMT), (int)((p.N + BNT - 1) / BNT), mt, nt);
     const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
@@ -382,11 +385,13 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
         for (int i = 0; i < 4; ++i) pb[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
     };
 
-    i32x4 acc[TI][TJ];
+    i32x16 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
     fetch(0);
     stage(0);
@@ -395,19 +400,21 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
         const int buf = kt & 1;
         fetch(kt + 1);  // clamped past the end: re-reads the last tile (staged into an unread buffer)
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
-        const uint8_t* as = &As[buf][(wm * WM + r16) * LDAA + 16 * g];
-        const uint8_t* bs = &Bs[buf][(wn * WN + r16) * LDAA + 16 * g];
+        // A / B fragment of a 32 x 32 x 32 step: lane l holds row (column) l % 32 and the 16
+        // consecutive k values 16 (l / 32) .. + 15 of the step, in both operands alike
+        const uint8_t* as = &As[buf][(wm * WM + r32) * LDAA + 16 * h];
+        const uint8_t* bs = &Bs[buf][(wn * WN + r32) * LDAA + 16 * h];
 #pragma unroll
-        for (int kk = 0; kk < BKA / 64; ++kk) {
+        for (int kk = 0; kk < BKA / 32; ++kk) {
             i32x4 bf[TJ];
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bs + 16 * j * LDAA + 64 * kk);
+            for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bs + 32 * j * LDAA + 32 * kk);
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const i32x4 af = *reinterpret_cast<const i32x4*>(as + 16 * i * LDAA + 64 * kk);
+                const i32x4 af = *reinterpret_cast<const i32x4*>(as + 32 * i * LDAA + 32 * kk);
 #pragma unroll
                 for (int j = 0; j < TJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[i][j], 0, 0, 0);
             }
         }
         // unconditional: a conditional use lets the compiler sink the loads above past the MFMAs;
@@ -417,26 +424,60 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
         __syncthreads();
     }
 
-    {
+    // Epilogue: y = fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]), each operation rounded on its
+    // own.  The int32 tile goes through LDS in two passes of 128 rows (row stride 264 words: rows
+    // 4 apart fall 32 banks apart), then every thread writes 8 consecutive outputs of a row with
+    // 16-byte stores.  Lane l, register r of a 32 x 32 sub-tile holds row 8 (r / 4) + 4 (l / 32) +
+    // r % 4, column l % 32.
+    constexpr int ORW = BNT + 8;  // output staging row stride (words)
+    static_assert(128 * ORW * 4 <= (int)sizeof(smem), "output staging must fit in the operand buffers");
+    int32_t* ot = reinterpret_cast<int32_t*>(smem);
+    const int cc = tid % (BNT / 8);              // this thread's 8-column chunk (the same in every pass)
+    const int64_t nc = n0 + 8 * cc;
+    const int ncount = (int)max<int64_t>(0, min<int64_t>(8, p.N - nc));
+    float sc[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t n = min(nc + e, p.N - 1);
+        sc[e] = p.s_ch[n];
+        bv[e] = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+    }
+    const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
+        if ((wm >> 1) == pass) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        ot[((wm & 1) * WM + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] =
+                            acc[i][j][r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 128 * (BNT / 8) / NT; ++q) {
+            const int row = tid / (BNT / 8) + (NT / (BNT / 8)) * q;
+            const int64_t m = m0 + 128 * pass + row;
+            if (m >= p.M || ncount == 0) continue;
+            const i32x4 a0 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc);
+            const i32x4 a1 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc + 4);
+            const float sxm = p.sx[m];
+            float v[8];
+            {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int64_t n = n0 + wn * WN + 16 * j + r16;
-        if (n >= p.N) continue;
-        const float sc = p.s_ch[n];
-        const float bv = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int64_t m = m0 + wm * WM + 16 * i + 4 * g + v;
-                if (m >= p.M) continue;
-                float val = (float)acc[i][j][v] * p.sx[m];
-                val = val * sc;
-                if (p.bias) val = val + bv;
-                store_rt(p.y, p.y_dtype, m * p.ldy + n, val);
+                for (int e = 0; e < 8; ++e) {
+                    float val = (float)(e < 4 ? a0[e] : a1[e - 4]) * sxm;
+                    val = val * sc[e];
+                    if (p.bias) val = val + bv[e];
+                    v[e] = val;
+                }
             }
-    }
+            store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v, ncount, vec);
+        }
     }
 }
 

@@ -157,6 +157,31 @@ __device__ __forceinline__ void store_rt(void* base, int dtype, int64_t idx, flo
     else if (dtype == 1) reinterpret_cast<f16*>(base)[idx] = (f16)v;
     else reinterpret_cast<uint16_t*>(base)[idx] = f32_to_bf16_bits(v);
 }
+// Eight consecutive outputs v[0..7] at element idx of an output of runtime dtype.  `vec`: the
+// caller has checked that base + idx is 16-byte aligned for this dtype; `count` < 8 stores a
+// ragged row end element by element.
+__device__ __forceinline__ void store8_rt(void* base, int dtype, int64_t idx, const float* v, int count, bool vec) {
+    if (vec && count == 8) {
+        if (dtype == 0) {
+            float* p = reinterpret_cast<float*>(base) + idx;
+            *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+        } else if (dtype == 1) {
+            f16x8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (f16)v[e];
+            *reinterpret_cast<f16x8*>(reinterpret_cast<f16*>(base) + idx) = h;
+        } else {
+            u32x4 b;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                b[e] = (uint32_t)f32_to_bf16_bits(v[2 * e]) | ((uint32_t)f32_to_bf16_bits(v[2 * e + 1]) << 16);
+            *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + idx) = b;
+        }
+        return;
+    }
+    for (int e = 0; e < count; ++e) store_rt(base, dtype, idx + e, v[e]);
+}
 __device__ __forceinline__ float load_rt(const void* base, int dtype, int64_t idx) {
     if (dtype == 0) return reinterpret_cast<const float*>(base)[idx];
     if (dtype == 1) return (float)reinterpret_cast<const f16*>(base)[idx];
