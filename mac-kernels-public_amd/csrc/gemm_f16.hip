@@ -9,6 +9,8 @@
 // Epilogue: y = acc * 2^E[m] * (scale[n] | 2^e[n]) + bias[n], cast to the output dtype.
 // Global->LDS is double-buffered through registers: the next tile's loads are issued before the
 // current tile's MFMAs.
+#include <type_traits>
+
 #include "qlin_internal.h"
 #include "gguf_exact.h"
 
@@ -239,17 +241,23 @@ __device__ __forceinline__ void xcd_tile_f16(int b, int nblocks, int n_m, int n_
 template <int BMT, int BNT, bool DEEP>
 __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     constexpr int NT = 512;
-    constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 16, TJ = WN / 16;
+    constexpr int WM = BMT / 4, WN = BNT / 2;
+    // 32 x 32 x 16 MFMA sub-tiles where the wave tile allows (about 1.6x the throughput of the
+    // 16 x 16 x 32 form here), else 16 x 16 x 32
+    constexpr bool MF32 = WM % 32 == 0 && WN % 32 == 0;
+    constexpr int SUB = MF32 ? 32 : 16, TI = WM / SUB, TJ = WN / SUB;
     constexpr int UA = WBK / 8;                 // 16-byte activation units per row and k-tile
     constexpr int NA = BMT * UA / NT;           // ... per thread
     constexpr int TPR = NT / BNT;               // threads per weight row
     constexpr int VPT = WBK / TPR;              // weight values (bytes) per thread and k-tile
     static_assert(NA >= 1 && TI >= 1 && TJ >= 1 && VPT % 8 == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) f16 As[2][BMT * WLDK];
-    __shared__ __attribute__((aligned(16))) f16 Bs[2][BNT * WLDK];
+    // one LDS block: double-buffered operands in the loop, then the output staging of the epilogue
+    __shared__ __attribute__((aligned(16))) f16 smem[2 * (BMT + BNT) * WLDK];
+    f16 (*As)[BMT * WLDK] = reinterpret_cast<f16 (*)[BMT * WLDK]>(smem);
+    f16 (*Bs)[BNT * WLDK] = reinterpret_cast<f16 (*)[BNT * WLDK]>(smem + 2 * BMT * WLDK);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int r16 = lane & 15, g = lane >> 4;
+    const int r16 = lane & 15, g = lane >> 4, r32 = lane & 31, h32 = lane >> 5;
     int mt, nt;
     xcd_tile_f16(blockIdx.x, (int)gridDim.x, (int)((a.M + BMT - 1) / BMT), (int)((a.N + BNT - 1) / BNT), mt, nt);
     const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
@@ -300,25 +308,48 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
         }
     };
 
-    f32x4 acc[TI][TJ];
+    typedef typename std::conditional<MF32, f32x16, f32x4>::type Acc;
+    Acc acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < (MF32 ? 16 : 4); ++r) acc[i][j][r] = 0.f;
     auto compute = [&](int buf) {
-        const f16* as = &As[buf][(wm * WM + r16) * WLDK + 8 * g];
-        const f16* bs = &Bs[buf][(wn * WN + r16) * WLDK + 8 * g];
+        if constexpr (MF32) {
+            // lane l holds row (column) l % 32 and the 8 consecutive k 8 (l / 32) .. + 7 of a
+            // 16-value step, in both operands alike
+            const f16* as = &As[buf][(wm * WM + r32) * WLDK + 8 * h32];
+            const f16* bs = &Bs[buf][(wn * WN + r32) * WLDK + 8 * h32];
 #pragma unroll
-        for (int kk = 0; kk < WBK / 32; ++kk) {
-            f16x8 bf[TJ];
+            for (int kk = 0; kk < WBK / 16; ++kk) {
+                f16x8 bf[TJ];
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + 16 * j * WLDK + 32 * kk);
+                for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + 32 * j * WLDK + 16 * kk);
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const f16x8 af = *reinterpret_cast<const f16x8*>(as + 16 * i * WLDK + 32 * kk);
+                for (int i = 0; i < TI; ++i) {
+                    const f16x8 af = *reinterpret_cast<const f16x8*>(as + 32 * i * WLDK + 16 * kk);
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        } else {
+            const f16* as = &As[buf][(wm * WM + r16) * WLDK + 8 * g];
+            const f16* bs = &Bs[buf][(wn * WN + r16) * WLDK + 8 * g];
+#pragma unroll
+            for (int kk = 0; kk < WBK / 32; ++kk) {
+                f16x8 bf[TJ];
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const f16x8*>(bs + 16 * j * WLDK + 32 * kk);
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const f16x8 af = *reinterpret_cast<const f16x8*>(as + 16 * i * WLDK + 32 * kk);
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+                }
             }
         }
     };
@@ -358,22 +389,57 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
         }
     }
 
-    // acc[i][j][v] = D[m = wm*WM + 16i + 4g + v][n = wn*WN + 16j + r16]
+    // Epilogue: y = ldexp(acc, xexp[m]) * scale[n] + bias[n].  The fp32 tile goes through LDS in
+    // passes of RP rows (row stride BNT + 8 words), then every thread writes 8 consecutive outputs of
+    // a row with 16-byte stores.  32 x 32 sub-tiles: lane l, register r holds row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32; 16 x 16: row 4 (l / 16) + r, column l % 16.
+    constexpr int ORW = BNT + 8;
+    constexpr int RP = (BMT * ORW * 4 <= (int)sizeof(smem)) ? BMT : BMT / 2;
+    static_assert(RP * ORW * 4 <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
+    constexpr int CPR = BNT / 8;                 // 8-column chunks per row
+    static_assert(NT % CPR == 0 && (RP * CPR) % NT == 0, "chunks must split evenly");
+    float* ot = reinterpret_cast<float*>(smem);
+    const int cc = tid % CPR;                    // this thread's chunk (the same in every pass)
+    const int64_t nc = n0 + 8 * cc;
+    const int ncount = (int)max<int64_t>(0, min<int64_t>(8, a.N - nc));
+    float cs[8], bv[8];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int64_t n = n0 + wn * WN + 16 * j + r16;
-        if (n >= a.N) continue;
-        const float cs = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-        const float bv = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+    for (int e = 0; e < 8; ++e) {
+        const int64_t n = min(nc + e, a.N - 1);
+        cs[e] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+        bv[e] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+    }
+    const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+    for (int pass = 0; pass < BMT / RP; ++pass) {
+        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
+        if ((wm * WM) / RP == pass) {
+            const int rw = wm * WM - pass * RP;  // this wave's first row in the staging block
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int64_t m = m0 + wm * WM + 16 * i + 4 * g + v;
-                if (m >= a.M) continue;
-                float val = a.xexp ? __builtin_ldexpf(acc[i][j][v], a.xexp[m]) : acc[i][j][v];
-                store_rt(a.y, a.y_dtype, m * a.ldy + n, val * cs + bv);
-            }
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < (MF32 ? 16 : 4); ++r) {
+                        const int row = MF32 ? rw + 32 * i + 8 * (r / 4) + 4 * h32 + r % 4 : rw + 16 * i + 4 * g + r;
+                        const int col = MF32 ? wn * WN + 32 * j + r32 : wn * WN + 16 * j + r16;
+                        ot[row * ORW + col] = acc[i][j][r];
+                    }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < RP * CPR / NT; ++q) {
+            const int row = tid / CPR + (NT / CPR) * q;
+            const int64_t m = m0 + pass * RP + row;
+            if (m >= a.M || ncount == 0) continue;
+            const f32x4 v0 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc);
+            const f32x4 v1 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc + 4);
+            const int e2 = a.xexp ? a.xexp[m] : 0;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
+            store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
+        }
     }
 }
 
