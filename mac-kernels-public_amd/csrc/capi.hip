@@ -142,7 +142,9 @@ size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
     return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
            (S > 1 ? align_up((size_t)S * M * N * 4) : 0);
 }
-size_t ws_w4a8(int64_t M, int64_t K) { return align_up((size_t)(M * K)) + align_up((size_t)M * 4); }
+size_t ws_w4a8(int64_t M, int64_t N, int64_t K) {
+    return align_up((size_t)(M * K)) + align_up((size_t)M * 4) + (a8_decode_once(M, K) ? align_up((size_t)(N * K)) : 0);
+}
 
 // Runs the weight-only prologue unless x is already usable as the fp16 MFMA operand (fp16, no
 // rotation, aligned rows), in which case x itself is used and no exponents are needed.
@@ -197,7 +199,7 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
     (void)x_dtype;
     switch (op) {
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
-        case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, K);
+        case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K);
         case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param);
     }
     return 0;
@@ -379,7 +381,8 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     int bdt;
     if ((s = check_bias(bias, N, bdt))) return s;
     const int64_t M = X.rows;
-    if (workspace_bytes < ws_w4a8(M, K)) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_w4a8(M, K));
+    if (workspace_bytes < ws_w4a8(M, N, K))
+        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_w4a8(M, N, K));
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
@@ -403,6 +406,7 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     g.s_ch = (const float*)s_channel->data; g.codebook = cb;
     g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
     g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
+    if (a8_decode_once(M, K)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
     return hip_status(run_gemm_i8(g, st), "A8 gemm");
 }
 

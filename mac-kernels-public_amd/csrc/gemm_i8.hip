@@ -313,17 +313,38 @@ __device__ __forceinline__ void xcd_tile(int b, int nblocks, int n_m, int n_n, i
 // 512 threads = 8 waves, 4 (M) x 2 (N) of 64 x 128; tile 256 x 256 x 128 (int8).
 constexpr int BKA = 128, LDAA = BKA + 16;  // k-tile and LDS row stride (bytes)
 
-template <int BITS, bool CB, typename TSrel>
+// Wait until at most n vector-memory operations of this wave are outstanding (the LDS DMA of the
+// activation tile counts as one); other counters are left alone.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (lds wave-uniform).
+__device__ __forceinline__ void lds_dma16(const int8_t* g, uint8_t* lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+// Workgroup barrier that orders LDS only (a plain __syncthreads also waits for every global load
+// in flight).  LDS DMA writes are covered by an explicit wait_vmcnt before it.
+__device__ __forceinline__ void lds_barrier_i8() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int BITS, bool CB, typename TSrel, bool PAIR>
 __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
     constexpr int BMT = 256, BNT = 256, NT = 512;
     // v_mfma_i32_32x32x32_i8 sub-tiles (about 1.6x the throughput of the 16x16x64 form here)
     constexpr int WM = 64, WN = 128, TI = WM / 32, TJ = WN / 32;
-    constexpr int NA = BMT * (BKA / 16) / NT;  // 16-byte activation units per thread and k-tile
-    constexpr int UA = BKA / 16;              // ... per activation row
+    constexpr int NA = BMT * (BKA / 16) / NT;  // 16-byte activation chunks per thread and k-tile
+    constexpr int ASZ = BMT * BKA;             // activation tile bytes (rows of 128 bytes, swizzled)
     // one LDS block: double-buffered operands in the loop, then the output staging of the epilogue
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (BMT + BNT) * LDAA];
-    uint8_t (*As)[BMT * LDAA] = reinterpret_cast<uint8_t (*)[BMT * LDAA]>(smem);
-    uint8_t (*Bs)[BNT * LDAA] = reinterpret_cast<uint8_t (*)[BNT * LDAA]>(smem + 2 * BMT * LDAA);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * ASZ + 2 * BNT * LDAA];
+    uint8_t (*As)[ASZ] = reinterpret_cast<uint8_t (*)[ASZ]>(smem);
+    uint8_t (*Bs)[BNT * LDAA] = reinterpret_cast<uint8_t (*)[BNT * LDAA]>(smem + 2 * ASZ);
     __shared__ float cb_s[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -343,43 +364,49 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
     const int br = tid >> 1, bh = tid & 1;
     const int64_t nrow = min(n0 + br, p.N - 1);
     const uint8_t* wrow = p.q + nrow * p.ldq;
-    // activation row pointers and the scale row do not change along K
-    const int8_t* arow[NA];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-        const int u = tid + NT * i;
-        arow[i] = p.xq + min(m0 + u / UA, p.M - 1) * p.ldx + 16 * (u % UA);
-    }
     const int gsh = p.group_size / 64;  // 64-value halves per scale group
     const void* srow = nullptr;
     if constexpr (sizeof(TSrel) == 1) srow = (const uint8_t*)p.s_rel + nrow * p.ld_srel;
     else srow = (const TSrel*)p.s_rel + nrow * p.ld_srel;
 
-    u32x4 ra[NA];
-    uint32_t rn[8], rh[4], rs;
-    auto fetch = [&](int kt) {
-        kt = min(kt, ktiles - 1);
-        const int k0 = kt * BKA;
+    // Activation tile: LDS DMA (global_load_lds, 16 bytes per lane) into rows of 128 bytes whose
+    // 16-byte chunks are XOR-swizzled by (row / 2) % 8, so that the 32-row fragment reads below hit
+    // 16 different bank groups per 16 lanes.  DMA instruction i of wave w fills physical chunks
+    // 512 i + 64 w + lane, i.e. row 64 i + 8 w + lane / 8, physical chunk lane % 8, which holds
+    // logical chunk (lane % 8) ^ ((4 w + lane / 16) % 8).  Rows past M re-read row M - 1.
+    const int8_t* asrc[NA];
 #pragma unroll
-        for (int i = 0; i < NA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + k0);
+    for (int i = 0; i < NA; ++i) {
+        const int row = 64 * i + 8 * wave + (lane >> 3);
+        const int c = (lane & 7) ^ ((4 * wave + (lane >> 4)) & 7);
+        asrc[i] = p.xq + min(m0 + row, p.M - 1) * p.ldx + 16 * c;
+    }
+    auto fetch_a = [&](int kt, int buf) {
+        const int k0 = min(kt, ktiles - 1) * BKA;
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_global_load_lds(asrc[i] + k0, &As[buf][16 * (512 * i + 64 * wave)], 16, 0, 0);
+    };
+    struct Regs {
+        uint32_t n[8], hh[4], s;
+    };
+    constexpr int NB = (BITS == 6) ? 4 : 3;  // vector-memory operations per fetch_b
+    auto fetch_b = [&](int kt, Regs& R) {
+        kt = min(kt, ktiles - 1);  // past the end: re-reads the last tile (never staged for use)
+        const int k0 = kt * BKA;
         const uint8_t* pn = wrow + k0 / 2 + 32 * bh;
         const u32x4 n_0 = *reinterpret_cast<const u32x4*>(pn), n_1 = *reinterpret_cast<const u32x4*>(pn + 16);
-        rn[0] = n_0.x; rn[1] = n_0.y; rn[2] = n_0.z; rn[3] = n_0.w;
-        rn[4] = n_1.x; rn[5] = n_1.y; rn[6] = n_1.z; rn[7] = n_1.w;
+        R.n[0] = n_0.x; R.n[1] = n_0.y; R.n[2] = n_0.z; R.n[3] = n_0.w;
+        R.n[4] = n_1.x; R.n[5] = n_1.y; R.n[6] = n_1.z; R.n[7] = n_1.w;
         if constexpr (BITS == 6) {
             const u32x4 hv = *reinterpret_cast<const u32x4*>(wrow + p.K / 2 + k0 / 4 + 16 * bh);
-            rh[0] = hv.x; rh[1] = hv.y; rh[2] = hv.z; rh[3] = hv.w;
+            R.hh[0] = hv.x; R.hh[1] = hv.y; R.hh[2] = hv.z; R.hh[3] = hv.w;
         }
-        rs = srel_bits<TSrel>(srow, (unsigned)(2 * kt + bh) / (unsigned)gsh);
+        R.s = srel_bits<TSrel>(srow, (unsigned)(2 * kt + bh) / (unsigned)gsh);
     };
-    auto stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            const int u = tid + NT * i;
-            *reinterpret_cast<u32x4*>(&As[buf][(u / UA) * LDAA + 16 * (u % UA)]) = ra[i];
-        }
+    auto stage_b = [&](int buf, const Regs& R) {
         uint32_t o[16];
-        decode64<BITS, CB>(rn, rh, srel_from_bits<TSrel>(rs), cb, bh, gsh >= 2, o);
+        decode64<BITS, CB>(R.n, R.hh, srel_from_bits<TSrel>(R.s), cb, bh, PAIR, o);
         u32x4* pb = reinterpret_cast<u32x4*>(&Bs[buf][br * LDAA + 64 * bh]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) pb[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
@@ -392,36 +419,76 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
         for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int buf = kt & 1;
-        fetch(kt + 1);  // clamped past the end: re-reads the last tile (staged into an unread buffer)
-        __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
-        // A / B fragment of a 32 x 32 x 32 step: lane l holds row (column) l % 32 and the 16
-        // consecutive k values 16 (l / 32) .. + 15 of the step, in both operands alike
-        const uint8_t* as = &As[buf][(wm * WM + r32) * LDAA + 16 * h];
+    // A / B fragment of a 32 x 32 x 32 step: lane l holds row (column) l % 32 and the 16
+    // consecutive k values 16 (l / 32) .. + 15 of the step, in both operands alike
+    const int asw = (r32 >> 1) & 7;  // swizzle of this lane's activation rows
+    auto mfmas = [&](int buf) {
+        const uint8_t* as = &As[buf][(wm * WM + r32) * BKA];
         const uint8_t* bs = &Bs[buf][(wn * WN + r32) * LDAA + 16 * h];
 #pragma unroll
         for (int kk = 0; kk < BKA / 32; ++kk) {
             i32x4 bf[TJ];
 #pragma unroll
             for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bs + 32 * j * LDAA + 32 * kk);
+            const int ac = 16 * ((2 * kk + h) ^ asw);
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const i32x4 af = *reinterpret_cast<const i32x4*>(as + 32 * i * LDAA + 32 * kk);
+                const i32x4 af = *reinterpret_cast<const i32x4*>(as + 32 * i * BKA + ac);
 #pragma unroll
                 for (int j = 0; j < TJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[i][j], 0, 0, 0);
             }
         }
-        // unconditional: a conditional use lets the compiler sink the loads above past the MFMAs;
-        // and after them: staging waits for those loads, so it must not move ahead of the MFMAs
+    };
+    // Schedule of one k-tile: the first fragment reads, then each MFMA followed by seven VALU
+    // instructions (the next tile's weight decode), the next 32-k step's fragment reads spread over
+    // the MFMAs, the LDS writes last.
+    auto interleave = [&]() {
+        constexpr int FR = TI + TJ;  // fragment reads per 32-k step
+        __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);
+#pragma unroll
+        for (int kk = 0; kk < BKA / 32; ++kk)
+#pragma unroll
+            for (int m = 0; m < TI * TJ; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+                if (kk + 1 < BKA / 32 && m < FR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);
+    };
+
+    // Iteration kt: the activation DMA of tile kt + 1 and the weight loads of tile kt + 2 go out
+    // first; tile kt's MFMAs share a basic block with the decode of tile kt + 1's weights (loaded one
+    // iteration earlier); the barrier waits for the DMA only.  Two weight register sets alternate
+    // (the loop is unrolled by two).
+    Regs R0, R1;
+    fetch_a(0, 0);
+    fetch_b(0, R0);
+    fetch_b(1, R1);
+    wait_vmcnt<NB>();  // tile 0 (DMA and weights) has landed
+    stage_b(0, R0);
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; kt += 2) {
+        fetch_a(kt + 1, 1);
+        __builtin_amdgcn_sched_barrier(0);  // the DMA is older than the weight loads (wait_vmcnt<NB>)
+        fetch_b(kt + 2, R0);  // R0's tile is staged already
         __builtin_amdgcn_sched_barrier(0);
-        stage(buf ^ 1);
-        __syncthreads();
+        mfmas(0);
+        stage_b(1, R1);
+        interleave();
+        wait_vmcnt<NB>();
+        lds_barrier_i8();
+        if (kt + 1 < ktiles) {  // uniform
+            fetch_a(kt + 2, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_b(kt + 3, R1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(1);
+            stage_b(0, R0);
+            interleave();
+            wait_vmcnt<NB>();
+            lds_barrier_i8();
+        }
     }
 
     // Epilogue: y = fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]), each operation rounded on its
@@ -481,14 +548,216 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Decode-once path for many activation rows (M >= 1024): the int8 weight grid is decoded once
+// into the workspace (the same decode64 as the fused kernel), then a plain int8 x int8 GEMM reads
+// both operands with LDS DMA.  The fused kernel decodes every weight once per 256-row M-tile;
+// here the decode VALU work leaves the GEMM loop, whose MFMAs interleave with fragment reads only.
+// ------------------------------------------------------------------------------------------------
+
+// One thread per (weight row, 64-code segment): w8[n][64 s .. 64 s + 63].  Needs group_size % 64 == 0.
+template <int BITS, bool CB, typename TSrel>
+__global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __restrict__ w8) {
+    const int64_t segs = p.K / 64;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= p.N * segs) return;
+    const int64_t n = t / segs;
+    const int sg = (int)(t % segs);
+    const uint8_t* row = p.q + n * p.ldq;
+    uint32_t nib[8], hi2[4] = {0, 0, 0, 0};
+    const u32x4 n_0 = *reinterpret_cast<const u32x4*>(row + 32 * sg), n_1 = *reinterpret_cast<const u32x4*>(row + 32 * sg + 16);
+    nib[0] = n_0.x; nib[1] = n_0.y; nib[2] = n_0.z; nib[3] = n_0.w;
+    nib[4] = n_1.x; nib[5] = n_1.y; nib[6] = n_1.z; nib[7] = n_1.w;
+    if constexpr (BITS == 6) {
+        const u32x4 hv = *reinterpret_cast<const u32x4*>(row + p.K / 2 + 16 * sg);
+        hi2[0] = hv.x; hi2[1] = hv.y; hi2[2] = hv.z; hi2[3] = hv.w;
+    }
+    const void* srow;
+    if constexpr (sizeof(TSrel) == 1) srow = (const uint8_t*)p.s_rel + n * p.ld_srel;
+    else srow = (const TSrel*)p.s_rel + n * p.ld_srel;
+    const float sv = srel_from_bits<TSrel>(srel_bits<TSrel>(srow, (unsigned)(64 * sg) / (unsigned)p.group_size));
+    uint32_t o[16];
+    decode64<BITS, CB>(nib, hi2, sv, p.codebook, 0, false, o);
+    u32x4* dst = reinterpret_cast<u32x4*>(w8 + n * p.K + 64 * sg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+}
+
+// int8 GEMM y = epilogue(xq[M, K] . w8[N, K]^T), tile BMT x BNT x 128, 8 waves 4 (M) x 2 (N),
+// v_mfma_i32_32x32x32_i8.  Both operand tiles arrive by LDS DMA into 128-byte rows whose 16-byte
+// chunks are XOR-swizzled by (row / 2) % 8 (double buffered); each k-tile's DMA goes out before
+// the previous tile's MFMAs.
+template <int BMT, int BNT>
+__global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int8_t* __restrict__ w8) {
+    constexpr int NT = 512, BK = 128;
+    constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
+    static_assert(TI >= 1 && TJ >= 1 && BMT % 64 == 0 && BNT % 64 == 0, "tile shape");
+    constexpr int ASZ = BMT * BK, BSZ = BNT * BK;  // bytes per buffer
+    constexpr int NA = BMT / 64, NB = BNT / 64;     // DMA instructions per thread and k-tile
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (ASZ + BSZ)];
+    uint8_t (*buf_of)[ASZ + BSZ] = reinterpret_cast<uint8_t (*)[ASZ + BSZ]>(smem);  // [buffer][A | B]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r32 = lane & 31, h = lane >> 5;
+    int mt, nt;
+    xcd_tile(blockIdx.x, (int)gridDim.x, (int)((p.M + BMT - 1) / BMT), (int)((p.N + BNT - 1) / BNT), mt, nt);
+    const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
+    const int ktiles = (int)(p.K / BK);
+
+    // DMA instruction i of wave w fills physical chunks 512 i + 64 w + lane of a buffer: row
+    // 64 i + 8 w + lane / 8, physical chunk lane % 8 = logical chunk (lane % 8) ^ ((4 w + lane / 16) % 8).
+    // Rows past M (N) re-read row M - 1 (N - 1) and are never stored.
+    const int c_l = (lane & 7) ^ ((4 * wave + (lane >> 4)) & 7);
+    const int8_t* asrc[NA];
+    const int8_t* bsrc[NB];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) asrc[i] = p.xq + min(m0 + 64 * i + 8 * wave + (lane >> 3), p.M - 1) * p.ldx + 16 * c_l;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) bsrc[i] = w8 + min(n0 + 64 * i + 8 * wave + (lane >> 3), p.N - 1) * p.K + 16 * c_l;
+    auto dma = [&](int kt, int buf) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) lds_dma16(asrc[i] + k0, &buf_of[buf][16 * (512 * i + 64 * wave)]);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) lds_dma16(bsrc[i] + k0, &buf_of[buf][ASZ + 16 * (512 * i + 64 * wave)]);
+    };
+
+    i32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    // fragments: lane l holds row (column) l % 32 and k 16 (l / 32) .. + 15 of a 32-k step in both
+    // operands; rows wm * WM + 32 i + l % 32 share the swizzle (l % 32 / 2) % 8
+    const int sw = (r32 >> 1) & 7;
+    auto mfmas = [&](int buf) {
+        const uint8_t* as = &buf_of[buf][(wm * WM + r32) * BK];
+        const uint8_t* bs = &buf_of[buf][ASZ + (wn * WN + r32) * BK];
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            const int c = 16 * ((2 * kk + h) ^ sw);
+            i32x4 bf[TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) bf[j] = *reinterpret_cast<const i32x4*>(bs + 32 * j * BK + c);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                const i32x4 af = *reinterpret_cast<const i32x4*>(as + 32 * i * BK + c);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        // the first step's fragments, then each MFMA with one of the next step's fragment reads
+        constexpr int FR = TI + TJ;
+        __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk)
+#pragma unroll
+            for (int m = 0; m < TI * TJ; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (kk + 1 < BK / 32 && m < FR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+    };
+
+    dma(0, 0);
+    wait_vmcnt<0>();
+    lds_barrier_i8();
+    for (int kt = 0; kt < ktiles; ++kt) {
+        dma(kt + 1, (kt + 1) & 1);  // past the end: re-reads the last tile into the unused buffer
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(kt & 1);
+        wait_vmcnt<0>();
+        lds_barrier_i8();
+    }
+
+    // Epilogue: y = fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]), each operation rounded on its
+    // own, staged through LDS in passes of RP rows and written as 16-byte row pieces.  Lane l,
+    // register r of a 32 x 32 sub-tile holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+    constexpr int ORW = BNT + 8;
+    constexpr int RP = (BMT * ORW * 4 <= (int)sizeof(smem)) ? BMT
+                       : (BMT / 2 * ORW * 4 <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
+    static_assert(RP * ORW * 4 <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
+    constexpr int CPR = BNT / 8;
+    static_assert(NT % CPR == 0 && (RP * CPR) % NT == 0, "chunks must split evenly");
+    int32_t* ot = reinterpret_cast<int32_t*>(smem);
+    const int cc = tid % CPR;
+    const int64_t nc = n0 + 8 * cc;
+    const int ncount = (int)max<int64_t>(0, min<int64_t>(8, p.N - nc));
+    float sc[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t n = min(nc + e, p.N - 1);
+        sc[e] = p.s_ch[n];
+        bv[e] = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+    }
+    const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
+#pragma unroll
+    for (int pass = 0; pass < BMT / RP; ++pass) {
+        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
+        if ((wm * WM) / RP == pass) {
+            const int rw = wm * WM - pass * RP;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        ot[(rw + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] = acc[i][j][r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < RP * CPR / NT; ++q) {
+            const int row = tid / CPR + (NT / CPR) * q;
+            const int64_t m = m0 + pass * RP + row;
+            if (m >= p.M || ncount == 0) continue;
+            const i32x4 a0 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc);
+            const i32x4 a1 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc + 4);
+            const float sxm = p.sx[m];
+            float v[8];
+            {
+#pragma clang fp contract(off)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float val = (float)(e < 4 ? a0[e] : a1[e - 4]) * sxm;
+                    val = val * sc[e];
+                    if (p.bias) val = val + bv[e];
+                    v[e] = val;
+                }
+            }
+            store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v, ncount, vec);
+        }
+    }
+}
+
 template <int BITS, bool CB, typename TSrel>
 hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if (p.w8 && a8_decode_once(p.M, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
+        (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0) {
+        const int64_t segs = p.N * (p.K / 64);
+        hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, TSrel>), dim3((unsigned)((segs + 255) / 256)), dim3(256), 0, st,
+                           p, p.w8);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
+        if (tiles(256, 256) >= 192)
+            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p, p.w8);
+        else if (tiles(128, 256) >= 192)
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p, p.w8);
+        else
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 128>), dim3((unsigned)tiles(128, 128)), dim3(512), 0, st, p, p.w8);
+        return hipGetLastError();
+    }
     // large tiles when the grid still fills the GPU and one scale covers each row's k-tile
     const int64_t big_tiles = ((p.N + 255) / 256) * ((p.M + 255) / 256);
     if (p.group_size % 64 == 0 && p.K % BKA == 0 && p.ldq % 16 == 0 && big_tiles >= 192) {
         dim3 grid((unsigned)big_tiles), block(512);
-        hipLaunchKernelGGL((gemm_a8_kernel<BITS, CB, TSrel>), grid, block, 0, st, p);
+        if (p.group_size >= 128)  // one scale per k-tile row: the decoding thread pair shares its table
+            hipLaunchKernelGGL((gemm_a8_kernel<BITS, CB, TSrel, true>), grid, block, 0, st, p);
+        else
+            hipLaunchKernelGGL((gemm_a8_kernel<BITS, CB, TSrel, false>), grid, block, 0, st, p);
         return hipGetLastError();
     }
     dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM)), block(256);

@@ -133,7 +133,11 @@ struct GemmI8Args {
     void* y = nullptr;
     int y_dtype = DT_F16;
     int64_t ldy = 0;
+    int8_t* w8 = nullptr;            // workspace for the decoded int8 grid [N, K] (decode-once path)
 };
+// Activation rows from which the A8 linear decodes the weight grid once into the workspace
+// (N * K bytes) instead of once per 256-row tile inside the GEMM.
+inline bool a8_decode_once(int64_t M, int64_t K) { return M >= 1024 && K % 128 == 0; }
 hipError_t run_gemm_i8(const GemmI8Args& a, hipStream_t st);
 
 // ---- standalone decodes (dequant.hip) ----
