@@ -583,18 +583,22 @@ __global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __re
     for (int i = 0; i < 4; ++i) dst[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
 }
 
-// int8 GEMM y = epilogue(xq[M, K] . w8[N, K]^T), tile BMT x BNT x 128, 8 waves 4 (M) x 2 (N),
-// v_mfma_i32_32x32x32_i8.  Both operand tiles arrive by LDS DMA into 128-byte rows whose 16-byte
-// chunks are XOR-swizzled by (row / 2) % 8 (double buffered); each k-tile's DMA goes out before
-// the previous tile's MFMAs.
-template <int BMT, int BNT>
+// int8 GEMM y = epilogue(xq[M, K] . w8[N, K]^T), tile BMT x BNT x BK, 8 waves 4 (M) x 2 (N),
+// v_mfma_i32_32x32x32_i8.  Both operand tiles arrive by LDS DMA into rows of BK bytes whose 16-byte
+// chunks are XOR-swizzled (so that the 16 rows a fragment read touches fall in 16 bank groups),
+// in STAGES buffers: the DMA of k-tile kt + STAGES - 1 goes out before tile kt's MFMAs, and each
+// step waits only for the oldest DMA in flight.
+template <int BMT, int BNT, int BK, int STAGES>
 __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int8_t* __restrict__ w8) {
-    constexpr int NT = 512, BK = 128;
+    constexpr int NT = 512;
     constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
-    static_assert(TI >= 1 && TJ >= 1 && BMT % 64 == 0 && BNT % 64 == 0, "tile shape");
-    constexpr int ASZ = BMT * BK, BSZ = BNT * BK;  // bytes per buffer
-    constexpr int NA = BMT / 64, NB = BNT / 64;     // DMA instructions per thread and k-tile
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * (ASZ + BSZ)];
+    static_assert(TI >= 1 && TJ >= 1 && (BK == 64 || BK == 128), "tile shape");
+    constexpr int CPRW = BK / 16;                   // 16-byte chunks per row
+    constexpr int RPS = 16 / CPRW;                  // rows per swizzle step
+    constexpr int ASZ = BMT * BK, BSZ = BNT * BK;   // bytes per buffer
+    constexpr int NA = ASZ / 16 / NT, NB = BSZ / 16 / NT;  // DMA instructions per thread and k-tile
+    static_assert(NA * 16 * NT == ASZ && NB * 16 * NT == BSZ, "tile must split into whole DMA rounds");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ)];
     uint8_t (*buf_of)[ASZ + BSZ] = reinterpret_cast<uint8_t (*)[ASZ + BSZ]>(smem);  // [buffer][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -605,15 +609,18 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     const int ktiles = (int)(p.K / BK);
 
     // DMA instruction i of wave w fills physical chunks 512 i + 64 w + lane of a buffer: row
-    // 64 i + 8 w + lane / 8, physical chunk lane % 8 = logical chunk (lane % 8) ^ ((4 w + lane / 16) % 8).
-    // Rows past M (N) re-read row M - 1 (N - 1) and are never stored.
-    const int c_l = (lane & 7) ^ ((4 * wave + (lane >> 4)) & 7);
+    // (512 i + 64 w + lane) / CPRW, physical chunk lane % CPRW, which holds logical chunk
+    // (lane % CPRW) ^ ((row / RPS) % CPRW) -- the same for every i.  Rows past M (N) re-read row
+    // M - 1 (N - 1) and are never stored.
+    const int c_l = (lane % CPRW) ^ (((64 * wave + lane) / CPRW / RPS) % CPRW);
     const int8_t* asrc[NA];
     const int8_t* bsrc[NB];
 #pragma unroll
-    for (int i = 0; i < NA; ++i) asrc[i] = p.xq + min(m0 + 64 * i + 8 * wave + (lane >> 3), p.M - 1) * p.ldx + 16 * c_l;
+    for (int i = 0; i < NA; ++i)
+        asrc[i] = p.xq + min(m0 + (512 * i + 64 * wave + lane) / CPRW, p.M - 1) * p.ldx + 16 * c_l;
 #pragma unroll
-    for (int i = 0; i < NB; ++i) bsrc[i] = w8 + min(n0 + 64 * i + 8 * wave + (lane >> 3), p.N - 1) * p.K + 16 * c_l;
+    for (int i = 0; i < NB; ++i)
+        bsrc[i] = w8 + min(n0 + (512 * i + 64 * wave + lane) / CPRW, p.N - 1) * p.K + 16 * c_l;
     auto dma = [&](int kt, int buf) {
         const int k0 = min(kt, ktiles - 1) * BK;
 #pragma unroll
@@ -630,8 +637,8 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
     // fragments: lane l holds row (column) l % 32 and k 16 (l / 32) .. + 15 of a 32-k step in both
-    // operands; rows wm * WM + 32 i + l % 32 share the swizzle (l % 32 / 2) % 8
-    const int sw = (r32 >> 1) & 7;
+    // operands; rows wm * WM + 32 i + l % 32 share the swizzle (l % 32 / RPS) % CPRW
+    const int sw = (r32 / RPS) % CPRW;
     auto mfmas = [&](int buf) {
         const uint8_t* as = &buf_of[buf][(wm * WM + r32) * BK];
         const uint8_t* bs = &buf_of[buf][ASZ + (wn * WN + r32) * BK];
@@ -661,16 +668,22 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
             }
     };
 
-    dma(0, 0);
-    wait_vmcnt<0>();
-    lds_barrier_i8();
+    // Barrier without a memory fence: the DMA data this wave needs is covered by wait_vmcnt, and
+    // the loop writes LDS only by DMA.
+    constexpr int ND = NA + NB;  // DMA instructions per k-tile and thread
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st) dma(st, st);
+    wait_vmcnt<(STAGES - 2) * ND>();
+    __builtin_amdgcn_s_barrier();
     for (int kt = 0; kt < ktiles; ++kt) {
-        dma(kt + 1, (kt + 1) & 1);  // past the end: re-reads the last tile into the unused buffer
+        // past the end: re-reads the last tile into a buffer no step reads
+        dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(kt & 1);
-        wait_vmcnt<0>();
-        lds_barrier_i8();
+        mfmas(kt % STAGES);
+        wait_vmcnt<(STAGES - 2) * ND>();  // tile kt + 1 has landed
+        __builtin_amdgcn_s_barrier();
     }
+    wait_vmcnt<0>();
 
     // Epilogue: y = fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]), each operation rounded on its
     // own, staged through LDS in passes of RP rows and written as 16-byte row pieces.  Lane l,
@@ -743,11 +756,14 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         if (err != hipSuccess) return err;
         auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
         if (tiles(256, 256) >= 192)
-            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p, p.w8);
+            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p,
+                               p.w8);
         else if (tiles(128, 256) >= 192)
-            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p, p.w8);
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p,
+                               p.w8);
         else
-            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 128>), dim3((unsigned)tiles(128, 128)), dim3(512), 0, st, p, p.w8);
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 128, 128, 2>), dim3((unsigned)tiles(128, 128)), dim3(512), 0, st, p,
+                               p.w8);
         return hipGetLastError();
     }
     // large tiles when the grid still fills the GPU and one scale covers each row's k-tile
