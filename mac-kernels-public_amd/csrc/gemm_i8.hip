@@ -313,19 +313,6 @@ __device__ __forceinline__ void xcd_tile(int b, int nblocks, int n_m, int n_n, i
 // 512 threads = 8 waves, 4 (M) x 2 (N) of 64 x 128; tile 256 x 256 x 128 (int8).
 constexpr int BKA = 128, LDAA = BKA + 16;  // k-tile and LDS row stride (bytes)
 
-// Wait until at most n vector-memory operations of this wave are outstanding (the LDS DMA of the
-// activation tile counts as one); other counters are left alone.
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
-}
-
-// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (lds wave-uniform).
-__device__ __forceinline__ void lds_dma16(const int8_t* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
-}
-
 // Workgroup barrier that orders LDS only (a plain __syncthreads also waits for every global load
 // in flight).  LDS DMA writes are covered by an explicit wait_vmcnt before it.
 __device__ __forceinline__ void lds_barrier_i8() {

@@ -200,6 +200,19 @@ __device__ __forceinline__ float bits_to_f32_rt(uint32_t bits, int dtype) {
     return bf16_bits_to_f32((uint16_t)bits);
 }
 
+// Wait until at most n vector-memory operations of this wave are outstanding (an LDS DMA counts as
+// one); the other counters are left alone.
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+}
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (lds wave-uniform).
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
 __device__ __forceinline__ float load_f(const float* p) { return *p; }
 __device__ __forceinline__ float load_f(const f16* p) { return (float)*p; }
 __device__ __forceinline__ float load_f(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
