@@ -10,9 +10,10 @@
 //   * per stage (SV values) the activation slice is loaded once, 16 bytes per lane with 512 or
 //     1024 contiguous bytes per row, into LDS (rows padded by 16 bytes so the fragment reads are
 //     conflict-free), and all eight waves read their MFMA A fragments from there;
-//   * each wave stages its own 16 weight rows through LDS and decodes them with the policies the
-//     small-M kernel uses (exact fp16 integers, fp32 scales), reusing each B fragment for its MT
-//     m-tiles;
+//   * the eight waves form four pairs; a pair owns 32 weight rows (two 16-row n-tiles), stages them
+//     through LDS and splits each stage's K range in halves, one per wave.  A wave decodes with
+//     the policies the small-M kernel uses (exact fp16 integers, fp32 scales) and reuses each B
+//     fragment for its MT m-tiles; the two halves' accumulators are added through LDS at the end;
 //   * the next stage's activations and weights are in flight while a stage is computed;
 //   * S > 1: each workgroup stores its fp32 partial tile to the workspace ([S][M][N]) and a second
 //     kernel adds the S partials in split order (the result does not depend on timing) and applies

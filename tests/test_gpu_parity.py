@@ -377,14 +377,27 @@ def test_w4a8_linear(bits, gs, cb, srdt, m):
     check_linear(yb, want + b.numpy()[None, :].astype(np.float64), "bias")
 
 
-@pytest.mark.parametrize("bits,cb,srdt,gs,k", [(4, None, torch.float16, 128, 256), (4, None, torch.float16, 64, 128),
-                                                (4, "auto", torch.float8_e4m3fn, 64, 128),
-                                                (6, None, torch.float8_e4m3fn, 64, 256)])
-def test_w4a8_linear_large_tiles(bits, cb, srdt, gs, k):
-    """Shapes that take the 256 x 256 tile kernel (>= 192 tiles), ragged in M and N; group size 128
-    shares one scale table per thread pair, 64 does not.  9 x 23 = 207 tiles (not a multiple of the
-    8 XCDs) for the 4-bit uniform group-64 case, 8 x 24 otherwise."""
-    m, n, g = (2303, 5880, 128) if (bits, cb, gs) == (4, None, 64) else (2047, 6136, 128)
+A8_TILE_CASES = [
+    # M >= 1024: int8 grid decoded once, then the LDS-DMA GEMM; 256 x 256 tiles (8 x 24 = 192, and
+    # 9 x 23 = 207, not a multiple of the 8 XCDs)
+    (4, None, torch.float16, 128, 256, 2047, 6136),
+    (4, None, torch.float16, 64, 128, 2303, 5880),
+    (4, "auto", torch.float8_e4m3fn, 64, 128, 2047, 6136),
+    (6, None, torch.float8_e4m3fn, 64, 256, 2047, 6136),
+    # the same GEMM with 128 x 256 tiles (6 x 20 tiles of 256 x 256 would not fill the GPU) and 128 x 128
+    (6, "auto", torch.float16, 64, 128, 1300, 5000),
+    (4, None, torch.float8_e4m3fn, 128, 256, 1024, 2000),
+    # M < 1024 with >= 192 tiles of 256 x 256: the fused-decode kernel, one scale table per thread
+    # pair (group 128) and per thread (group 64)
+    (4, None, torch.float16, 128, 128, 1000, 12300),
+    (6, "auto", torch.float8_e4m3fn, 64, 256, 777, 12500),
+]
+
+
+@pytest.mark.parametrize("bits,cb,srdt,gs,k,m,n", A8_TILE_CASES)
+def test_w4a8_linear_large_tiles(bits, cb, srdt, gs, k, m, n):
+    """Shapes that take the large-tile A8 kernels, ragged in M and N."""
+    g = 128
     rng = np.random.default_rng(20 + bits)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
     if cb == "auto":  # heavy tails (the quantizer fits a codebook), rescaled to the same spread
