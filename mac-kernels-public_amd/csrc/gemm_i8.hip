@@ -574,8 +574,10 @@ __global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __re
 // v_mfma_i32_32x32x32_i8.  Both operand tiles arrive by LDS DMA into rows of BK bytes whose 16-byte
 // chunks are XOR-swizzled (so that the 16 rows a fragment read touches fall in 16 bank groups),
 // in STAGES buffers: the DMA of k-tile kt + STAGES - 1 goes out before tile kt's MFMAs, and each
-// step waits only for the oldest DMA in flight.
-template <int BMT, int BNT, int BK, int STAGES>
+// step waits only for the oldest DMA in flight.  L2PF: one step earlier still, every 64-byte half
+// line of k-tile kt + STAGES is touched with a 4-byte DMA into a sink, so that the tile's own DMA
+// finds it in L2 (a second tile of look-ahead for the price of two instructions per thread).
+template <int BMT, int BNT, int BK, int STAGES, bool L2PF>
 __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int8_t* __restrict__ w8) {
     constexpr int NT = 512;
     constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
@@ -585,7 +587,10 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     constexpr int ASZ = BMT * BK, BSZ = BNT * BK;   // bytes per buffer
     constexpr int NA = ASZ / 16 / NT, NB = BSZ / 16 / NT;  // DMA instructions per thread and k-tile
     static_assert(NA * 16 * NT == ASZ && NB * 16 * NT == BSZ, "tile must split into whole DMA rounds");
-    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ)];
+    // operand buffers, then (L2PF) a 4-byte-per-thread sink for the prefetch DMAs; one LDS object,
+    // so that the compiler's alias tracking does not make fragment reads wait for the prefetches
+    constexpr int SINK = L2PF ? NT * 4 : 0;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ) + SINK];
     uint8_t (*buf_of)[ASZ + BSZ] = reinterpret_cast<uint8_t (*)[ASZ + BSZ]>(smem);  // [buffer][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -614,6 +619,22 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
         for (int i = 0; i < NA; ++i) lds_dma16(asrc[i] + k0, &buf_of[buf][16 * (512 * i + 64 * wave)]);
 #pragma unroll
         for (int i = 0; i < NB; ++i) lds_dma16(bsrc[i] + k0, &buf_of[buf][ASZ + 16 * (512 * i + 64 * wave)]);
+    };
+    // L2 prefetch: half line u = tid + NT i of a k-tile is row u / HPR (A rows, then B rows), half
+    // u % HPR; rows past M (N) touch row M - 1 (N - 1)
+    constexpr int HPR = BK / 64, PFN = L2PF ? (BMT + BNT) * HPR / NT : 0;
+    static_assert(!L2PF || PFN * NT == (BMT + BNT) * HPR, "prefetch must split into whole rounds");
+    const int8_t* pfsrc[PFN > 0 ? PFN : 1];
+#pragma unroll
+    for (int i = 0; i < PFN; ++i) {
+        const int u = tid + NT * i, row = u / HPR;
+        pfsrc[i] = (row < BMT ? p.xq + min<int64_t>(m0 + row, p.M - 1) * p.ldx
+                              : w8 + min<int64_t>(n0 + row - BMT, p.N - 1) * p.K) + 64 * (u % HPR);
+    }
+    auto l2pf = [&](int kt) {
+        const int k0 = min(kt, ktiles - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < PFN; ++i) lds_dma4(pfsrc[i] + k0, smem + STAGES * (ASZ + BSZ) + 256 * wave);
     };
 
     i32x16 acc[TI][TJ];
@@ -656,18 +677,27 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     };
 
     // Barrier without a memory fence: the DMA data this wave needs is covered by wait_vmcnt, and
-    // the loop writes LDS only by DMA.
+    // the loop writes LDS only by DMA.  Each step issues its tile DMA, then the prefetch of the
+    // tile after it; a step may leave the prefetch and the DMAs of later tiles in flight.
     constexpr int ND = NA + NB;  // DMA instructions per k-tile and thread
+    constexpr int INFLIGHT = PFN + (STAGES - 2) * (ND + PFN);
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st) dma(st, st);
-    wait_vmcnt<(STAGES - 2) * ND>();
+    for (int st = 0; st < STAGES - 1; ++st) {
+        dma(st, st);
+        l2pf(st + 1);
+    }
+    wait_vmcnt<INFLIGHT>();
     __builtin_amdgcn_s_barrier();
     for (int kt = 0; kt < ktiles; ++kt) {
         // past the end: re-reads the last tile into a buffer no step reads
         dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        l2pf(kt + STAGES);
         __builtin_amdgcn_sched_barrier(0);
         mfmas(kt % STAGES);
-        wait_vmcnt<(STAGES - 2) * ND>();  // tile kt + 1 has landed
+        // this wave's fragment reads of buffer kt % STAGES are complete before the barrier, after
+        // which the next step's DMA may overwrite it; tile kt + 1 has landed
+        wait_lgkmcnt0();
+        wait_vmcnt<INFLIGHT>();
         __builtin_amdgcn_s_barrier();
     }
     wait_vmcnt<0>();
@@ -743,13 +773,13 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         if (err != hipSuccess) return err;
         auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
         if (tiles(256, 256) >= 192)
-            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p,
+            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2, false>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p,
                                p.w8);
         else if (tiles(128, 256) >= 192)
-            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p,
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2, false>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p,
                                p.w8);
         else
-            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 128, 128, 2>), dim3((unsigned)tiles(128, 128)), dim3(512), 0, st, p,
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 128, 128, 2, false>), dim3((unsigned)tiles(128, 128)), dim3(512), 0, st, p,
                                p.w8);
         return hipGetLastError();
     }

@@ -43,19 +43,25 @@ __device__ __forceinline__ void stage2_reg(float* v) {
     }
 }
 
+// Lane exchanges: DPP quad permutes within quads, ds_swizzle (the LDS crossbar) beyond -- the
+// measured best split of the rotation's work between the VALU and the LDS pipe.
+template <int MASK>
+__device__ __forceinline__ float hx(float v) { return lane_xor<MASK>(v); }
+
 // Radix-4 stage on lane bits (C, C+1): every lane of the 4-lane group computes the same S.
+// Lane L forms t = a_L + a_(L^u) and adds the partner pair's t from lane L^2u, so
+// S = (a_L + a_(L^u)) + (a_(L^2u) + a_(L^3u)) -- the same rounded sum in all four lanes
+// (commutativity).
 template <int C>
 __device__ __forceinline__ void stage4_lane(float* v) {
     constexpr int u = 1 << C;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const float a = v[i];
-        const float p1 = lane_xor<u>(a);
-        const float p2 = lane_xor<2 * u>(a);
-        const float p3 = lane_xor<3 * u>(a);
-        // (a + p1) + (p2 + p3) is the same rounded sum in all four lanes (commutativity).
-        const float s = (a + p1) + (p2 + p3);
-        v[i] = s - 2.0f * p3;
+        const float p1 = hx<u>(a);
+        const float t = a + p1;
+        const float s = t + hx<2 * u>(t);
+        v[i] = s - 2.0f * hx<3 * u>(a);
     }
 }
 
@@ -66,7 +72,7 @@ __device__ __forceinline__ void stage2_lane(float* v, int lane) {
     const bool upper = (lane >> C) & 1;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const float p = lane_xor<u>(v[i]);
+        const float p = hx<u>(v[i]);
         v[i] = upper ? (p - v[i]) : (v[i] + p);
     }
 }

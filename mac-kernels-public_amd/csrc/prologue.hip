@@ -6,8 +6,9 @@
 //     s = dtype(scale) (0 -> dtype tiny), q = clamp(rne(dtype(x / s)), -128, 127); or
 //   * rotate-only mode (fp32 rows in, fp32 rows out), used to bring decoded weights back to the
 //     original basis.
-// One 256-thread workgroup per row; each thread holds 16 consecutive elements per 4096-element
-// slot, so a rotation group (<= 256 elements) lives in one 16-lane DPP row.
+// One workgroup per row, of NT threads (a multiple of 64, chosen with SLOTS so that NT x SLOTS x 16
+// just covers the row); each thread holds 16 consecutive elements per (16 NT)-element slot, so a
+// rotation group (<= 256 elements) lives in one 16-lane DPP row.
 #include "qlin_internal.h"
 #include "hadamard.h"
 
@@ -45,21 +46,25 @@ __device__ __forceinline__ void load16(const TIn* row, int64_t e0, int K, bool v
     }
 }
 
+// Largest workgroup per slot count (keeps 16 x SLOTS row values in registers without spilling).
+constexpr int prologue_max_threads(int slots) { return slots <= 2 ? 1024 : slots == 4 ? 512 : 256; }
+
 template <typename TIn, int MODE, int G, int SLOTS>
-__global__ __launch_bounds__(256) void prologue_kernel(const TIn* __restrict__ x, int64_t ldx, int K,
+__global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) void prologue_kernel(const TIn* __restrict__ x, int64_t ldx, int K,
                                                        bool vec_ok, f16* __restrict__ xo, int64_t ldo,
                                                        int32_t* __restrict__ eo, int8_t* __restrict__ qo,
                                                        float* __restrict__ so, TIn* __restrict__ xr,
                                                        float* __restrict__ fo) {
-    __shared__ float red[4];
+    __shared__ float red[16];
     const int m = blockIdx.x;
+    const int NT = (int)blockDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const TIn* row = x + (int64_t)m * ldx;
     float v[SLOTS][16];
     float amax = 0.0f;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
-        const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+        const int64_t e0 = ((int64_t)s * NT + tid) * 16;
         load16<TIn>(row, e0, K, vec_ok, v[s]);
         if constexpr (G > 0) {
             hadamard16<G>(v[s], lane);
@@ -78,14 +83,15 @@ __global__ __launch_bounds__(256) void prologue_kernel(const TIn* __restrict__ x
         amax = wave_max(amax);
         if (lane == 0) red[wave] = amax;
         __syncthreads();
-        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        amax = red[0];
+        for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, red[w]);
     }
 
     if constexpr (MODE == 0) {
         const int E = frexp_exp(amax);
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) {
-            const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+            const int64_t e0 = ((int64_t)s * NT + tid) * 16;
             if (e0 >= K) break;
             f16 h[16];
 #pragma unroll
@@ -115,14 +121,32 @@ __global__ __launch_bounds__(256) void prologue_kernel(const TIn* __restrict__ x
         if (!(scale >= 1e-30f)) scale = (scale != scale) ? scale : 1e-30f;
         float st = round_to<TIn>(scale);
         if (st == 0.0f) st = dtype_traits<TIn>::tiny();
+        // x / st: for 16-bit inputs and a finite normal st, the reciprocal y = 1/st with one
+        // residual correction, q = fma(fma(-x y, st, x), y, x y) (Markstein).  Checked against the
+        // IEEE quotient for every pair of fp16 (bf16) values x, st with |x| <= 130 st: identical
+        // fp32 quotients for fp16, identical int8 results for bf16.  Otherwise the IEEE division.
+        const bool fast = sizeof(TIn) == 2 && st >= 0x1p-126f && st <= 0x1.fffffep127f;
+        const float y = 1.0f / st;
+        // the row-uniform choice is made once, outside the element loops
+        auto quantize_row = [&]<bool FAST>() {
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) {
-            const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+            const int64_t e0 = ((int64_t)s * NT + tid) * 16;
             if (e0 >= K) break;
             int8_t qq[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float t = __builtin_rintf(round_to<TIn>(v[s][i] / st));
+                float qt;
+                {
+#pragma clang fp contract(off)
+                    if constexpr (FAST) {
+                        const float q0 = v[s][i] * y;
+                        qt = __builtin_fmaf(__builtin_fmaf(-q0, st, v[s][i]), y, q0);
+                    } else {
+                        qt = v[s][i] / st;
+                    }
+                }
+                float t = __builtin_rintf(round_to<TIn>(qt));
                 t = fminf(fmaxf(t, -128.0f), 127.0f);
                 qq[i] = (int8_t)(int)t;
             }
@@ -144,11 +168,14 @@ __global__ __launch_bounds__(256) void prologue_kernel(const TIn* __restrict__ x
                     if (e0 + i < K) xd[i] = dtype_traits<TIn>::from_f32(v[s][i]);
             }
         }
+        };
+        if (fast) quantize_row.template operator()<true>();
+        else quantize_row.template operator()<false>();
         if (tid == 0) so[m] = scale;
     } else {
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s) {
-            const int64_t e0 = ((int64_t)s * 256 + tid) * 16;
+            const int64_t e0 = ((int64_t)s * NT + tid) * 16;
             if (e0 >= K) break;
             float* dst = fo + (int64_t)m * ldo + e0;
             for (int i = 0; i < 16; ++i)
@@ -157,16 +184,34 @@ __global__ __launch_bounds__(256) void prologue_kernel(const TIn* __restrict__ x
     }
 }
 
+// Threads per row and slots per thread: one or two slots whenever the workgroup allows (four and
+// eight hold 200+ registers per thread, which leaves two waves per SIMD), then the fewest idle
+// 16-element units (NT x SLOTS x 16 - K), then the thread count nearest 384.
+static void prologue_shape(int K, int& nt, int& slots) {
+    const int units = (K + 15) / 16;
+    bool have = false;
+    int bk0 = 0, bk1 = 0, bk2 = 0;
+    for (int sl : {1, 2, 4, 8}) {
+        const int n = ((units + sl - 1) / sl + 63) / 64 * 64;
+        if (n > prologue_max_threads(sl)) continue;
+        const int k0 = sl > 2, k1 = n * sl - units, k2 = n > 384 ? n - 384 : 384 - n;
+        if (!have || k0 < bk0 || (k0 == bk0 && (k1 < bk1 || (k1 == bk1 && k2 < bk2)))) {
+            nt = n; slots = sl; bk0 = k0; bk1 = k1; bk2 = k2; have = true;
+        }
+    }
+}
+
 template <typename TIn, int MODE>
 static hipError_t launch_prologue(const PrologueArgs& a, hipStream_t st) {
-    const int slots = (a.K + 4095) / 4096;
+    int nt = 0, slots = 0;
+    prologue_shape(a.K, nt, slots);
     const bool vec_ok = (a.K % 16 == 0) && (a.ldx % 16 == 0) && (a.ldo % 16 == 0) &&
                         ((uintptr_t)a.x % 64 == 0);
     bool ok = false;
     auto go = [&]<int G>() {
         auto launch = [&](auto kern) {
-            hipLaunchKernelGGL(kern, dim3((unsigned)a.M), dim3(256), 0, st, (const TIn*)a.x, a.ldx, a.K, vec_ok,
-                               a.xo, a.ldo, a.eo, a.qo, a.so, (TIn*)a.xr, a.fo);
+            hipLaunchKernelGGL(kern, dim3((unsigned)a.M), dim3((unsigned)nt), 0, st, (const TIn*)a.x, a.ldx, a.K,
+                               vec_ok, a.xo, a.ldo, a.eo, a.qo, a.so, (TIn*)a.xr, a.fo);
             ok = true;
         };
         if (slots <= 1) launch(prologue_kernel<TIn, MODE, G, 1>);

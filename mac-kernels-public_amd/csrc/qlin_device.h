@@ -208,9 +208,19 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
 }
 
+// Wait until this wave's LDS reads and writes (and scalar loads) have completed; the vector-memory
+// counter is left alone.
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14)); }
+
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (lds wave-uniform).
 __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+// 4 bytes per lane into LDS at lds + 4 * lane: used to pull cache lines into L2 ahead of their
+// 16-byte DMA (the LDS destination is a sink nobody reads).
+__device__ __forceinline__ void lds_dma4(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0);
 }
 
 __device__ __forceinline__ float load_f(const float* p) { return *p; }
