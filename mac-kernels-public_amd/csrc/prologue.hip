@@ -123,8 +123,9 @@ __global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) vo
         if (st == 0.0f) st = dtype_traits<TIn>::tiny();
         // x / st: for 16-bit inputs and a finite normal st, the reciprocal y = 1/st with one
         // residual correction, q = fma(fma(-x y, st, x), y, x y) (Markstein).  Checked against the
-        // IEEE quotient for every pair of fp16 (bf16) values x, st with |x| <= 130 st: identical
-        // fp32 quotients for fp16, identical int8 results for bf16.  Otherwise the IEEE division.
+        // IEEE quotient for every pair of finite fp16 (bf16) values x, st with |x| <= 130 st
+        // (tests/quotient_check.c): identical fp32 quotients for fp16, identical int8 results for
+        // bf16.  Otherwise (fp32 inputs, subnormal or infinite st) the IEEE division.
         const bool fast = sizeof(TIn) == 2 && st >= 0x1p-126f && st <= 0x1.fffffep127f;
         const float y = 1.0f / st;
         // the row-uniform choice is made once, outside the element loops
