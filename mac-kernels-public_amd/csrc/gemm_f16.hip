@@ -443,6 +443,163 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     }
 }
 
+// INT8 weight-only GEMM with both operands moved by LDS DMA: y = epilogue(x[M, K] . w[N, K]^T), x the
+// normalized fp16 activations, w the int8 weights as stored (no widening before LDS, so a 64-value
+// k-tile brings in 32 KB of activations and 16 KB of weights).  Tile BMT x 256, 8 waves 4 (M) x
+// 2 (N), v_mfma_f32_32x32x16_f16, STAGES k-tiles in flight.
+//
+// k order inside a 64-value k-tile: MFMA step s = 2p + e (p, e in {0, 1}) gives the lanes of half
+// h (lane / 32) the 8 values k = 32p + 16h + 8e .. + 7 in both operands, so one 16-byte read of a
+// weight row (chunk 2p + h, 16 int8) feeds steps 2p and 2p + 1.  The int8 values become exact fp16
+// in registers after the read.  LDS rows: activations 128 bytes (8 chunks, chunk c of row r stored
+// at c ^ (r / 2) % 8), weights 64 bytes (4 chunks, at c ^ (r / 4) % 4): the 16 rows a 16-lane group
+// reads land in 16 distinct bank groups.
+template <int BMT, int STAGES>
+__global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
+    constexpr int NT = 512, BNT = 256, KT = 64;
+    constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
+    constexpr int ASZ = BMT * KT * 2, BSZ = BNT * KT;   // bytes per stage
+    constexpr int NA = ASZ / 16 / NT, NB = BSZ / 16 / NT;
+    static_assert(TI >= 1 && NA * 16 * NT == ASZ && NB * 16 * NT == BSZ, "tile shape");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ)];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, r32 = lane & 31, h = lane >> 5;
+    int mt, nt;
+    xcd_tile_f16(blockIdx.x, (int)gridDim.x, (int)((a.M + BMT - 1) / BMT), (int)((a.N + BNT - 1) / BNT), mt, nt);
+    const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
+    const int ktiles = (int)(a.K / KT);
+
+    // DMA instruction i of wave w fills physical chunk u = NT i + 64 w + lane of a stage: activation
+    // row u / 8, weight row u / 4.  The logical chunk it holds is the same for every i.
+    const int ca = (lane % 8) ^ ((4 * wave + lane / 16) % 8);
+    const int cb = (lane % 4) ^ (lane / 16);
+    const f16* asrc[NA];
+    const int8_t* bsrc[NB];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+        asrc[i] = a.x + min(m0 + (NT * i + 64 * wave + lane) / 8, a.M - 1) * a.ldx + 8 * ca;
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        bsrc[i] = (const int8_t*)a.w + min(n0 + (NT * i + 64 * wave + lane) / 4, a.N - 1) * a.ldw + 16 * cb;
+    auto dma = [&](int kt, int buf) {
+        const int k0 = min(kt, ktiles - 1) * KT;  // past the end: re-reads the last tile
+        uint8_t* st = smem + buf * (ASZ + BSZ);
+#pragma unroll
+        for (int i = 0; i < NA; ++i) lds_dma16(asrc[i] + k0, st + 16 * (NT * i + 64 * wave));
+#pragma unroll
+        for (int i = 0; i < NB; ++i) lds_dma16(bsrc[i] + k0, st + ASZ + 16 * (NT * i + 64 * wave));
+    };
+
+    f32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    // this lane's rows: activation rows wm WM + 32 i + r32 (swizzle (row / 2) % 8 = (r32 / 2) % 8
+    // since WM and 32 are multiples of 16), weight rows wn WN + 32 j + r32 (swizzle (r32 / 4) % 4)
+    const int swa = (r32 / 2) % 8, swb = (r32 / 4) % 4;
+    auto mfmas = [&](int buf) {
+        const uint8_t* as = smem + buf * (ASZ + BSZ) + (wm * WM + r32) * (KT * 2);
+        const uint8_t* bs = smem + buf * (ASZ + BSZ) + ASZ + (wn * WN + r32) * KT;
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            f16x8 bf[2][TJ];
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const u32x4 q = *reinterpret_cast<const u32x4*>(bs + 32 * j * KT + 16 * ((2 * pp + h) ^ swb));
+                uint32_t o[8];
+                i8x4_to_f16(q.x, o[0], o[1]);
+                i8x4_to_f16(q.y, o[2], o[3]);
+                i8x4_to_f16(q.z, o[4], o[5]);
+                i8x4_to_f16(q.w, o[6], o[7]);
+                bf[0][j] = __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+                bf[1][j] = __builtin_bit_cast(f16x8, u32x4{o[4], o[5], o[6], o[7]});
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int c = 16 * ((4 * pp + 2 * h + e) ^ swa);
+#pragma unroll
+                for (int i = 0; i < TI; ++i) {
+                    const f16x8 af = *reinterpret_cast<const f16x8*>(as + 32 * i * (KT * 2) + c);
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[e][j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Barrier without a memory fence: the DMA data a wave needs is covered by its wait_vmcnt, and
+    // the loop writes LDS only by DMA; the fragment reads of a buffer complete before the barrier
+    // after which the next DMA may overwrite it.
+    constexpr int ND = NA + NB;
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st) dma(st, st);
+    wait_vmcnt<(STAGES - 2) * ND>();
+    __builtin_amdgcn_s_barrier();
+    for (int kt = 0; kt < ktiles; ++kt) {
+        dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(kt % STAGES);
+        wait_lgkmcnt0();
+        wait_vmcnt<(STAGES - 2) * ND>();  // tile kt + 1 has landed
+        __builtin_amdgcn_s_barrier();
+    }
+    wait_vmcnt<0>();
+
+    // Epilogue: y = ldexp(acc, xexp[m]) * scale[n] + bias[n], staged through LDS in passes of RP
+    // rows (row stride BNT + 8 words); every thread writes 8 consecutive outputs with 16-byte stores.
+    // Lane l, register r of a 32 x 32 sub-tile holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
+    constexpr int ORW = BNT + 8;
+    constexpr int RP = (BMT * ORW * 4 <= (int)sizeof(smem)) ? BMT
+                       : (BMT / 2 * ORW * 4 <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
+    static_assert(RP * ORW * 4 <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
+    constexpr int CPR = BNT / 8;
+    static_assert(NT % CPR == 0 && (RP * CPR) % NT == 0, "chunks must split evenly");
+    float* ot = reinterpret_cast<float*>(smem);
+    const int cc = tid % CPR;
+    const int64_t nc = n0 + 8 * cc;
+    const int ncount = (int)max<int64_t>(0, min<int64_t>(8, a.N - nc));
+    float cs[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t n = min(nc + e, a.N - 1);
+        cs[e] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+        bv[e] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+    }
+    const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
+#pragma unroll
+    for (int pass = 0; pass < BMT / RP; ++pass) {
+        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
+        if ((wm * WM) / RP == pass) {
+            const int rw = wm * WM - pass * RP;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        ot[(rw + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] = acc[i][j][r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < RP * CPR / NT; ++q) {
+            const int row = tid / CPR + (NT / CPR) * q;
+            const int64_t m = m0 + pass * RP + row;
+            if (m >= a.M || ncount == 0) continue;
+            const f32x4 v0 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc);
+            const f32x4 v1 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc + 4);
+            const int e2 = a.xexp ? a.xexp[m] : 0;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
+            store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
+        }
+    }
+}
+
 template <int WK, int GT>
 hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
     if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
@@ -452,6 +609,10 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
         const bool vec = a.K % WBK == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 16 == 0 &&
                          (uintptr_t)a.w % 16 == 0;
         auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
+        if (vec && tiles(256, 256) >= 160) {
+            hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, a);
+            return hipGetLastError();
+        }
         if (vec) {
         // two-deep prefetch for the smaller tiles (at 256 x 256 it spills and measured slower)
         const bool deep = (a.K / WBK) % 2 == 0;
