@@ -271,29 +271,35 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     lds_barrier();
     const int nt0 = blockIdx.x * SP_ROWS;
     if (part) {
-        // Partials are written through to memory (device-scope stores), so the reduction kernel
-        // reads them without an L2 write-back of the whole tile at the end of this kernel; each
-        // store instruction covers 256 contiguous bytes of a row.
-        const int c = tid % SP_ROWS, n = nt0 + c;
+        // Partials: 16-byte non-temporal stores (streamed to memory rather than kept in L2, where
+        // the end of the kernel would have to write the tiles back); a row's N % 4 tail goes element
+        // by element.
 #pragma unroll
-        for (int j = 0; j < XR * SP_ROWS / SP_THREADS; ++j) {
-            const int r = tid / SP_ROWS + (SP_THREADS / SP_ROWS) * j;
-            if (r < M && n < N)
-                __hip_atomic_store(part + ((int64_t)split * M + r) * N + n,
-                                   *reinterpret_cast<const float*>(xs + r * ORS + 4 * c), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < XR * (SP_ROWS / 4) / SP_THREADS; ++j) {
+            const int c = tid + SP_THREADS * j, r = c / (SP_ROWS / 4), n = nt0 + 4 * (c % (SP_ROWS / 4));
+            if (r >= M || n >= N) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xs + r * ORS + 16 * (c % (SP_ROWS / 4)));
+            float* d = part + ((int64_t)split * M + r) * N + n;
+            if (N % 4 == 0) {
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d));
+            } else {
+                for (int q = 0; q < 4 && n + q < N; ++q) __builtin_nontemporal_store(v[q], d + q);
+            }
         }
         return;
     }
+    const bool vec = ldy % 4 == 0 && (uintptr_t)y % (y_dt == 0 ? 16 : 8) == 0;
 #pragma unroll
     for (int j = 0; j < XR * (SP_ROWS / 4) / SP_THREADS; ++j) {
         const int c = tid + SP_THREADS * j, r = c / (SP_ROWS / 4), n = nt0 + 4 * (c % (SP_ROWS / 4));
         if (r >= M || n >= N) continue;
         const f32x4 v = *reinterpret_cast<const f32x4*>(xs + r * ORS + 16 * (c % (SP_ROWS / 4)));
         const int e = xexp ? xexp[r] : 0;
-        for (int q = 0; q < 4 && n + q < N; ++q)
-            store_rt(y, y_dt, (int64_t)r * ldy + n + q,
-                     __builtin_ldexpf(v[q], e) + (bias ? load_rt(bias, bias_dt, n + q) : 0.0f));
+        float o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            o[q] = __builtin_ldexpf(v[q], e) + (bias ? load_rt(bias, bias_dt, min(n + q, N - 1)) : 0.0f);
+        store4_rt(y, y_dt, (int64_t)r * ldy + n, o, min(4, N - n), vec);
     }
 }
 
@@ -328,9 +334,13 @@ __global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
             for (int k = 1; k < S; ++k) s[q] += v[k];
         }
     }
-    for (int q = 0; q < 4 && n + q < N; ++q)
-        store_rt(y, y_dt, (int64_t)m * ldy + n + q,
-                 __builtin_ldexpf(s[q], e) + (bias ? load_rt(bias, bias_dt, n + q) : 0.0f));
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        o[q] = __builtin_ldexpf(s[q], e) + (bias ? load_rt(bias, bias_dt, min(n + q, N - 1)) : 0.0f);
+    // one 8-byte (f16, bf16) or 16-byte (f32) store per thread where rows allow it
+    const bool vec = ldy % 4 == 0 && (uintptr_t)y % (y_dt == 0 ? 16 : 8) == 0;
+    store4_rt(y, y_dt, (int64_t)m * ldy + n, o, min(4, N - n), vec);
 }
 
 template <int T>

@@ -182,6 +182,27 @@ __device__ __forceinline__ void store8_rt(void* base, int dtype, int64_t idx, co
     }
     for (int e = 0; e < count; ++e) store_rt(base, dtype, idx + e, v[e]);
 }
+// The same for 4 consecutive outputs (8-byte stores for f16/bf16, 16-byte for f32; the caller has
+// checked the alignment).
+__device__ __forceinline__ void store4_rt(void* base, int dtype, int64_t idx, const float* v, int count, bool vec) {
+    if (vec && count == 4) {
+        if (dtype == 0) {
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(base) + idx) = f32x4{v[0], v[1], v[2], v[3]};
+        } else if (dtype == 1) {
+            f16x4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (f16)v[e];
+            *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(base) + idx) = h;
+        } else {
+            u32x2 b;
+            b[0] = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+            b[1] = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+            *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(base) + idx) = b;
+        }
+        return;
+    }
+    for (int e = 0; e < count; ++e) store_rt(base, dtype, idx + e, v[e]);
+}
 __device__ __forceinline__ float load_rt(const void* base, int dtype, int64_t idx) {
     if (dtype == 0) return reinterpret_cast<const float*>(base)[idx];
     if (dtype == 1) return (float)reinterpret_cast<const f16*>(base)[idx];
