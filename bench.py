@@ -13,7 +13,7 @@ its average launch duration (HIP events around graph replays of that call alone)
 HBM peak; `traffic` is its measured HBM bytes per launch from the committed counter summary.
 cpu_baseline: the oracle's dequantize-then-matmul on the host (C decode, fp32 BLAS matmul).
 
-Other suites (--suite int8|w4a8|w6a8|dit|all) print their own JSON lines to stderr.
+Other suites (--suite int8|w4a8|w6a8|dit|lora|all) print their own JSON lines to stderr.
 """
 import argparse
 import json
@@ -331,6 +331,37 @@ def other_suites(which, steps, warmup):
         nb = sum(n * k for n, k in shapes)
         timed("dit_layer int8_convrot (4 linears, M4608)", qstep, fl, nb, FP16_PEAK_TFLOPS, "TFLOPs")
         timed("dit_layer fp16 torch F.linear (resident weights)", dstep, fl, nb * 2, FP16_PEAK_TFLOPS, "TFLOPs")
+    if which in ("lora", "all"):
+        # unmerged LoRA beside the quantized linears at the reference's LoRA benchmark shape
+        # (M, K, N) = (4608, 6144, 6144), rank 64, bf16 in and out, ConvRot on: the base call, the
+        # call with lora_down / lora_up, and the LoRA as two separate bf16 GEMMs on the base output
+        m, n, k, r = 4608, 6144, 6144, 64
+        x = torch.randn(m, k).to(torch.bfloat16).cuda()
+        down = (torch.randn(r, k) * 0.02).to(torch.bfloat16).cuda()
+        up = (torch.randn(n, r) * 0.02).to(torch.bfloat16).cuda()
+        q, s = quantize_int8_convrot_weight(weight(n, k), 256)
+        qd, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+        log("[lora] quantizing 6144x6144 (6-bit) ...")
+        q6, sr6, sc6, _ = quantize_w4a8_int8_weight(weight(n, k), bits=6, group_size=64, convrot_groupsize=256,
+                                                    codebook=None, s_rel_dtype=torch.float16)
+        q6, sr6, sc6 = q6.cuda(), sr6.cuda(), sc6.cuda()
+        calls = {
+            "int8_convrot": lambda **kw: qlin.int8_linear(x, qd, sd, None, torch.bfloat16, convrot=True,
+                                                          convrot_groupsize=256, **kw),
+            "w6a8": lambda **kw: qlin.w4a8_int8_linear(x, q6, sr6, sc6, None, None, None, 64, 256, torch.bfloat16, **kw),
+        }
+        fl, flr = 2 * m * n * k, 2 * m * r * (k + n)
+        for fmt, f in calls.items():
+            peak, unit = (FP16_PEAK_TFLOPS, "TFLOPs") if fmt == "int8_convrot" else (INT8_PEAK_TOPS, "TOPs")
+            timed(f"lora base {fmt} M{m} K{k} N{n}", lambda f=f: f(), fl, n * k + m * k * 2 + m * n * 2, peak, unit)
+            timed(f"lora fused {fmt} r{r}", lambda f=f: f(lora_down=down, lora_up=up, lora_scale=0.8), fl + flr,
+                  n * k + m * k * 2 + m * n * 4, peak, unit)
+
+            def unfused(f=f):
+                y = f()
+                y.addmm_(torch.nn.functional.linear(x, down), up.t(), alpha=0.8)
+            timed(f"lora unfused {fmt} r{r} (bf16 addmm beside the call)", unfused, fl + flr,
+                  n * k + m * k * 2 + m * n * 4, peak, unit)
     return out
 
 
@@ -339,7 +370,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--suite", default="gguf", choices=["gguf", "int8", "w4a8", "w6a8", "dit", "all"])
+    ap.add_argument("--suite", default="gguf", choices=["gguf", "int8", "w4a8", "w6a8", "dit", "lora", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=1024, help="weight rows decoded per call for the CPU baseline")
     ap.add_argument("--profile", action="store_true",

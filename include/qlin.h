@@ -58,6 +58,7 @@ typedef enum {
     QLIN_OP_INT8_LINEAR = 0,
     QLIN_OP_W4A8_LINEAR = 1,
     QLIN_OP_GGUF_LINEAR = 2,
+    QLIN_OP_LORA = 3,   /* qlin_lora_apply: param = the LoRA rank R */
 } qlin_op;
 
 /* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
@@ -111,6 +112,20 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
 qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                              const qlin_tensor* bias, qlin_tensor* y,
                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* Unmerged LoRA on a finished linear output: y[m,n] = dtype(y[m,n] + lora_scale * sum_r t[m,r] *
+ * lora_up[n,r]) with t = x @ lora_down^T kept in fp32 in the workspace (up to 8 K-split partials of
+ * M*R*4 bytes and their sum: qlin_workspace_size(QLIN_OP_LORA, M, N, K, R, x_dtype)).  x is the caller's activation (before
+ * any ConvRot rotation); x [M,K], lora_down [R,K], lora_up [N,R], y [M,N]: f32/f16/bf16, unit
+ * column stride.  Factors enter as hi + lo bf16 parts (16 significand bits; bf16 MFMA, the lo*lo
+ * term dropped) with fp32's exponent range; sums are fp32.
+ * Replaces the lora_down / lora_up / lora_scale keywords of comfy_kitchen's int8_linear,
+ * w4a8_int8_linear and gguf_linear (bench/bench_lora_sidepath_kernel.py:80;
+ * bench/bench_lora_fused_rank.py:36; docs/upstream/comfy-kitchen-mps-backend.md:54-57): the
+ * caller runs the base linear, then this call on the same stream. */
+qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
+                            float lora_scale, qlin_tensor* y, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* Decode GGUF blocks to a dense [N,K] f32 (bit-exact with gguf-py 0.19.0's fp32 decode), or
  * f16/bf16 (that value rounded once, to nearest even).  Rows may straddle blocks (flat index).

@@ -201,6 +201,10 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
         case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K);
         case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param);
+        case QLIN_OP_LORA: {  // the split partials, then their sum
+            const int S = lora_splits(M, K, param);
+            return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(param > 0 ? param : 0) * 4);
+        }
     }
     return 0;
 }
@@ -229,6 +233,41 @@ qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x
         }
     }
     return fail(QLIN_EUNSUPPORTED, "unknown op %d", op);
+}
+
+qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
+                            float lora_scale, qlin_tensor* y, void* workspace, size_t workspace_bytes, void* stream) {
+    Mat X, D, U, Y;
+    qlin_status s;
+    if ((s = as_matrix(x, "x", X)) || (s = as_matrix(lora_down, "lora_down", D)) ||
+        (s = as_matrix(lora_up, "lora_up", U)) || (s = as_matrix(y, "y", Y)))
+        return s;
+    if (!is_float(X.dtype) || !is_float(D.dtype) || !is_float(U.dtype) || !is_float(Y.dtype))
+        return fail(QLIN_EUNSUPPORTED, "lora operands must be f32/f16/bf16");
+    const int64_t M = X.rows, K = X.cols, R = D.rows, N = U.rows;
+    if (D.cols != K) return fail(QLIN_EINVAL, "lora_down is [%lld, %lld], x has K=%lld", (long long)R,
+                                 (long long)D.cols, (long long)K);
+    if (U.cols != R) return fail(QLIN_EINVAL, "lora_up has rank %lld, lora_down %lld", (long long)U.cols, (long long)R);
+    if (Y.rows != M || Y.cols != N) return fail(QLIN_EINVAL, "y must be [%lld, %lld]", (long long)M, (long long)N);
+    if (R < 1) return fail(QLIN_EINVAL, "lora rank must be positive");
+    const int S = lora_splits(M, K, R);
+    const size_t need = align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)R * 4);
+    if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
+    if (M == 0 || N == 0) return QLIN_OK;
+    auto vec = [](const Mat& A) {
+        const int es = A.dtype == QLIN_DT_F32 ? 4 : 2;
+        return A.cols >= 8 && A.cols % 8 == 0 && (A.ld * es) % 16 == 0 && (uintptr_t)A.data % 16 == 0;
+    };
+    LoraArgs a;
+    a.x = X.data; a.x_dt = X.dtype; a.ldx = X.ld; a.vec_x = vec(X);
+    a.down = D.data; a.down_dt = D.dtype; a.ld_down = D.ld; a.vec_down = vec(D);
+    a.up = U.data; a.up_dt = U.dtype; a.ld_up = U.ld; a.vec_up = vec(U);
+    a.scale = lora_scale;
+    a.M = M; a.N = N; a.K = K; a.R = R;
+    a.t = (float*)workspace;
+    a.S = S;
+    a.y = Y.data; a.y_dt = Y.dtype; a.ldy = Y.ld;
+    return hip_status(run_lora(a, (hipStream_t)stream), "lora");
 }
 
 qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,

@@ -1,0 +1,432 @@
+// Unmerged LoRA on a finished linear: y[m, n] <- y[m, n] + scale * sum_r t[m, r] up[n, r], with
+// t = x down^T (roblennon/mac-kernels-public: the lora_down / lora_up / lora_scale keywords of the
+// quantized linears, bench/bench_lora_sidepath_kernel.py:80, semantics
+// docs/upstream/comfy-kitchen-mps-backend.md:54-57; the activation is the caller's x, before any
+// ConvRot rotation).
+//
+// Both products run on v_mfma_f32_32x32x16_bf16 with every operand that is not already bf16 split
+// into bf16 parts hi = bf16(v), lo = bf16(v - hi).  bf16 x bf16 products are exact in fp32 and bf16
+// has fp32's exponent range, so there is no overflow or normalization; hi + lo carries 16
+// significand bits (the lo x lo product, ~2^-16 of a term, is dropped).  t is kept in fp32.
+//
+//   lora_down_kernel: one workgroup per 32 rows x 64 ranks (32 when R <= 32) of t and K split, 4
+//     waves on contiguous K quarters, added through LDS in a fixed order (the result does not
+//     depend on timing).  Fragments come straight from global memory, 8 steps of loads in flight.
+//   The K range is split S ways over workgroups (S fp32 partials of t) when the row tiles alone
+//     would leave CUs idle; lora_sum_kernel adds the partials in split order.
+//   lora_up_kernel: 128 x 128 output tiles, 4 waves of 64 x 64, the rank in chunks of 64 staged
+//     in LDS; the tile is staged through LDS, then each output is read, increased by scale * acc
+//     in fp32 and rounded once to y's dtype, 8 outputs per thread.
+#include "qlin_internal.h"
+
+namespace qlin {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ __bf16 to_bf16(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16_bits(f)); }
+
+// hi = bf16(v), lo = bf16(v - hi) (v - hi is exact in fp32)
+__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint16_t hb = f32_to_bf16_bits(v[i]);
+        hi[i] = __builtin_bit_cast(__bf16, hb);
+        lo[i] = to_bf16(v[i] - bf16_bits_to_f32(hb));
+    }
+}
+
+// Raw storage of 8 consecutive values of one operand (16 bytes for f16/bf16, 32 for f32), loaded
+// ahead of use so that several steps of loads are in flight.
+template <int DT>
+struct Raw8 {
+    u32x4 v[DT == DT_F32 ? 2 : 1];
+};
+
+// VEC (16-byte loads) requires cols % 8 == 0 and cols >= 8, so with k a multiple of 8 a piece is
+// either wholly inside the row or wholly past its end: the load is issued unconditionally from a
+// clamped column, and the caller zeroes a past-the-end piece when it uses it (a load behind a
+// lane-dependent branch, or a select right after it, would be waited for on the spot).
+template <int DT, bool VEC>
+__device__ __forceinline__ Raw8<DT> raw_load(const void* base, int64_t ld, int64_t row, int64_t k, int64_t cols) {
+    Raw8<DT> r;
+    if constexpr (VEC) {
+        const int64_t kc = min(k, cols - 8);
+        if constexpr (DT == DT_F32) {
+            const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(base) + row * ld + kc);
+            r.v[0] = p[0];
+            r.v[1] = p[1];
+        } else {
+            r.v[0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + row * ld + kc);
+        }
+        return r;  // a piece past the end holds the row's last 8 values: the caller zeroes it at use
+    } else {
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = k + i < cols ? load_rt(base, DT, row * ld + k + i) : 0.0f;
+    if constexpr (DT == DT_F32) {
+        r.v[0] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+        r.v[1] = u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])};
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = DT == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)f[2 * i])
+                                             : (uint32_t)f32_to_bf16_bits(f[2 * i]);
+            const uint32_t hi = DT == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)f[2 * i + 1])
+                                             : (uint32_t)f32_to_bf16_bits(f[2 * i + 1]);
+            w[i] = lo | (hi << 16);  // the loaded values are exact in the storage type
+        }
+        r.v[0] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    return r;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> zero_unless(const Raw8<DT>& r, bool keep) {
+    Raw8<DT> z;
+#pragma unroll
+    for (int j = 0; j < (DT == DT_F32 ? 2 : 1); ++j) z.v[j] = keep ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
+    return z;
+}
+
+template <int DT>
+__device__ __forceinline__ void raw_to_f32(const Raw8<DT>& r, float* f) {
+    if constexpr (DT == DT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = __uint_as_float(r.v[0][i]);
+            f[4 + i] = __uint_as_float(r.v[1][i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bits_to_f32_rt(r.v[0][i] & 0xFFFFu, DT);
+            f[2 * i + 1] = bits_to_f32_rt(r.v[0][i] >> 16, DT);
+        }
+    }
+}
+
+// acc += A . B over one 16-value step from raw loads; bf16 operands are used as loaded.
+template <int DA, int DB>
+__device__ __forceinline__ void mfma_raw(const Raw8<DA>& ra, const Raw8<DB>& rb, f32x16& acc) {
+    constexpr bool SA = DA != DT_BF16, SB = DB != DT_BF16;
+    bf16x8 ah, al, bh, bl;
+    if constexpr (SA) {
+        float f[8];
+        raw_to_f32(ra, f);
+        split8(f, ah, al);
+    } else {
+        ah = __builtin_bit_cast(bf16x8, ra.v[0]);
+    }
+    if constexpr (SB) {
+        float f[8];
+        raw_to_f32(rb, f);
+        split8(f, bh, bl);
+    } else {
+        bh = __builtin_bit_cast(bf16x8, rb.v[0]);
+    }
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+    if constexpr (SA) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+    if constexpr (SB) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+}
+
+// 16-value steps whose loads are in flight together: 8 x (1 + NH) 16-byte pieces for 16-bit
+// operands at NH = 1, fewer with two rank halves or an fp32 operand (8 registers per piece)
+template <int DX, int DD, int NH>
+constexpr int lora_pf() { return (DX == DT_F32 || DD == DT_F32 ? 4 : 8) / NH; }
+
+// t_s[m, r] = sum over split s's k of x[m, k] down[r, k] (fp32 partial s of [S][M][R]) for 32 rows
+// and 32 NH ranks per workgroup: 4 waves, each a contiguous quarter of the split's 16-value steps
+// for all of the tile's ranks, the quarters added through LDS in order.  Lane l holds row (rank)
+// l % 32 and the 8 k values 8 (l / 32) .. + 7 of a step in both operands, so the 4 loads of 4
+// consecutive steps cover 128 contiguous bytes of each row.  x is read once when R <= 32 NH.
+template <int DX, int DD, bool VEC, int NH>
+__global__ __launch_bounds__(256) void lora_down_kernel(LoraArgs a) {
+    constexpr int PF = lora_pf<DX, DD, NH>(), RW = 32 * NH + 1;
+    __shared__ float red[4][32 * RW];
+    const int tid = threadIdx.x, lane = tid & 63, kq = tid >> 6;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int64_t m0 = (int64_t)blockIdx.y * 32, q0 = (int64_t)blockIdx.x * 32 * NH;
+    const int64_t xm = min(m0 + r32, a.M - 1);  // rows past the end repeat
+    int64_t dr[NH];
+#pragma unroll
+    for (int i = 0; i < NH; ++i) dr[i] = min(q0 + 32 * i + r32, a.R - 1);
+    f32x16 acc[NH];
+#pragma unroll
+    for (int i = 0; i < NH; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+    // this wave's steps [w0, w1): quarter kq of split blockIdx.z's steps
+    const int64_t steps = (a.K + 15) / 16, sp = blockIdx.z;
+    const int64_t st0 = steps * sp / a.S, st1 = steps * (sp + 1) / a.S;
+    const int64_t w0 = st0 + (st1 - st0) * kq / 4, w1 = st0 + (st1 - st0) * (kq + 1) / 4;
+    // every lane of a wave runs the same trip count; steps past the quarter (or K) count zero
+    for (int64_t s0 = w0; s0 < w1; s0 += PF) {
+        Raw8<DX> xr[PF];
+        Raw8<DD> dv[PF][NH];
+        if (VEC && s0 + PF <= w1 && 16 * (s0 + PF) <= a.K) {
+            // the whole batch is inside the quarter and K (uniform over the wave): one base
+            // pointer per operand row and constant offsets, no clamping
+            const int64_t k = 16 * s0 + 8 * h;
+#pragma unroll
+            for (int j = 0; j < PF; ++j) {
+                xr[j] = raw_load<DX, true>(a.x, a.ldx, xm, k + 16 * j, k + 16 * j + 8);
+#pragma unroll
+                for (int i = 0; i < NH; ++i) dv[j][i] = raw_load<DD, true>(a.down, a.ld_down, dr[i], k + 16 * j, k + 16 * j + 8);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < PF; ++j) {
+                const int64_t k = 16 * (s0 + j) + 8 * h;
+                xr[j] = raw_load<DX, VEC>(a.x, a.ldx, xm, k, a.K);
+#pragma unroll
+                for (int i = 0; i < NH; ++i) dv[j][i] = raw_load<DD, VEC>(a.down, a.ld_down, dr[i], k, a.K);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the batch goes out before the first MFMA
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const Raw8<DX> xz = zero_unless(xr[j], s0 + j < w1 && 16 * (s0 + j) + 8 * h < a.K);
+#pragma unroll
+            for (int i = 0; i < NH; ++i) mfma_raw<DX, DD>(xz, dv[j][i], acc[i]);
+        }
+    }
+    // C layout: lane l, register e holds row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32
+#pragma unroll
+    for (int i = 0; i < NH; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[kq][(8 * (e / 4) + 4 * h + e % 4) * RW + 32 * i + r32] = acc[i][e];
+    __syncthreads();
+    for (int e = tid; e < 32 * 32 * NH; e += 256) {
+        const int row = e / (32 * NH), col = e % (32 * NH);
+        const int64_t m = m0 + row, q = q0 + col;
+        if (m >= a.M || q >= a.R) continue;
+        const int o = row * RW + col;
+        a.t[(sp * a.M + m) * a.R + q] = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
+    }
+}
+
+// t[i] = sum over s, in split order, of partial s (for S > 1), written after the partials.
+__global__ __launch_bounds__(256) void lora_sum_kernel(const float* __restrict__ part, int S, int64_t n,
+                                                       float* __restrict__ t) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = part[i];
+    for (int sp = 1; sp < S; ++sp) v += part[sp * n + i];
+    t[i] = v;
+}
+
+// y[m, n] = dtype(float(y[m, n]) + scale * sum_r t[m, r] up[n, r]) for a 128 x 128 tile: 4 waves of
+// 64 x 64 (2 x 2 MFMA sub-tiles), the rank in chunks of 64.  Each chunk of t (fp32 [M][R]) is staged
+// in LDS for the tile's 128 rows; up fragments come from global memory.
+// The output tile is staged through the same LDS in two 64-row halves, so y is read and written 8
+// outputs per thread.
+constexpr int UP_T = 128, UP_RC = 64;
+template <int DU, bool VEC>
+__global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
+    // one buffer: the t chunk during the rank loop, then 64-row halves of the output tile
+    constexpr int TSW = UP_RC + 4, OTW = UP_T + 4;
+    constexpr int SZ = UP_T * TSW > 64 * OTW ? UP_T * TSW : 64 * OTW;
+    __shared__ __attribute__((aligned(16))) float smem[SZ];
+    float* ts = smem;
+    float* ot = smem;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, h = lane >> 5, wm = wave >> 1, wn = wave & 1;
+    const int64_t mt = (int64_t)blockIdx.y * UP_T, nt = (int64_t)blockIdx.x * UP_T;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    int64_t un[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) un[j] = min(nt + 64 * wn + 32 * j + r32, a.N - 1);
+    // the tile's y (8 outputs per thread and chunk, rows clamped) is requested first, so its
+    // memory round trip overlaps the rank loop; 16-bit outputs only (f32 y takes the plain path)
+    const bool vec = a.ldy % 8 == 0 && (uintptr_t)a.y % 16 == 0;
+    constexpr int YC = UP_T * UP_T / 8 / 256;  // output chunks per thread
+    const bool ypre = vec && a.y_dt != DT_F32 && a.N % 8 == 0;
+    u32x4 yv[YC];
+    if (ypre) {
+#pragma unroll
+        for (int j = 0; j < YC; ++j) {
+            const int c = tid + 256 * j, row = c / (UP_T / 8), col = 8 * (c % (UP_T / 8));
+            const int64_t m = min(mt + row, a.M - 1), n = min(nt + col, a.N - 8);
+            yv[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.y) + m * a.ldy + n);
+        }
+    }
+    for (int64_t rc = 0; rc < a.R; rc += UP_RC) {
+        __syncthreads();  // the previous chunk's t is no longer read
+        if (a.R % 4 == 0) {
+            // 16-byte pieces: piece e = row e / 16, ranks 4 (e % 16) .. + 3, loaded from a clamped
+            // rank (all before any store), pieces past R zeroed
+            constexpr int PPT = UP_T * UP_RC / 4 / 256;  // pieces per thread
+            f32x4 pv[PPT];
+#pragma unroll
+            for (int i = 0; i < PPT; ++i) {
+                const int e = tid + 256 * i, row = e / (UP_RC / 4);
+                const int64_t m = min(mt + row, a.M - 1), r = min(rc + 4 * (e % (UP_RC / 4)), a.R - 4);
+                pv[i] = *reinterpret_cast<const f32x4*>(a.t + m * a.R + r);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < PPT; ++i) {
+                const int e = tid + 256 * i, row = e / (UP_RC / 4), c = 4 * (e % (UP_RC / 4));
+                *reinterpret_cast<f32x4*>(ts + row * TSW + c) = rc + c < a.R ? pv[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        } else {
+            for (int e = tid; e < UP_T * UP_RC; e += 256) {
+                const int row = e / UP_RC, c = e % UP_RC;
+                const int64_t m = min(mt + row, a.M - 1), r = rc + c;
+                ts[row * TSW + c] = r < a.R ? a.t[m * a.R + r] : 0.f;
+            }
+        }
+        __syncthreads();
+        // 4 rank steps of 16 per chunk; up loads of the chunk go out first
+        Raw8<DU> ur[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) ur[q][j] = raw_load<DU, VEC>(a.up, a.ld_up, un[j], rc + 16 * q + 8 * h, a.R);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool in = rc + 16 * q + 8 * h < a.R;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float* tp = ts + (64 * wm + 32 * i + r32) * TSW + 16 * q + 8 * h;
+                float tv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) tv[e] = in ? tp[e] : 0.f;  // zero past R (LDS holds zeros too)
+                bf16x8 th, tl;
+                split8(tv, th, tl);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    bf16x8 uh, ul;
+                    if constexpr (DU == DT_BF16) {
+                        uh = __builtin_bit_cast(bf16x8, ur[q][j].v[0]);
+                    } else {
+                        float uv[8];
+                        raw_to_f32(ur[q][j], uv);
+                        split8(uv, uh, ul);
+                    }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(th, uh, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tl, uh, acc[i][j], 0, 0, 0);
+                    if constexpr (DU != DT_BF16) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(th, ul, acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // C layout: lane l, register e holds row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.  Two
+    // passes: the waves of row half `pass` stage their 64 rows, then every thread updates y.
+    for (int pass = 0; pass < 2; ++pass) {
+    __syncthreads();  // t (or the previous half) is no longer read
+    if (wm == pass) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    ot[(32 * i + 8 * (e / 4) + 4 * h + e % 4) * OTW + 64 * wn + 32 * j + r32] = acc[i][j][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 64 * UP_T / 8 / 256; ++j) {
+        const int c = tid + 256 * j, row = c / (UP_T / 8), col = 8 * (c % (UP_T / 8));
+        const int64_t m = mt + 64 * pass + row, n = nt + col;
+        if (m >= a.M || n >= a.N) continue;
+        const int cnt = (int)min<int64_t>(8, a.N - n);
+        float v[8];
+        if (ypre) {
+            const u32x4 q = yv[pass * (YC / 2) + j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[2 * e] = bits_to_f32_rt(q[e] & 0xFFFFu, a.y_dt);
+                v[2 * e + 1] = bits_to_f32_rt(q[e] >> 16, a.y_dt);
+            }
+        } else if (vec && cnt == 8) {
+            if (a.y_dt == DT_F32) {
+                raw_to_f32(raw_load<DT_F32, true>(a.y, a.ldy, m, n, a.N), v);
+            } else if (a.y_dt == DT_F16) {
+                raw_to_f32(raw_load<DT_F16, true>(a.y, a.ldy, m, n, a.N), v);
+            } else {
+                raw_to_f32(raw_load<DT_BF16, true>(a.y, a.ldy, m, n, a.N), v);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = e < cnt ? load_rt(a.y, a.y_dt, m * a.ldy + n + e) : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = v[e] + a.scale * ot[row * OTW + col + e];
+        store8_rt(a.y, a.y_dt, m * a.ldy + n, v, cnt, vec);
+    }
+    }
+}
+
+}  // namespace
+
+hipError_t run_lora(const LoraArgs& a, hipStream_t st) {
+    if (a.M == 0 || a.N == 0) return hipSuccess;
+    if (a.R < 1 || !a.t) return hipErrorInvalidValue;
+    if (a.S < 1 || a.S > 8) return hipErrorInvalidValue;
+    const int nh = a.R <= 32 ? 1 : 2;  // rank halves per workgroup
+    const dim3 dgrid((unsigned)((a.R + 32 * nh - 1) / (32 * nh)), (unsigned)((a.M + 31) / 32), (unsigned)a.S);
+    bool ok = false;
+    const bool vd = a.vec_x && a.vec_down, vu = a.vec_up;
+    auto down = [&]<int DX, int DD>() {
+        if (a.x_dt == DX && a.down_dt == DD) {
+            if (vd && nh == 1) hipLaunchKernelGGL((lora_down_kernel<DX, DD, true, 1>), dgrid, dim3(256), 0, st, a);
+            else if (vd) hipLaunchKernelGGL((lora_down_kernel<DX, DD, true, 2>), dgrid, dim3(256), 0, st, a);
+            else if (nh == 1) hipLaunchKernelGGL((lora_down_kernel<DX, DD, false, 1>), dgrid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((lora_down_kernel<DX, DD, false, 2>), dgrid, dim3(256), 0, st, a);
+            ok = true;
+        }
+    };
+    auto by_down = [&]<int DX>() {
+        down.template operator()<DX, DT_F32>();
+        down.template operator()<DX, DT_F16>();
+        down.template operator()<DX, DT_BF16>();
+    };
+    by_down.template operator()<DT_F32>();
+    by_down.template operator()<DT_F16>();
+    by_down.template operator()<DT_BF16>();
+    if (!ok) return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    LoraArgs u = a;  // the up kernel reads one t: the partials' sum when K was split
+    if (a.S > 1) {
+        const int64_t n = a.M * a.R;
+        u.t = a.t + (int64_t)a.S * n;
+        hipLaunchKernelGGL(lora_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.t, a.S, n, u.t);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    const dim3 ugrid((unsigned)((a.N + UP_T - 1) / UP_T), (unsigned)((a.M + UP_T - 1) / UP_T));
+#define QLIN_LORA_UP(DU)                                                                              \
+    if (vu) hipLaunchKernelGGL((lora_up_kernel<DU, true>), ugrid, dim3(256), 0, st, u);               \
+    else hipLaunchKernelGGL((lora_up_kernel<DU, false>), ugrid, dim3(256), 0, st, u);
+    switch (a.up_dt) {
+        case DT_F32: QLIN_LORA_UP(DT_F32) break;
+        case DT_F16: QLIN_LORA_UP(DT_F16) break;
+        case DT_BF16: QLIN_LORA_UP(DT_BF16) break;
+        default: return hipErrorInvalidValue;
+    }
+#undef QLIN_LORA_UP
+    return hipGetLastError();
+}
+
+// As many splits as fit one round of about 3 workgroups per CU (768), at least 256 k-values each.
+int lora_splits(int64_t M, int64_t K, int64_t R) {
+    const int64_t nh = R <= 32 ? 1 : 2;
+    const int64_t tiles = ((M + 31) / 32) * ((R + 32 * nh - 1) / (32 * nh));
+    int64_t s = 768 / std::max<int64_t>(tiles, 1);
+    s = std::min<int64_t>(s, std::max<int64_t>(K / 256, 1));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(s, 8));
+}
+
+}  // namespace qlin

@@ -138,6 +138,30 @@ struct GemmI8Args {
 // Activation rows from which the A8 linear decodes the weight grid once into the workspace
 // (N * K bytes) instead of once per 256-row tile inside the GEMM.
 inline bool a8_decode_once(int64_t M, int64_t K) { return M >= 1024 && K % 128 == 0; }
+
+// Unmerged LoRA: y += scale * (x down^T) up^T after the base linear (lora.hip).
+struct LoraArgs {
+    const void* x = nullptr;     // [M, K] f32/f16/bf16, unit column stride
+    int x_dt = DT_F16;
+    int64_t ldx = 0;
+    const void* down = nullptr;  // [R, K]
+    int down_dt = DT_BF16;
+    int64_t ld_down = 0;
+    const void* up = nullptr;    // [N, R]
+    int up_dt = DT_BF16;
+    int64_t ld_up = 0;
+    bool vec_x = false, vec_down = false, vec_up = false;  // 16-byte loads of 8 values allowed
+    float scale = 1.0f;
+    int64_t M = 0, N = 0, K = 0, R = 0;
+    float* t = nullptr;          // workspace: x down^T as S fp32 partials [S][M][R] (K split S ways)
+    int S = 1;
+    void* y = nullptr;           // [M, N] f32/f16/bf16, read and rewritten
+    int y_dt = DT_F16;
+    int64_t ldy = 0;
+};
+hipError_t run_lora(const LoraArgs& a, hipStream_t st);
+// K splits of the LoRA down-projection for this shape (the workspace holds that many partials).
+int lora_splits(int64_t M, int64_t K, int64_t R);
 hipError_t run_gemm_i8(const GemmI8Args& a, hipStream_t st);
 
 // ---- standalone decodes (dequant.hip) ----

@@ -30,9 +30,42 @@ def _disabled(op):
         raise NoCapableBackendError(op, {"hip": "disabled by QLIN_DISABLE"})
 
 
-def _decline_lora(op, lora_down, lora_up, lora_scale):
-    if lora_down is not None or lora_up is not None or lora_scale is not None:
-        raise NoCapableBackendError(op, {"hip": "lora_* side path is not implemented"})
+def _lora_args(op, lora_down, lora_up, lora_scale, n, k):
+    """Validated (down [R, K], up [N, R], scale) or None.  lora_scale None means 1.0; a scale
+    without both factors is rejected (the reference passes the three together)."""
+    if lora_down is None and lora_up is None:
+        if lora_scale is not None:
+            raise ValueError(f"{op}: lora_scale given without lora_down / lora_up")
+        return None
+    if lora_down is None or lora_up is None:
+        raise ValueError(f"{op}: lora_down and lora_up go together")
+    if lora_down.dim() != 2 or lora_up.dim() != 2:
+        raise ValueError(f"{op}: lora_down must be [R, K] and lora_up [N, R]")
+    r = lora_down.shape[0]
+    if lora_down.shape[1] != k or tuple(lora_up.shape) != (n, r):
+        raise ValueError(f"{op}: lora_down {tuple(lora_down.shape)} / lora_up {tuple(lora_up.shape)} "
+                         f"do not fit K={k}, N={n}")
+    for t in (lora_down, lora_up):
+        if t.dtype not in _FLOAT:
+            raise NoCapableBackendError(op, {"hip": f"lora dtype {t.dtype} unsupported"})
+    scale = 1.0 if lora_scale is None else float(lora_scale)
+    return lora_down, lora_up, scale
+
+
+def _apply_lora(op, lora, x2, y):
+    """y += scale * (x2 @ down^T) @ up^T on the GPU (qlin_lora_apply), after the base linear."""
+    if lora is None or y.numel() == 0:
+        return
+    down, up, scale = lora
+    _check_device(op, down, up)
+    if down.stride(-1) != 1:
+        down = down.contiguous()
+    if up.stride(-1) != 1:
+        up = up.contiguous()
+    r = down.shape[0]
+    ws = _workspace(_lib.OP_LORA, x2.shape[0], up.shape[0], x2.shape[1], r, x2)
+    _lib.check(_lib.load().qlin_lora_apply(_lib.desc(x2), _lib.desc(down), _lib.desc(up), scale, _lib.desc(y),
+                                           ws.data_ptr(), ws.numel(), _lib.stream_of(x2.device)), op)
 
 
 def _check_device(op, *tensors):
@@ -94,13 +127,13 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     scale [N] / [N, 1] / scalar (fp32 or fp16).  fp16 MFMA, fp32 accumulate."""
     op = "int8_linear"
     _disabled(op)
-    _decline_lora(op, lora_down, lora_up, lora_scale)
     _check_device(op, x, qdata, scale, bias)
     if qdata.dtype != torch.int8 or qdata.dim() != 2:
         raise NoCapableBackendError(op, {"hip": "qdata must be a 2-D int8 tensor"})
     if x.dtype not in _FLOAT:
         raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
     n, k = qdata.shape
+    lora = _lora_args(op, lora_down, lora_up, lora_scale, n, k)
     x2, lead = _as_2d(x, k)
     y, shape = _out(x2, lead, n, out_dtype, x)
     if x2.shape[0] == 0 or n == 0:
@@ -113,6 +146,7 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(y), g,
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
+    _apply_lora(op, lora, x2, y)
     return y.reshape(shape)
 
 
@@ -160,7 +194,6 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     against the int8 weight grid, y = acc * sx[m] * s_channel[n] + bias."""
     op = "w4a8_int8_linear"
     _disabled(op)
-    _decline_lora(op, lora_down, lora_up, lora_scale)
     if correction is not None:
         raise NoCapableBackendError(op, {"hip": "the asymmetric `correction` variant is not implemented"})
     _check_device(op, x, qdata, s_rel, s_channel, codebook, bias)
@@ -168,6 +201,7 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
         raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
     bits, k = _bits_of(qdata, s_rel, group_size)
     n = qdata.shape[0]
+    lora = _lora_args(op, lora_down, lora_up, lora_scale, n, k)
     x2, lead = _as_2d(x, k)
     y, shape = _out(x2, lead, n, out_dtype, x)
     if x2.shape[0] == 0 or n == 0:
@@ -182,6 +216,7 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
                             _lib.desc(b), _lib.desc(y), bits, int(group_size), int(convrot_groupsize or 0),
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
+    _apply_lora(op, lora, x2, y)
     return y.reshape(shape)
 
 
@@ -250,10 +285,10 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
     `weight` is the tensor's raw bytes (uint8, [N, K/qk*ts] or flat)."""
     op = "gguf_linear"
     _disabled(op)
-    _decline_lora(op, lora_down, lora_up, lora_scale)
     _check_device(op, x, weight, bias)
     tid = gguf_type_id(qtype)
     n, k = int(shape[0]), int(shape[1])
+    lora = _lora_args(op, lora_down, lora_up, lora_scale, n, k)
     if weight.dtype != torch.uint8:
         raise NoCapableBackendError(op, {"hip": "weight must be the uint8 block bytes"})
     if not weight.is_contiguous():
@@ -272,6 +307,7 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
     st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(y),
                                       ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
+    _apply_lora(op, lora, x2, y)
     return y.reshape(oshape)
 
 

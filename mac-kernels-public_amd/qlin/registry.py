@@ -18,9 +18,9 @@ from .exceptions import NoCapableBackendError
 
 # func name -> (callable, keyword arguments the backend accepts beyond the plain signature)
 _HIP = {
-    "int8_linear": (ops.int8_linear, set()),
-    "w4a8_int8_linear": (ops.w4a8_int8_linear, set()),
-    "gguf_linear": (ops.gguf_linear, set()),
+    "int8_linear": (ops.int8_linear, {"lora_down", "lora_up", "lora_scale"}),
+    "w4a8_int8_linear": (ops.w4a8_int8_linear, {"lora_down", "lora_up", "lora_scale"}),
+    "gguf_linear": (ops.gguf_linear, {"lora_down", "lora_up", "lora_scale"}),
     "dequantize_gguf": (ops.dequantize_gguf, set()),
     "dequantize_int8_convrot_weight": (ops.dequantize_int8_convrot_weight, set()),
     "dequantize_w4a8_int8_weight": (ops.dequantize_w4a8_int8_weight, set()),

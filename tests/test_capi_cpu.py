@@ -92,8 +92,10 @@ def test_registry():
     from qlin.exceptions import NoCapableBackendError
     fn = qlin.registry.get_implementation("int8_linear")
     assert fn is qlin.int8_linear
+    # the lora_* keywords are declared by the three linears; other opt-in keywords still decline
+    assert qlin.registry.get_implementation("gguf_linear", kwargs={"lora_down": object()}) is qlin.gguf_linear
     with pytest.raises(NoCapableBackendError) as e:
-        qlin.registry.get_implementation("int8_linear", kwargs={"lora_down": object()})
+        qlin.registry.get_implementation("int8_linear", kwargs={"correction": object()})
     assert "hip" in e.value.reasons
     with pytest.raises(NoCapableBackendError):
         qlin.registry.get_implementation("scaled_mm_nvfp4")

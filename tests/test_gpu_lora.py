@@ -1,0 +1,156 @@
+"""Unmerged LoRA (lora_down / lora_up / lora_scale) on the three quantized linears, on the GPU.
+
+Reference semantics (roblennon/mac-kernels-public tests/test_lora_sidepath.py:80-91,
+tests/test_gguf_node.py:110-174): the output equals the linear over the dequantized base weight
+plus delta = scale * up @ down, applied to the caller's activation (before ConvRot).  Checked here:
+  - the side term y(lora) - y(base) against the exact float64 product scale * (x down^T) up^T,
+    within the reference's bar: 2 eps(out dtype) * max|y| + 2e-3 * max|side|;
+  - the whole output against the oracle's float64 linear plus that product, within 1e-3 relative
+    Frobenius and 2e-2 max-abs error;
+  - the reference's overflow case (a merged delta of 2 from factors 4e4 and 2.5e-5) to the bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def qlin():
+    import qlin as Q
+    return Q
+
+
+def qz():
+    from qlin import quantize as QZ
+    return QZ
+
+
+def factors(n, k, r, dt_down, dt_up, seed=5):
+    g = torch.Generator().manual_seed(seed)
+    up = (torch.randn(n, r, generator=g) * 0.05).to(dt_up)
+    down = (torch.randn(r, k, generator=g) * 0.05).to(dt_down)
+    return down, up
+
+
+def side_ref(x, down, up, scale):
+    x64 = x.double().cpu().numpy().reshape(-1, x.shape[-1])
+    return scale * (x64 @ down.double().numpy().T) @ up.double().numpy().T
+
+
+def check_side(y_lora, y_base, ref, what):
+    eps = torch.finfo(y_lora.dtype).eps
+    got = y_lora.float().cpu().numpy().reshape(ref.shape).astype(np.float64)
+    base = y_base.float().cpu().numpy().reshape(ref.shape).astype(np.float64)
+    assert np.isfinite(got).all(), what
+    tol = 2 * eps * float(np.abs(got).max()) + 2e-3 * float(np.abs(ref).max())
+    err = float(np.abs((got - base) - ref).max())
+    assert err <= tol, f"{what}: side error {err:.3e} > {tol:.3e}"
+
+
+def check_full(y, want, what):
+    got = y.float().cpu().numpy().reshape(want.shape).astype(np.float64)
+    rel = O.rel_fro(got, want)
+    mx = float(np.abs(got - want).max())
+    assert rel < 1e-3 and mx < 2e-2, f"{what}: rel_fro={rel:.3e} max_abs={mx:.3e}"
+
+
+@pytest.mark.parametrize("m,r,xdt,fdt", [(64, 16, torch.bfloat16, torch.bfloat16), (37, 1, torch.float16, torch.float16),
+                                         (300, 64, torch.bfloat16, torch.float32), (5, 200, torch.float16, torch.bfloat16)])
+def test_int8_convrot_lora(m, r, xdt, fdt):
+    Q = qlin()
+    n, k, g = 384, 512, 256
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(0)) * 0.02).numpy()
+    qn, sn = qz().quantize_int8_convrot_weight(w, g)
+    q, s = torch.from_numpy(qn).to(DEV), torch.from_numpy(sn).reshape(-1).to(DEV)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(1)) * 0.5).to(xdt)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(2)) * 0.1).half().to(DEV)
+    down, up = factors(n, k, r, fdt, fdt)
+    base = Q.int8_linear(x.to(DEV), q, s, b, convrot=True, convrot_groupsize=g)
+    y = Q.int8_linear(x.to(DEV), q, s, b, convrot=True, convrot_groupsize=g,
+                      lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.8)
+    assert y.dtype == xdt and y.shape == (m, n)
+    ref = side_ref(x, down, up, 0.8)
+    check_side(y, base, ref, f"int8 m={m} r={r}")
+    if xdt == torch.float16:
+        wdq = O.dequantize_int8_convrot(qn, sn, g)  # original basis, so x enters unrotated
+        want = O.linear_ref(x.float().numpy(), wdq) + b.double().cpu().numpy()[None, :] + ref
+        check_full(y, want, "int8 full")
+
+
+@pytest.mark.parametrize("bits,m", [(4, 48), (6, 1100), (6, 3)])
+def test_w4a8_lora(bits, m):
+    Q = qlin()
+    n, k, g, gs = 256, 1024, 256, 64
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(3)) * 0.02).numpy()
+    q, s_rel, s_ch, book = qz().quantize_w4a8_int8_weight(w, bits=bits, group_size=gs, convrot_groupsize=g,
+                                                          codebook=None, s_rel_dtype=torch.float16)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(4)).half()
+    down, up = factors(n, k, 32, torch.bfloat16, torch.bfloat16)
+    dev = lambda t: t.to(DEV)
+    base = Q.w4a8_int8_linear(dev(x), dev(q), dev(s_rel), dev(s_ch), None, None, None, gs, g)
+    y = Q.w4a8_int8_linear(dev(x), dev(q), dev(s_rel), dev(s_ch), None, None, None, gs, g,
+                           lora_down=dev(down), lora_up=dev(up), lora_scale=1.5)
+    check_side(y, base, side_ref(x, down, up, 1.5), f"w{bits}a8 m={m}")
+
+
+@pytest.mark.parametrize("name,m", [("Q4_K", 1), ("Q4_K", 8), ("Q8_0", 64), ("Q6_K", 5), ("IQ4_XS", 130)])
+def test_gguf_lora(name, m):
+    Q = qlin()
+    n, k = 192, 512
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(6)) * 0.02).numpy()
+    raw = torch.from_numpy(qz().quantize_gguf(w, name)).to(DEV)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(7)).half()
+    down, up = factors(n, k, 16, torch.float16, torch.bfloat16)
+    base = Q.gguf_linear(x.to(DEV), raw, name, (n, k))
+    y = Q.gguf_linear(x.to(DEV), raw, name, (n, k), lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.5)
+    ref = side_ref(x, down, up, 0.5)
+    check_side(y, base, ref, f"{name} m={m}")
+    wdq = O.gguf_dequantize(raw.cpu().numpy(), name, (n, k))
+    check_full(y, O.linear_ref(x.float().numpy(), wdq) + ref, f"{name} full")
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("large_down", [False, True])
+def test_lora_large_factors_exact(xdt, large_down):
+    """tests/test_gguf_node.py:139-165: Q8_0 [3, 32] with zero codes, x = 1, up and down of 4e4 and
+    2.5e-5 (either way round), strength 2: every output is exactly 64 (fp16 factors or an fp16
+    intermediate would overflow or round away from it)."""
+    Q = qlin()
+    packed = torch.zeros(3, 34, dtype=torch.uint8)
+    packed[:, :2] = torch.tensor([0.02], dtype=torch.float16).view(torch.uint8)
+    up_value, down_value = (0.000025, 40000.) if large_down else (40000., 0.000025)
+    up = torch.full((3, 1), up_value)
+    down = torch.full((1, 32), down_value)
+    x = torch.ones(2, 32, dtype=xdt, device=DEV)
+    y = Q.gguf_linear(x, packed.to(DEV), "Q8_0", (3, 32), lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=2.0)
+    assert y.dtype == xdt and torch.isfinite(y).all()
+    torch.testing.assert_close(y.cpu(), torch.full((2, 3), 64.0, dtype=xdt), rtol=0, atol=0)
+
+
+def test_lora_arguments():
+    Q = qlin()
+    n, k = 64, 256
+    q = torch.zeros(n, k, dtype=torch.int8, device=DEV)
+    s = torch.ones(n, device=DEV)
+    x = torch.randn(3, k, device=DEV).half()
+    down = torch.randn(8, k, device=DEV).half() * 0.1
+    up = torch.randn(n, 8, device=DEV).half() * 0.1
+    base = Q.int8_linear(x, q, s)
+    # lora_scale None means 1.0; non-contiguous factors are accepted
+    y1 = Q.int8_linear(x, q, s, lora_down=down, lora_up=up)
+    yt = Q.int8_linear(x, q, s, lora_down=down.t().contiguous().t(), lora_up=up.t().contiguous().t(), lora_scale=1.0)
+    torch.testing.assert_close(y1, yt, rtol=0, atol=0)
+    check_side(y1, base, side_ref(x.cpu(), down.cpu().float(), up.cpu().float(), 1.0), "scale None")
+    with pytest.raises(ValueError):
+        Q.int8_linear(x, q, s, lora_down=down)
+    with pytest.raises(ValueError):
+        Q.int8_linear(x, q, s, lora_down=down, lora_up=up[:, :4])
+    with pytest.raises(ValueError):
+        Q.int8_linear(x, q, s, lora_scale=0.5)
+    # empty activations
+    e = Q.int8_linear(torch.empty(0, k, device=DEV).half(), q, s, lora_down=down, lora_up=up)
+    assert e.shape == (0, n)

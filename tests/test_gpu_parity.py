@@ -196,7 +196,7 @@ def test_gguf_linear_shapes_and_empty():
     xs = torch.randn(5, k + 8, device=DEV).half()[:, 8:]  # strided rows with a storage offset
     torch.testing.assert_close(Q.gguf_linear(xs, raw, name, (n, k)), Q.gguf_linear(xs.contiguous(), raw, name, (n, k)),
                                rtol=0, atol=0)
-    with pytest.raises(Q.NoCapableBackendError):
+    with pytest.raises(ValueError):  # lora_down without lora_up
         Q.gguf_linear(x, raw, name, (n, k), lora_down=torch.zeros(1, k, device=DEV))
 
 
@@ -449,5 +449,5 @@ def test_w4a8_declines():
     x = torch.randn(2, 256, device=DEV).half()
     with pytest.raises(Q.NoCapableBackendError):
         Q.w4a8_int8_linear(x, q, sr, sc, None, torch.zeros(16, 16, device=DEV))
-    with pytest.raises(Q.NoCapableBackendError):
+    with pytest.raises(ValueError):  # lora_up without lora_down
         Q.w4a8_int8_linear(x, q, sr, sc, lora_up=torch.zeros(16, 1, device=DEV))
