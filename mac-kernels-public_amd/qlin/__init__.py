@@ -7,6 +7,7 @@ decoded inside the kernels).  Everything runs in libqlin.so (HIP, C ABI in inclu
 """
 from .exceptions import NoCapableBackendError, QlinError
 from .gguf import GGUF_TYPES, gguf_type_id
+from .loader import PackedLinear, gguf_header, load_gguf, load_safetensors, quantized_linears, safetensors_header
 from .ops import (
     dequantize_gguf,
     dequantize_int8,
@@ -23,5 +24,6 @@ from .registry import registry
 __all__ = [
     "NoCapableBackendError", "QlinError", "GGUF_TYPES", "gguf_type_id", "dequantize_gguf", "dequantize_int8",
     "dequantize_int8_convrot_weight", "dequantize_w4a8_int8_weight", "gguf_linear", "int8_linear",
-    "quantize_int8_rowwise", "w4a8_int8_grid", "w4a8_int8_linear", "registry",
+    "quantize_int8_rowwise", "w4a8_int8_grid", "w4a8_int8_linear", "registry", "PackedLinear", "gguf_header",
+    "load_gguf", "load_safetensors", "quantized_linears", "safetensors_header",
 ]
