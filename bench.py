@@ -13,7 +13,7 @@ its average launch duration (HIP events around graph replays of that call alone)
 HBM peak; `traffic` is its measured HBM bytes per launch from the committed counter summary.
 cpu_baseline: the oracle's dequantize-then-matmul on the host (C decode, fp32 BLAS matmul).
 
-Other suites (--suite int8|w4a8|w6a8|dit|lora|all) print their own JSON lines to stderr.
+Other suites (--suite int8|w4a8|w6a8|dit|lora|grad|all) print their own JSON lines to stderr.
 """
 import argparse
 import json
@@ -362,6 +362,26 @@ def other_suites(which, steps, warmup):
                 y.addmm_(torch.nn.functional.linear(x, down), up.t(), alpha=0.8)
             timed(f"lora unfused {fmt} r{r} (bf16 addmm beside the call)", unfused, fl + flr,
                   n * k + m * k * 2 + m * n * 4, peak, unit)
+    if which in ("grad", "all"):
+        # frozen-weight input gradient at the reference's training shapes: 1056 tokens, Krea 2
+        # layers attn.wq 6144->6144, attn.wk 6144->1536, mlp.up 6144->16384, mlp.down 16384->6144;
+        # fp16 dy, INT8-ConvRot weights.  Beside it: torch's dense fp16 dy @ W on a resident fp16
+        # weight, and dequantizing the whole layer to fp16 before that GEMM.
+        m = 1056
+        for name, k, n in (("attn.wq", 6144, 6144), ("attn.wk", 6144, 1536), ("mlp.up", 6144, 16384),
+                           ("mlp.down", 16384, 6144)):
+            q, s = quantize_int8_convrot_weight(weight(n, k), 256)
+            qd, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+            dy = torch.randn(m, n).half().cuda()
+            wd = qlin.dequantize_int8_convrot_weight(qd, sd, 256).half()
+            fl = 2 * m * n * k
+            timed(f"grad int8_convrot {name} M{m} K{k} N{n}", lambda: qlin.int8_linear_grad_input(dy, qd, sd, True, 256),
+                  fl, n * k + m * n * 2 + m * k * 2, FP16_PEAK_TFLOPS, "TFLOPs")
+            timed(f"grad dense fp16 torch {name}", lambda: dy @ wd, fl, n * k * 2 + m * n * 2 + m * k * 2,
+                  FP16_PEAK_TFLOPS, "TFLOPs")
+            timed(f"grad dequantize-then-gemm {name}", lambda: dy @ (qd.half() * sd.half()[:, None]), fl,
+                  n * k * 5 + m * n * 2 + m * k * 2, FP16_PEAK_TFLOPS, "TFLOPs")
+            del wd
     return out
 
 
@@ -370,7 +390,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--suite", default="gguf", choices=["gguf", "int8", "w4a8", "w6a8", "dit", "lora", "all"])
+    ap.add_argument("--suite", default="gguf", choices=["gguf", "int8", "w4a8", "w6a8", "dit", "lora", "grad", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-rows", type=int, default=1024, help="weight rows decoded per call for the CPU baseline")
     ap.add_argument("--profile", action="store_true",

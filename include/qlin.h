@@ -59,6 +59,8 @@ typedef enum {
     QLIN_OP_W4A8_LINEAR = 1,
     QLIN_OP_GGUF_LINEAR = 2,
     QLIN_OP_LORA = 3,   /* qlin_lora_apply: param = the LoRA rank R */
+    QLIN_OP_INT8_GRAD_INPUT = 4,  /* qlin_int8_linear_grad_input: M rows of dy, N outputs, K inputs */
+    QLIN_OP_W4A8_GRAD_INPUT = 5,  /* qlin_w4a8_linear_grad_input (holds the decoded int8 grid, N*K bytes) */
 } qlin_op;
 
 /* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
@@ -126,6 +128,28 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
 qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
                             float lora_scale, qlin_tensor* y, void* workspace, size_t workspace_bytes,
                             void* stream);
+
+/* Input gradient of the frozen INT8 linear: dx [M,K] = dy [M,N] @ W with W = rotate(q * scale) the
+ * weight in the original basis (convrot_groupsize 0 = no rotation), i.e. dx = ((dy * scale) @ q) H.
+ * dy * scale is normalized per row by a power of two and rounded once to fp16; the product runs on
+ * fp16 MFMA with exact int8 operands and fp32 accumulation; dx is rounded once to its dtype
+ * (f32/f16/bf16).  K must be a multiple of 16 and of the group; N >= 1.  No gradient for the codes,
+ * scale or bias.  Workspace: qlin_workspace_size(QLIN_OP_INT8_GRAD_INPUT, M, N, K, 0, dy_dtype).
+ * Replaces comfy_kitchen int8_linear_grad_input(dy, qdata, scale, convrot, convrot_groupsize,
+ * out_dtype) (bench/bench_int8_backward.py:15, 52) and the backward of int8_linear_trainable
+ * (train/train_lora.py:187-188, 210). */
+qlin_status qlin_int8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                        int convrot_groupsize, qlin_tensor* dx, void* workspace,
+                                        size_t workspace_bytes, void* stream);
+
+/* Input gradient of the frozen W4A8 / W6A8 linear: dx = dy @ W with W = rotate(s_channel * grid) the
+ * dequantized weight (grid = the int8 grid of the codes, as qlin_dequantize_w4a8 with an int8
+ * output); same arithmetic as qlin_int8_linear_grad_input.  Replaces the backward of comfy_kitchen
+ * w4a8_linear_trainable (train/train_lora.py:221-223; tests/test_training_packed.py:33-36). */
+qlin_status qlin_w4a8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                        const qlin_tensor* s_channel, const qlin_tensor* codebook, qlin_tensor* dx,
+                                        int bits, int group_size, int convrot_groupsize, void* workspace,
+                                        size_t workspace_bytes, void* stream);
 
 /* Decode GGUF blocks to a dense [N,K] f32 (bit-exact with gguf-py 0.19.0's fp32 decode), or
  * f16/bf16 (that value rounded once, to nearest even).  Rows may straddle blocks (flat index).

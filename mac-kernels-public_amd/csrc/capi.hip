@@ -142,6 +142,12 @@ size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
     return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
            (S > 1 ? align_up((size_t)S * M * N * 4) : 0);
 }
+// input gradient: normalized dy rows (N rounded up to 64) + row exponents (+ the W4A8 int8 grid)
+size_t ws_grad(int64_t M, int64_t N, int64_t K, bool grid) {
+    const int64_t lda = (N + 63) / 64 * 64;
+    return align_up((size_t)(M * lda * 2)) + align_up((size_t)M * 4) + (grid ? align_up((size_t)(N * K)) : 0);
+}
+
 size_t ws_w4a8(int64_t M, int64_t N, int64_t K) {
     return align_up((size_t)(M * K)) + align_up((size_t)M * 4) + (a8_decode_once(M, K) ? align_up((size_t)(N * K)) : 0);
 }
@@ -201,6 +207,8 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
         case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K);
         case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param);
+        case QLIN_OP_INT8_GRAD_INPUT: return ws_grad(M, N, K, false);
+        case QLIN_OP_W4A8_GRAD_INPUT: return ws_grad(M, N, K, true);
         case QLIN_OP_LORA: {  // the split partials, then their sum
             const int S = lora_splits(M, K, param);
             return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(param > 0 ? param : 0) * 4);
@@ -233,6 +241,98 @@ qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x
         }
     }
     return fail(QLIN_EUNSUPPORTED, "unknown op %d", op);
+}
+
+// dx = ((dy diag(s)) b) H on the GPU: the row prologue, then the gradient GEMM.
+static qlin_status grad_input(const Mat& DY, const Mat& DX, const int8_t* b, int64_t ldb, int64_t N, int64_t K,
+                              const void* sc, int sc_dt, int64_t sst, int G, Carver& ws, hipStream_t st) {
+    const int64_t M = DY.rows, lda = (N + 63) / 64 * 64;
+    f16* a = (f16*)ws.take((size_t)(M * lda * 2));
+    int32_t* e = (int32_t*)ws.take((size_t)M * 4);
+    qlin_status s;
+    if ((s = hip_status(run_bwd_rows(DY.data, DY.dtype, DY.ld, M, N, sc, sc_dt, sst, a, lda, e, st), "gradient rows")))
+        return s;
+    BwdGemmArgs p;
+    p.a = a; p.lda = lda; p.e = e; p.b = b; p.ldb = ldb; p.M = M; p.N = N; p.K = K; p.G = G;
+    p.out = DX.data; p.out_dt = DX.dtype; p.ldo = DX.ld;
+    return hip_status(run_bwd_gemm(p, st), "gradient gemm");
+}
+
+static qlin_status grad_shapes(int64_t N, int64_t K, int G) {
+    if (N < 1) return fail(QLIN_EUNSUPPORTED, "N = 0 (the gradient is zero)");
+    if (K % 16) return fail(QLIN_EUNSUPPORTED, "K %% 16 != 0");
+    if (!valid_group(G)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", G);
+    if (G && K % G) return fail(QLIN_EINVAL, "K %% ConvRot group != 0");
+    return QLIN_OK;
+}
+
+qlin_status qlin_int8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                        int convrot_groupsize, qlin_tensor* dx, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    Mat Q, DY, DX;
+    qlin_status s = as_matrix(qdata, "qdata", Q);
+    if (s) return s;
+    if (Q.dtype != QLIN_DT_I8) return fail(QLIN_EUNSUPPORTED, "qdata must be int8");
+    const int64_t N = Q.rows, K = Q.cols;
+    // dy [M, N] in, dx [M, K] out
+    if ((s = check_xy(dy, dx, K, N, DY, DX))) return s;
+    if ((s = grad_shapes(N, K, convrot_groupsize))) return s;
+    if (Q.ld % 4 || (uintptr_t)Q.data % 4) return fail(QLIN_EUNSUPPORTED, "qdata rows must be 4-byte aligned");
+    int64_t sst;
+    if ((s = as_vector(scale, "scale", N, true, sst))) return s;
+    if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype %d unsupported", scale->dtype);
+    const int64_t M = DY.rows;
+    if (workspace_bytes < ws_grad(M, N, K, false))
+        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_grad(M, N, K, false));
+    if (M == 0) return QLIN_OK;
+    Carver ws{(uint8_t*)workspace, workspace_bytes};
+    return grad_input(DY, DX, (const int8_t*)Q.data, Q.ld, N, K, scale->data, scale->dtype, sst, convrot_groupsize, ws,
+                      (hipStream_t)stream);
+}
+
+qlin_status qlin_w4a8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                        const qlin_tensor* s_channel, const qlin_tensor* codebook, qlin_tensor* dx,
+                                        int bits, int group_size, int convrot_groupsize, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    if (bits != 4 && bits != 6) return fail(QLIN_EUNSUPPORTED, "bits=%d unsupported (4 or 6)", bits);
+    Mat Q, DY, DX, SR;
+    qlin_status s = as_matrix(qdata, "qdata", Q);
+    if (s) return s;
+    if (Q.dtype != QLIN_DT_I8 && Q.dtype != QLIN_DT_U8) return fail(QLIN_EUNSUPPORTED, "qdata must be int8/uint8");
+    if ((Q.cols * 8) % bits) return fail(QLIN_EINVAL, "qdata columns do not hold whole codes");
+    const int64_t N = Q.rows, K = Q.cols * 8 / bits;
+    if ((s = check_xy(dy, dx, K, N, DY, DX))) return s;
+    if ((s = grad_shapes(N, K, convrot_groupsize))) return s;
+    if (group_size <= 0 || K % group_size) return fail(QLIN_EINVAL, "group_size does not divide K");
+    if ((s = as_matrix(s_rel, "s_rel", SR))) return s;
+    if (SR.rows != N || SR.cols != K / group_size)
+        return fail(QLIN_EINVAL, "s_rel must be [%lld, %lld]", (long long)N, (long long)(K / group_size));
+    if (SR.dtype != QLIN_DT_E4M3 && SR.dtype != QLIN_DT_F16 && SR.dtype != QLIN_DT_BF16 && SR.dtype != QLIN_DT_F32 &&
+        SR.dtype != QLIN_DT_U8)
+        return fail(QLIN_EUNSUPPORTED, "s_rel dtype %d unsupported", SR.dtype);
+    int64_t sst;
+    if ((s = as_vector(s_channel, "s_channel", N, false, sst))) return s;
+    if (s_channel->dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "s_channel must be float32");
+    const float* cb = nullptr;
+    if (codebook && codebook->data) {
+        if (bits != 4) return fail(QLIN_EUNSUPPORTED, "a codebook is only defined for 4-bit codes");
+        int64_t cst;
+        if ((s = as_vector(codebook, "codebook", 16, false, cst))) return s;
+        if (codebook->dtype != QLIN_DT_F32 || cst != 1) return fail(QLIN_EUNSUPPORTED, "codebook must be contiguous float32");
+        cb = (const float*)codebook->data;
+    }
+    const int64_t M = DY.rows;
+    if (workspace_bytes < ws_grad(M, N, K, true))
+        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_grad(M, N, K, true));
+    if (M == 0) return QLIN_OK;
+    hipStream_t st = (hipStream_t)stream;
+    Carver ws{(uint8_t*)workspace, workspace_bytes};
+    int8_t* grid = (int8_t*)ws.take((size_t)(N * K));
+    const int srdt = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype;
+    if ((s = hip_status(run_dequant_w4a8((const uint8_t*)Q.data, N, K, Q.ld, bits, group_size, SR.data, srdt, SR.ld,
+                                         (const float*)s_channel->data, cb, grid, DT_I8, st), "w4a8 grid")))
+        return s;
+    return grad_input(DY, DX, grid, K, N, K, s_channel->data, DT_F32, sst, convrot_groupsize, ws, st);
 }
 
 qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,

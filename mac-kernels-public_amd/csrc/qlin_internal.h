@@ -160,6 +160,23 @@ struct LoraArgs {
     int64_t ldy = 0;
 };
 hipError_t run_lora(const LoraArgs& a, hipStream_t st);
+
+// ---- frozen-weight input gradient (backward.hip) ----
+struct BwdGemmArgs {
+    const f16* a = nullptr;      // [M][lda] normalized dy * s, zero past N (lda = N rounded up to 64)
+    int64_t lda = 0;
+    const int32_t* e = nullptr;  // [M] row exponents
+    const int8_t* b = nullptr;   // [N][ldb] int8 weight codes (rotated basis)
+    int64_t ldb = 0;
+    int64_t M = 0, N = 0, K = 0;
+    int G = 0;                   // ConvRot group applied to the output rows (0 = none)
+    void* out = nullptr;         // dx [M][ldo]
+    int out_dt = DT_F16;
+    int64_t ldo = 0;
+};
+hipError_t run_bwd_rows(const void* dy, int dy_dt, int64_t ldd, int64_t M, int64_t N, const void* s, int s_dt,
+                        int64_t s_stride, f16* a, int64_t lda, int32_t* e, hipStream_t st);
+hipError_t run_bwd_gemm(const BwdGemmArgs& p, hipStream_t st);
 // K splits of the LoRA down-projection for this shape (the workspace holds that many partials).
 int lora_splits(int64_t M, int64_t K, int64_t R);
 hipError_t run_gemm_i8(const GemmI8Args& a, hipStream_t st);
