@@ -142,9 +142,9 @@ size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
     return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
            (S > 1 ? align_up((size_t)S * M * N * 4) : 0);
 }
-// input gradient: normalized dy rows (N rounded up to 64) + row exponents (+ the W4A8 int8 grid)
+// input gradient: normalized dy rows (N rounded up to 128) + row exponents (+ the W4A8 int8 grid)
 size_t ws_grad(int64_t M, int64_t N, int64_t K, bool grid) {
-    const int64_t lda = (N + 63) / 64 * 64;
+    const int64_t lda = (N + 127) / 128 * 128;
     return align_up((size_t)(M * lda * 2)) + align_up((size_t)M * 4) + (grid ? align_up((size_t)(N * K)) : 0);
 }
 
@@ -246,7 +246,7 @@ qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x
 // dx = ((dy diag(s)) b) H on the GPU: the row prologue, then the gradient GEMM.
 static qlin_status grad_input(const Mat& DY, const Mat& DX, const int8_t* b, int64_t ldb, int64_t N, int64_t K,
                               const void* sc, int sc_dt, int64_t sst, int G, Carver& ws, hipStream_t st) {
-    const int64_t M = DY.rows, lda = (N + 63) / 64 * 64;
+    const int64_t M = DY.rows, lda = (N + 127) / 128 * 128;
     f16* a = (f16*)ws.take((size_t)(M * lda * 2));
     int32_t* e = (int32_t*)ws.take((size_t)M * 4);
     qlin_status s;

@@ -163,7 +163,7 @@ hipError_t run_lora(const LoraArgs& a, hipStream_t st);
 
 // ---- frozen-weight input gradient (backward.hip) ----
 struct BwdGemmArgs {
-    const f16* a = nullptr;      // [M][lda] normalized dy * s, zero past N (lda = N rounded up to 64)
+    const f16* a = nullptr;      // [M][lda] normalized dy * s, zero past N (lda = N rounded up to 128)
     int64_t lda = 0;
     const int32_t* e = nullptr;  // [M] row exponents
     const int8_t* b = nullptr;   // [N][ldb] int8 weight codes (rotated basis)
