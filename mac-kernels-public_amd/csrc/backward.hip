@@ -11,8 +11,8 @@
 //   bwd_gemm_kernel: c = a q over n with fp16 MFMA (the int8 codes are exact fp16), one
 //     workgroup per 128 rows x 256 columns of dx; the weight tile is read row by row (k
 //     contiguous) and written to LDS transposed, k-major, still int8, so that every MFMA
-//     fragment is one 8-byte LDS read widened in registers; the epilogue scales rows by 2^E[m], applies H to each 16-lane run of
-//     the row and rounds once to dx's dtype.
+//     fragment is one 8-byte LDS read widened in registers; the epilogue scales rows by
+//     2^E[m], applies H to each 16-lane run of the row and rounds once to dx's dtype.
 #include "qlin_internal.h"
 #include "hadamard.h"
 
@@ -151,8 +151,9 @@ struct BwdRegs {
 // + 63 and columns 64 (w % 4) .. + 63 of the tile (2 x 2 sub-tiles of 32 x 32).  Stage = 64 values
 // of n: a tile [128][64] fp16 and weight tile [64][256] int8, the latter stored in LDS transposed
 // as [256][64] int8 and widened to fp16 after each fragment read.  Two LDS buffers and two
-// register sets: each stage's global loads are issued two stages before it is computed; at most
-// 128 registers, so that two workgroups share a CU.
+// register sets: each stage's global loads are issued two stages before it is computed (174
+// registers: one workgroup per CU).  Measured at M = 1056: a three-set ring, buffer loads with
+// scalar row offsets, and a 128-register cap (two workgroups per CU, with spills) were all slower.
 // The tile size sets the operand bytes per MFMA: at 128 x 256 a 64-value stage brings 32 KB for
 // 4.2 MFLOP.
 template <int G>
