@@ -329,9 +329,17 @@ qlin_status qlin_w4a8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor
     Carver ws{(uint8_t*)workspace, workspace_bytes};
     int8_t* grid = (int8_t*)ws.take((size_t)(N * K));
     const int srdt = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype;
-    if ((s = hip_status(run_dequant_w4a8((const uint8_t*)Q.data, N, K, Q.ld, bits, group_size, SR.data, srdt, SR.ld,
-                                         (const float*)s_channel->data, cb, grid, DT_I8, st), "w4a8 grid")))
+    GemmI8Args g;  // the forward's grid decode (one thread per 64 codes) when its layout allows
+    g.N = N; g.K = K; g.q = (const uint8_t*)Q.data; g.ldq = Q.ld; g.bits = bits; g.group_size = group_size;
+    g.s_rel = SR.data; g.s_rel_dtype = srdt; g.ld_srel = SR.ld; g.s_ch = (const float*)s_channel->data;
+    g.codebook = cb; g.w8 = grid;
+    if (a8_grid_supported(g)) {
+        if ((s = hip_status(run_a8_grid(g, st), "w4a8 grid"))) return s;
+    } else if ((s = hip_status(run_dequant_w4a8((const uint8_t*)Q.data, N, K, Q.ld, bits, group_size, SR.data, srdt,
+                                                SR.ld, (const float*)s_channel->data, cb, grid, DT_I8, st),
+                               "w4a8 grid"))) {
         return s;
+    }
     return grad_input(DY, DX, grid, K, N, K, s_channel->data, DT_F32, sst, convrot_groupsize, ws, st);
 }
 

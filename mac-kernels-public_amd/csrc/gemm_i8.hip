@@ -809,7 +809,33 @@ hipError_t launch_s(const GemmI8Args& p, hipStream_t st) {
     return hipErrorInvalidValue;
 }
 
+template <int BITS, bool CB>
+hipError_t launch_grid(const GemmI8Args& p, hipStream_t st) {
+    const int64_t segs = p.N * (p.K / 64);
+    const dim3 grid((unsigned)((segs + 255) / 256));
+    switch (p.s_rel_dtype) {
+        case DT_E4M3: hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, uint8_t>), grid, dim3(256), 0, st, p, p.w8); break;
+        case DT_F16: hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, f16>), grid, dim3(256), 0, st, p, p.w8); break;
+        case DT_BF16: hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, bf16_t>), grid, dim3(256), 0, st, p, p.w8); break;
+        case DT_F32: hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, float>), grid, dim3(256), 0, st, p, p.w8); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
+
+bool a8_grid_supported(const GemmI8Args& p) {
+    return (p.bits == 4 || (p.bits == 6 && !p.codebook)) && p.K % 64 == 0 && p.group_size % 64 == 0 &&
+           p.ldq % 16 == 0 && (uintptr_t)p.q % 16 == 0 && (uintptr_t)p.w8 % 16 == 0;
+}
+
+hipError_t run_a8_grid(const GemmI8Args& p, hipStream_t st) {
+    if (p.N == 0 || p.K == 0) return hipSuccess;
+    if (!a8_grid_supported(p)) return hipErrorInvalidValue;
+    if (p.bits == 4) return p.codebook ? launch_grid<4, true>(p, st) : launch_grid<4, false>(p, st);
+    return launch_grid<6, false>(p, st);
+}
 
 hipError_t run_gemm_i8(const GemmI8Args& p, hipStream_t st) {
     if (p.M == 0 || p.N == 0) return hipSuccess;

@@ -138,6 +138,10 @@ struct GemmI8Args {
 // Activation rows from which the A8 linear decodes the weight grid once into the workspace
 // (N * K bytes) instead of once per 256-row tile inside the GEMM.
 inline bool a8_decode_once(int64_t M, int64_t K) { return M >= 1024 && K % 128 == 0; }
+// The int8 weight grid alone into p.w8 ([N][K], row stride K), one thread per 64-code segment:
+// group_size a multiple of 64, 16-byte aligned code rows.
+bool a8_grid_supported(const GemmI8Args& p);
+hipError_t run_a8_grid(const GemmI8Args& p, hipStream_t st);
 
 // Unmerged LoRA: y += scale * (x down^T) up^T after the base linear (lora.hip).
 struct LoraArgs {

@@ -95,10 +95,13 @@ def test_int8_grad_input_strided_and_batched():
     assert Q.int8_linear_grad_input(dy[:0], q, s, True, 256).shape == (0, k)
 
 
-@pytest.mark.parametrize("bits,codebook,g,m", [(4, "auto", 256, 48), (4, None, 128, 7), (6, None, 256, 100)])
-def test_w4a8_grad_input(bits, codebook, g, m):
+# group sizes 16 and 32 decode the grid element by element; 64 and 128 take the forward's
+# 64-code segment decode
+@pytest.mark.parametrize("bits,codebook,g,m,gs", [(4, "auto", 256, 48, 16), (4, None, 128, 7, 16), (6, None, 256, 100, 32),
+                                                  (4, "auto", 256, 33, 128), (6, None, 128, 20, 64)])
+def test_w4a8_grad_input(bits, codebook, g, m, gs):
     Q = qlin()
-    n, k, gs = 256, 1024, 16 if bits == 4 else 32
+    n, k = 256, 1024
     w = (torch.randn(n, k, generator=torch.Generator().manual_seed(4)) * 0.02).numpy()
     q, s_rel, s_ch, book = qz().quantize_w4a8_int8_weight(w, bits=bits, group_size=gs, convrot_groupsize=g,
                                                           codebook=codebook)
