@@ -9,10 +9,10 @@
 //     max |dy s| (one rounding, no overflow or underflow of the row's large values), rows
 //     zero-padded to a multiple of 128;
 //   bwd_gemm_kernel: c = a q over n with fp16 MFMA (the int8 codes are exact fp16), one
-//     workgroup per 128 rows x 256 columns of dx; the weight tile is read row by row (k
-//     contiguous) and written to LDS transposed, k-major, still int8, so that every MFMA
-//     fragment is one 8-byte LDS read widened in registers; the epilogue scales rows by
-//     2^E[m], applies H to each 16-lane run of the row and rounds once to dx's dtype.
+//     workgroup per 128 rows x 256 columns of dx; the weight tile goes to LDS as stored (rows
+//     of n, k contiguous) and each MFMA fragment (8 consecutive n of one column) is one
+//     transposing 8-byte LDS read, widened in registers; the epilogue scales rows by 2^E[m],
+//     applies H to each 16-lane run of the row and rounds once to dx's dtype.
 #include "qlin_internal.h"
 #include "hadamard.h"
 
@@ -23,10 +23,12 @@ namespace {
 constexpr int BW_BM = 128, BW_BK = 256, BW_BN = 64;
 constexpr int BW_RING = 2;  // register sets: a stage's loads are issued two stages before its use
 constexpr int BW_LS = BW_BN + 8;  // a tile LDS row stride in halves: 80 bytes, conflict-free fragment reads
-// weight tile LDS row stride in bytes: 72 (18 dwords) puts the 32 lanes of every 8-byte write and
-// fragment read on distinct bank pairs
-constexpr int BW_LB = BW_BN + 8;
-constexpr int BW_BUF = BW_BM * BW_LS * 2 + BW_BK * BW_LB;  // bytes per pipeline buffer
+// weight tile in LDS as stored, [64 n][256 k] int8, row r's 16-byte chunk c at chunk c ^ 2 (r % 8):
+// the 16-byte writes of a row and the transposing fragment reads (8 rows x 2 chunk halves per
+// 16 lanes, even and odd chunks in the two groups of a 32-lane half) fall on distinct banks
+constexpr int BW_LB = BW_BK;
+constexpr int BW_BUF = BW_BM * BW_LS * 2 + BW_BN * BW_LB;  // bytes per pipeline buffer
+__device__ __forceinline__ int bw_chunk(int row, int c) { return c ^ (2 * (row & 7)); }
 constexpr int BW_OW = BW_BK + BW_BK / 4;  // epilogue row stride in floats: 4 pad floats per 16
 
 // a[m, :] = fp16(dy[m, :] * s * 2^-E[m]), zero past N up to lda; e[m] = E[m].  8 consecutive
@@ -114,23 +116,6 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(const T* __restrict__ dy,
     if (tid == 0) e[m] = E;
 }
 
-// 8 rows x 4 columns of int8 (one dword per row) -> per column, the 8 rows' bytes (two dwords).
-__device__ __forceinline__ void transpose8x4(const uint32_t* r, uint32_t (*col)[2]) {
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const uint32_t* q = r + 4 * g;
-        // 4 x 4 byte transpose: t0 = [q00 q10 q01 q11], t1 = [q02 q12 q03 q13], t2, t3 likewise for rows 2, 3
-        const uint32_t t0 = __builtin_amdgcn_perm(q[1], q[0], 0x05010400u);
-        const uint32_t t1 = __builtin_amdgcn_perm(q[1], q[0], 0x07030602u);
-        const uint32_t t2 = __builtin_amdgcn_perm(q[3], q[2], 0x05010400u);
-        const uint32_t t3 = __builtin_amdgcn_perm(q[3], q[2], 0x07030602u);
-        col[0][g] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-        col[1][g] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-        col[2][g] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-        col[3][g] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-    }
-}
-
 // 8 int8 (two dwords, in order) -> 8 exact fp16: bits 0x6400 | (q + 128) = 1152 + q, minus 1152.
 __device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t w0, uint32_t w1) {
     const f16x2 off = {(f16)-1152.0f, (f16)-1152.0f};
@@ -143,14 +128,16 @@ __device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t w0, uint32_t w1) {
 }
 
 struct BwdRegs {
-    u32x4 a[2];     // 16 halves of one row of the a tile
-    uint32_t b[8];  // 4 int8 of each of 8 weight rows
+    u32x4 a[2];  // 16 halves of one row of the a tile
+    u32x4 b[2];  // 16 int8 of each of two weight rows
 };
+
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 // dx tile: rows m0 .. m0 + 127, columns k0 .. k0 + 255.  8 waves: wave w owns rows 64 (w / 4) ..
 // + 63 and columns 64 (w % 4) .. + 63 of the tile (2 x 2 sub-tiles of 32 x 32).  Stage = 64 values
-// of n: a tile [128][64] fp16 and weight tile [64][256] int8, the latter stored in LDS transposed
-// as [256][64] int8 and widened to fp16 after each fragment read.  Two LDS buffers and two
+// of n: a tile [128][64] fp16 and weight tile [64][256] int8, the latter stored in LDS as read and
+// transposed by the fragment reads, then widened to fp16.  Two LDS buffers and two
 // register sets: each stage's global loads are issued two stages before it is computed (174
 // registers: one workgroup per CU).  Measured at M = 1056: a three-set ring, buffer loads with
 // scalar row offsets, and a 128-register cap (two workgroups per CU, with spills) were all slower.
@@ -163,29 +150,20 @@ __global__ __launch_bounds__(512, 2) void bwd_gemm_kernel(BwdGemmArgs p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, h = lane >> 5, wm = wave >> 2, wk = wave & 3;
     const int64_t m0 = (int64_t)blockIdx.y * BW_BM, k0 = (int64_t)blockIdx.x * BW_BK;
-    // global load assignment: a row tid / 4, 16 halves at 16 (tid % 4); weight rows
-    // 32 (wave / 4) + 8 no .. + 7 of the stage (no = lane % 4) and columns 4 kq .. 4 kq + 3
-    // (kq = 16 (wave % 4) + lane / 4)
+    // global load assignment: a row tid / 4, 16 halves at 16 (tid % 4); weight rows tid / 16 and
+    // 32 + tid / 16 of the stage, 16 bytes at column 16 (tid % 16) of the tile
     const f16* ap = p.a + min(m0 + tid / 4, p.M - 1) * p.lda + 16 * (tid & 3);
-    const int no = lane & 3, kq = 16 * wk + (lane >> 2), nh = 32 * wm + 8 * no;
-    const int8_t* bp = p.b + min(k0 + 4 * kq, p.K - 4);
-    const int8_t* bq = bp + (int64_t)nh * p.ldb;  // this lane's first weight row of a stage
-    const int nst = (int)(p.lda / BW_BN);  // a multiple of BW_RING: lda is N rounded up to 128, a is zero past N
+    const int brow = tid >> 4, bc = tid & 15;
+    const int8_t* bp = p.b + min(k0 + 16 * bc, p.K - 16);  // columns past K re-read (never stored)
+    const int nst = (int)(p.lda / BW_BN);  // lda is N rounded up to 128; a is zero past N
     auto load = [&](int s, BwdRegs& r) {
         const u32x4* pa = reinterpret_cast<const u32x4*>(ap + (int64_t)BW_BN * s);
         r.a[0] = pa[0];
         r.a[1] = pa[1];
-        if ((int64_t)BW_BN * (s + 1) <= p.N) {
-            // whole stage inside N (uniform): one base pointer, rows at constant multiples of ldb
-            const int8_t* b0 = bq + (int64_t)BW_BN * s * p.ldb;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) r.b[i] = *reinterpret_cast<const uint32_t*>(b0 + i * p.ldb);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int64_t n = min((int64_t)BW_BN * s + nh + i, p.N - 1);  // rows past N meet a = 0
-                r.b[i] = *reinterpret_cast<const uint32_t*>(bp + n * p.ldb);
-            }
+        for (int i = 0; i < 2; ++i) {
+            const int64_t n = min((int64_t)BW_BN * s + 32 * i + brow, p.N - 1);  // rows past N meet a = 0
+            r.b[i] = *reinterpret_cast<const u32x4*>(bp + n * p.ldb);
         }
     };
     auto store = [&](const BwdRegs& r, int buf) {
@@ -194,12 +172,15 @@ __global__ __launch_bounds__(512, 2) void bwd_gemm_kernel(BwdGemmArgs p) {
         f16* ad = As + (tid >> 2) * BW_LS + 16 * (tid & 3);
         *reinterpret_cast<u32x4*>(ad) = r.a[0];
         *reinterpret_cast<u32x4*>(ad + 8) = r.a[1];
-        uint32_t col[4][2];
-        transpose8x4(r.b, col);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            *reinterpret_cast<uint2*>(Bs + (4 * kq + c) * BW_LB + nh) = uint2{col[c][0], col[c][1]};
+        for (int i = 0; i < 2; ++i) {
+            const int row = 32 * i + brow;
+            *reinterpret_cast<u32x4*>(Bs + row * BW_LB + 16 * bw_chunk(row, bc)) = r.b[i];
+        }
     };
+    // transposing fragment reads: in each 16-lane group, lane i names row nb + i / 2 at column
+    // kc + 8 (i % 2) and receives column kc + i of rows nb .. nb + 7 (ds_read_b64_tr_b8)
+    const int gi = lane & 15, g = lane >> 4;
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -218,8 +199,10 @@ __global__ __launch_bounds__(512, 2) void bwd_gemm_kernel(BwdGemmArgs p) {
                 af[i] = *reinterpret_cast<const f16x8*>(As + (64 * wm + 32 * i + r32) * BW_LS + 16 * st + 8 * h);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const uint2 w = *reinterpret_cast<const uint2*>(Bs + (64 * wk + 32 * j + r32) * BW_LB + 16 * st + 8 * h);
-                bf[j] = i8x8_to_f16(w.x, w.y);
+                const int row = 16 * st + 8 * (g >> 1) + (gi >> 1), kc = 64 * wk + 32 * j + 16 * (g & 1);
+                const uint8_t* src = Bs + row * BW_LB + 16 * bw_chunk(row, kc >> 4) + 8 * (gi & 1);
+                const v2i w = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)src);
+                bf[j] = i8x8_to_f16((uint32_t)w.x, (uint32_t)w.y);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -317,8 +300,8 @@ hipError_t run_bwd_rows(const void* dy, int dy_dt, int64_t ldd, int64_t M, int64
 hipError_t run_bwd_gemm(const BwdGemmArgs& p, hipStream_t st) {
     if (p.M == 0 || p.K == 0) return hipSuccess;
     // the kernel's loads assume: K a multiple of 16 (4-byte weight loads from clamped columns),
-    // 4-byte aligned weight rows, lda a multiple of 128 covering N, N >= 1
-    if (p.K % 16 || p.ldb % 4 || (uintptr_t)p.b % 4 || p.lda % (BW_RING * BW_BN) || p.lda < p.N || p.N < 1 ||
+    // 16-byte aligned weight rows, lda a multiple of 128 covering N, N >= 1
+    if (p.K % 16 || p.ldb % 16 || (uintptr_t)p.b % 16 || p.lda % (BW_RING * BW_BN) || p.lda < p.N || p.N < 1 ||
         (uintptr_t)p.a % 16)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((p.K + BW_BK - 1) / BW_BK), (unsigned)((p.M + BW_BM - 1) / BW_BM));

@@ -277,7 +277,7 @@ qlin_status qlin_int8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor
     // dy [M, N] in, dx [M, K] out
     if ((s = check_xy(dy, dx, K, N, DY, DX))) return s;
     if ((s = grad_shapes(N, K, convrot_groupsize))) return s;
-    if (Q.ld % 4 || (uintptr_t)Q.data % 4) return fail(QLIN_EUNSUPPORTED, "qdata rows must be 4-byte aligned");
+    if (Q.ld % 16 || (uintptr_t)Q.data % 16) return fail(QLIN_EUNSUPPORTED, "qdata rows must be 16-byte aligned");
     int64_t sst;
     if ((s = as_vector(scale, "scale", N, true, sst))) return s;
     if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype %d unsupported", scale->dtype);
