@@ -138,9 +138,10 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 // + 63 and columns 64 (w % 4) .. + 63 of the tile (2 x 2 sub-tiles of 32 x 32).  Stage = 64 values
 // of n: a tile [128][64] fp16 and weight tile [64][256] int8, the latter stored in LDS as read and
 // transposed by the fragment reads, then widened to fp16.  Two LDS buffers and two
-// register sets: each stage's global loads are issued two stages before it is computed (174
-// registers: one workgroup per CU).  Measured at M = 1056: a three-set ring, buffer loads with
-// scalar row offsets, and a 128-register cap (two workgroups per CU, with spills) were all slower.
+// register sets: each stage's global loads are issued two stages before it is computed (one
+// workgroup per CU).  Measured at M = 1056: a three-set ring, buffer loads with scalar row
+// offsets, a 128-register cap (two workgroups per CU, with spills) and LDS DMA of both tiles in
+// three stages were all slower.
 // The tile size sets the operand bytes per MFMA: at 128 x 256 a 64-value stage brings 32 KB for
 // 4.2 MFLOP.
 template <int G>
