@@ -308,11 +308,26 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
 template <int S>
 __global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
     const float* __restrict__ part, int M, int N, const int32_t* __restrict__ xexp,
-    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy) {
-    const int nq = (N + 3) / 4;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (int64_t)M * nq) return;
-    const int m = (int)(t / nq), n = (int)(t % nq) * 4;
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy, int xcd_blocks) {
+    int m, n;
+    if (xcd_blocks) {
+        // The split kernel's workgroup (x, s) is dispatched to XCD (s * blocks + x) % 8 = x % 8 when
+        // the row-block count is a multiple of 8: every partial of row block x was written through
+        // that XCD's L2.  Workgroup b reduces only row blocks x = b % 8 (mod 8), 4 outputs a thread.
+        const int xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+        const int64_t per = (int64_t)(xcd_blocks / 8) * SP_ROWS * M;  // outputs of this XCD's row blocks
+        const int64_t idx = (int64_t)j * 1024 + 4 * threadIdx.x;
+        if (idx >= per) return;
+        const int q = (int)(idx / ((int64_t)SP_ROWS * M)), rem = (int)(idx % ((int64_t)SP_ROWS * M));
+        m = rem / SP_ROWS;
+        n = (xcd + 8 * q) * SP_ROWS + rem % SP_ROWS;
+    } else {
+        const int nq = (N + 3) / 4;
+        const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        if (t >= (int64_t)M * nq) return;
+        m = (int)(t / nq);
+        n = (int)(t % nq) * 4;
+    }
     const int64_t mn = (int64_t)M * N;
     const float* p = part + (int64_t)m * N + n;
     const int e = xexp ? xexp[m] : 0;
@@ -363,11 +378,15 @@ hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
 #undef QLIN_SP_LAUNCH
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || a.S == 1) return err;
+    // row blocks in multiples of 8 (N a multiple of 1024): reduce each block on the XCD that wrote it
+    const int blocks = (int)((a.N + SP_ROWS - 1) / SP_ROWS);
+    const int xcd_blocks = (a.N % SP_ROWS == 0 && blocks % 8 == 0) ? blocks : 0;
     const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
-    const dim3 rgrid((unsigned)((threads + 255) / 256));
+    const dim3 rgrid(xcd_blocks ? (unsigned)(8 * (((int64_t)(blocks / 8) * SP_ROWS * a.M + 1023) / 1024))
+                                : (unsigned)((threads + 255) / 256));
 #define QLIN_SP_REDUCE(SV)                                                                                    \
     hipLaunchKernelGGL(gguf_split_reduce_kernel<SV>, rgrid, dim3(256), 0, st, a.part, a.M, a.N, a.xexp, a.bias, \
-                       a.bias_dtype, a.y, a.y_dtype, a.ldy)
+                       a.bias_dtype, a.y, a.y_dtype, a.ldy, xcd_blocks)
     switch (a.S) {
         case 2: QLIN_SP_REDUCE(2); break;
         case 3: QLIN_SP_REDUCE(3); break;
