@@ -80,6 +80,49 @@ def test_malformed_calls_are_rejected_before_launch():
     assert b"codebook" in L.qlin_last_error()
 
 
+def test_gradient_and_lora_calls_are_rejected_before_launch():
+    from qlin import _lib
+    L = _lib.load()
+    dy = torch.zeros(4, 32, dtype=torch.float16)
+    dx = torch.zeros(4, 256, dtype=torch.float16)
+    q = torch.zeros(32, 256, dtype=torch.int8)
+    s = torch.ones(32)
+    big = 1 << 30
+    # dx of the wrong shape, an unsupported group, K not a multiple of 16, a short workspace
+    assert L.qlin_int8_linear_grad_input(_d(dy), _d(q), _d(s), 0, _d(dx[:, :255]), None, big, None) == _lib.QLIN_EINVAL
+    assert L.qlin_int8_linear_grad_input(_d(dy), _d(q), _d(s), 100, _d(dx), None, big, None) == _lib.QLIN_EUNSUPPORTED
+    q8 = torch.zeros(32, 248, dtype=torch.int8)
+    dx8 = torch.zeros(4, 248, dtype=torch.float16)
+    assert L.qlin_int8_linear_grad_input(_d(dy), _d(q8), _d(s), 0, _d(dx8), None, big, None) == _lib.QLIN_EUNSUPPORTED
+    assert L.qlin_int8_linear_grad_input(_d(dy), _d(q), _d(s), 0, _d(dx), None, 0, None) == _lib.QLIN_EWORKSPACE
+    need = L.qlin_workspace_size(_lib.OP_INT8_GRAD_INPUT, 4, 32, 256, 0, _lib.DT_F16)
+    assert need >= 4 * 128 * 2 + 4 * 4  # dy rows padded to 128 values, plus exponents
+    assert L.qlin_workspace_size(_lib.OP_W4A8_GRAD_INPUT, 4, 32, 256, 4, _lib.DT_F16) >= need + 32 * 256
+    # W4A8 gradient: 5 bits, s_rel of the wrong shape
+    qq = torch.zeros(32, 128, dtype=torch.int8)
+    sr = torch.ones(32, 16)
+    assert L.qlin_w4a8_linear_grad_input(_d(dy), _d(qq), _d(sr), _d(s), None, _d(dx), 5, 16, 256, None, big, None) == 1
+    assert L.qlin_w4a8_linear_grad_input(_d(dy), _d(qq), _d(sr[:, :8]), _d(s), None, _d(dx), 4, 16, 256, None, big,
+                                         None) == _lib.QLIN_EINVAL
+    # LoRA: factors that do not fit x and y, a short workspace
+    x = torch.zeros(4, 256, dtype=torch.float16)
+    y = torch.zeros(4, 32, dtype=torch.float16)
+    down, up = torch.zeros(8, 256, dtype=torch.float16), torch.zeros(32, 8, dtype=torch.float16)
+    assert L.qlin_lora_apply(_d(x), _d(down[:, :128]), _d(up), 1.0, _d(y), None, big, None) == _lib.QLIN_EINVAL
+    assert L.qlin_lora_apply(_d(x), _d(down), _d(up[:, :4]), 1.0, _d(y), None, big, None) == _lib.QLIN_EINVAL
+    assert L.qlin_lora_apply(_d(x), _d(down), _d(up), 1.0, _d(y), None, 0, None) == _lib.QLIN_EWORKSPACE
+
+
+def test_gradient_ops_decline_on_the_host():
+    import qlin
+    dy = torch.zeros(2, 8, dtype=torch.float16)
+    with pytest.raises(qlin.NoCapableBackendError):
+        qlin.int8_linear_grad_input(dy, torch.zeros(8, 256, dtype=torch.int8), torch.ones(8), True, 256)
+    with pytest.raises(qlin.NoCapableBackendError):  # the asymmetric variant, before any device check
+        qlin.w4a8_linear_trainable(torch.zeros(2, 256), torch.zeros(8, 128, dtype=torch.int8), torch.ones(8, 16),
+                                   torch.ones(8), None, torch.zeros(16, 8), None, 16, 256)
+
+
 def test_ops_decline_cpu_tensors():
     import qlin
     x = torch.zeros(2, 256, dtype=torch.float16)
