@@ -113,6 +113,26 @@ def test_gguf_lora(name, m):
     check_full(y, O.linear_ref(x.float().numpy(), wdq) + ref, f"{name} full")
 
 
+@pytest.mark.parametrize("odt", [torch.float32, torch.float16])
+def test_lora_fp32_activations(odt):
+    """fp32 x and the fp32 output path of the up kernel (no y prefetch), odd N and M."""
+    Q = qlin()
+    n, k, g, m = 200, 512, 256, 45
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(8)) * 0.02).numpy()
+    qn, sn = qz().quantize_int8_convrot_weight(w, g)
+    q, s = torch.from_numpy(qn).to(DEV), torch.from_numpy(sn).reshape(-1).to(DEV)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(9))
+    down, up = factors(n, k, 24, torch.float32, torch.float32, seed=10)
+    base = Q.int8_linear(x.to(DEV), q, s, None, odt, convrot=True, convrot_groupsize=g)
+    y = Q.int8_linear(x.to(DEV), q, s, None, odt, convrot=True, convrot_groupsize=g,
+                      lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.7)
+    assert y.dtype == odt
+    ref = side_ref(x, down, up, 0.7)
+    check_side(y, base, ref, f"fp32 x, {odt} out")
+    wdq = O.dequantize_int8_convrot(qn, sn, g)
+    check_full(y, O.linear_ref(x.numpy(), wdq) + ref, "fp32 full")
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("large_down", [False, True])
 def test_lora_large_factors_exact(xdt, large_down):
