@@ -138,14 +138,14 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 // + 63 and columns 64 (w % 4) .. + 63 of the tile (2 x 2 sub-tiles of 32 x 32).  Stage = 64 values
 // of n: a tile [128][64] fp16 and weight tile [64][256] int8, the latter stored in LDS as read and
 // transposed by the fragment reads, then widened to fp16.  Two LDS buffers and two
-// register sets: each stage's global loads are issued two stages before it is computed (one
-// workgroup per CU).  Measured at M = 1056: a three-set ring, buffer loads with scalar row
-// offsets, a 128-register cap (two workgroups per CU, with spills) and LDS DMA of both tiles in
-// three stages were all slower.
+// register sets: each stage's global loads are issued two stages before it is computed.  WPE = 4
+// caps the registers at 128 so that two workgroups share a CU (grids beyond one round).  Measured
+// at M = 1056: a three-set ring, buffer loads with scalar row offsets and LDS DMA of both tiles in
+// three stages were slower.
 // The tile size sets the operand bytes per MFMA: at 128 x 256 a 64-value stage brings 32 KB for
 // 4.2 MFLOP.
-template <int G>
-__global__ __launch_bounds__(512, 2) void bwd_gemm_kernel(BwdGemmArgs p) {
+template <int G, int WPE>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void bwd_gemm_kernel(BwdGemmArgs p) {
     constexpr int SMEM = 2 * BW_BUF > 32 * BW_OW * 4 ? 2 * BW_BUF : 32 * BW_OW * 4;
     __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -307,8 +307,13 @@ hipError_t run_bwd_gemm(const BwdGemmArgs& p, hipStream_t st) {
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((p.K + BW_BK - 1) / BW_BK), (unsigned)((p.M + BW_BM - 1) / BW_BM));
     bool ok = false;
+    // grids of more than one workgroup per CU: 128 registers (4 waves per SIMD, a few spilled), two
+    // workgroups per CU (mlp.down-sized grids: 300 against 319 us); one round: the unconstrained
+    // kernel (148 against 154 us)
+    const bool two = (int64_t)grid.x * grid.y > 256;
     auto go = [&]<int G>() {
-        hipLaunchKernelGGL((bwd_gemm_kernel<G>), grid, dim3(512), 0, st, p);
+        if (two) hipLaunchKernelGGL((bwd_gemm_kernel<G, 4>), grid, dim3(512), 0, st, p);
+        else hipLaunchKernelGGL((bwd_gemm_kernel<G, 1>), grid, dim3(512), 0, st, p);
         ok = true;
     };
     if (!dispatch_group(p.G, go) || !ok) return hipErrorInvalidValue;

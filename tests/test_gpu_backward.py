@@ -49,6 +49,7 @@ INT8_CASES = [
     (130, 1024, 768, 0, torch.bfloat16, torch.float16, "f32", 2e-5),
     (300, 96, 1024, 256, torch.float16, torch.bfloat16, "f32", 1.0),
     (65, 33, 272, 16, torch.float16, torch.float32, "f32", 3.0),
+    (1100, 256, 8192, 256, torch.bfloat16, None, "f32", 1.0),  # 288 workgroups: the two-per-CU kernel
 ]
 
 
