@@ -313,14 +313,6 @@ __device__ __forceinline__ void xcd_tile(int b, int nblocks, int n_m, int n_n, i
 // 512 threads = 8 waves, 4 (M) x 2 (N) of 64 x 128; tile 256 x 256 x 128 (int8).
 constexpr int BKA = 128, LDAA = BKA + 16;  // k-tile and LDS row stride (bytes)
 
-// Workgroup barrier that orders LDS only (a plain __syncthreads also waits for every global load
-// in flight).  LDS DMA writes are covered by an explicit wait_vmcnt before it.
-__device__ __forceinline__ void lds_barrier_i8() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <int BITS, bool CB, typename TSrel, bool PAIR>
 __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
     constexpr int BMT = 256, BNT = 256, NT = 512;
@@ -464,7 +456,7 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
         stage_b(1, R1);
         interleave();
         wait_vmcnt<NB>();
-        lds_barrier_i8();
+        lds_barrier();
         if (kt + 1 < ktiles) {  // uniform
             fetch_a(kt + 2, 0);
             __builtin_amdgcn_sched_barrier(0);
@@ -474,7 +466,7 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
             stage_b(0, R0);
             interleave();
             wait_vmcnt<NB>();
-            lds_barrier_i8();
+            lds_barrier();
         }
     }
 

@@ -32,13 +32,6 @@ constexpr int SP_ROWS = 16 * SP_WAVES;  // weight rows per workgroup
 constexpr int SP_TARGET_BLOCKS = 256;   // one workgroup per CU
 constexpr int SP_MAX_SPLITS = 8;        // partial tiles added by the reduction kernel
 
-// Barrier for LDS only: waits for this wave's LDS operations, not for its global loads in flight.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <int T, int MT>
 __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,

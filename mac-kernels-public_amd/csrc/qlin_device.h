@@ -248,4 +248,13 @@ __device__ __forceinline__ float load_f(const float* p) { return *p; }
 __device__ __forceinline__ float load_f(const f16* p) { return (float)*p; }
 __device__ __forceinline__ float load_f(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS operations, not for its global
+// loads in flight (a plain __syncthreads also waits for every global load).  Data that reaches LDS
+// through global loads (LDS DMA) needs its own vmcnt wait first.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace qlin
