@@ -133,6 +133,10 @@ def test_gguf_linear(name, m):
     ("Q8_0", 20, 12800, 1280),  # 100 row tiles: three splits over five stages (uneven)
     ("Q3_K", 64, 200, 2048),    # two-block stages, sub-block minimum MFMA
     ("IQ4_XS", 47, 256, 4096),
+    # N a multiple of 1024: each row block's partials are added by workgroups of the XCD that wrote them
+    ("Q4_K", 64, 1024, 2048),   # 8 row blocks, 8 splits
+    ("Q6_K", 24, 2048, 1024),   # 16 row blocks, 4 splits
+    ("Q8_0", 40, 3072, 512),    # 24 row blocks, 2 splits
 ])
 def test_gguf_linear_split_k(name, m, n, k):
     """The K-split kernel (M = 17..64): ragged N, uneven and single splits, bias."""
