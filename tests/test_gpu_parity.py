@@ -149,6 +149,23 @@ def test_gguf_linear_split_k(name, m, n, k):
     check_linear(got, want, f"{name} M={m} N={n} K={k}")
 
 
+# One activation row with K / (values per lane chunk) in {16, 32, 64}: the GEMV kernel for every
+# format it covers (at K = 1024 most formats take the small-M kernel instead); K = 4096 is the
+# decode shape.
+@pytest.mark.parametrize("name", GGUF)
+@pytest.mark.parametrize("k", [2048, 4096, 8192])
+def test_gguf_linear_gemv(name, k):
+    n = 72
+    raw = qz().random_gguf_blocks(name, n, k, seed=31)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = x_fp16(1, k, seed=k)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(6)) * 0.1).half()
+    want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), bias=b.to(DEV))
+    assert got.shape == (1, n)
+    check_linear(got, want, f"{name} M=1 K={k}")
+
+
 @pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                      (torch.float32, torch.float32), (torch.float16, torch.float32)])
 @pytest.mark.parametrize("m", [3, 40, 200])
