@@ -149,21 +149,21 @@ def test_gguf_linear_split_k(name, m, n, k):
     check_linear(got, want, f"{name} M={m} N={n} K={k}")
 
 
-# One activation row with K / (values per lane chunk) in {16, 32, 64}: the GEMV kernel for every
-# format it covers (at K = 1024 most formats take the small-M kernel instead); K = 4096 is the
-# decode shape.
+# Long rows.  One activation row with K / (values per lane chunk) in {16, 32, 64} takes the GEMV
+# kernel for every format it covers (at K = 1024 most formats take the small-M kernel instead);
+# K = 4096 is the decode shape.  M = 8 and 16 take the small-M kernel (Q6_K: the K split).
 @pytest.mark.parametrize("name", GGUF)
-@pytest.mark.parametrize("k", [2048, 4096, 8192])
-def test_gguf_linear_gemv(name, k):
+@pytest.mark.parametrize("m,k", [(1, 2048), (1, 4096), (1, 8192), (8, 4096), (16, 8192)])
+def test_gguf_linear_long_k(name, m, k):
     n = 72
     raw = qz().random_gguf_blocks(name, n, k, seed=31)
     w = O.gguf_dequantize(raw, name, (n, k))
-    x = x_fp16(1, k, seed=k)
+    x = x_fp16(m, k, seed=k + m)
     b = (torch.randn(n, generator=torch.Generator().manual_seed(6)) * 0.1).half()
     want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
     got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), bias=b.to(DEV))
-    assert got.shape == (1, n)
-    check_linear(got, want, f"{name} M=1 K={k}")
+    assert got.shape == (m, n)
+    check_linear(got, want, f"{name} M={m} K={k}")
 
 
 @pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
