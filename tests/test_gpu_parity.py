@@ -166,6 +166,20 @@ def test_gguf_linear_long_k(name, m, k):
     check_linear(got, want, f"{name} M={m} K={k}")
 
 
+@pytest.mark.parametrize("name", ["Q4_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS"])
+def test_gguf_linear_decode_workload(name):
+    """The benchmarked calls themselves: K = N = 4096 at M = 1, 8 and 64 (GEMV, small-M or K split,
+    and the K split with its XCD-local reduction, S = 8)."""
+    n = k = 4096
+    raw = qz().random_gguf_blocks(name, n, k, seed=41)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    wd = torch.from_numpy(raw).to(DEV)
+    for m in (1, 8, 64):
+        x = x_fp16(m, k, seed=m + 40)
+        got = qlin().gguf_linear(x.to(DEV), wd, name, (n, k))
+        check_linear(got, O.linear_ref(x.float().numpy(), w), f"{name} M={m} K=N=4096")
+
+
 @pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                      (torch.float32, torch.float32), (torch.float16, torch.float32)])
 @pytest.mark.parametrize("m", [3, 40, 200])
