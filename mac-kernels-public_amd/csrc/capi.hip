@@ -609,24 +609,34 @@ qlin_status qlin_dequantize_w4a8(const qlin_tensor* qdata, const qlin_tensor* s_
     Mat Q, SR, O;
     qlin_status s = as_matrix(qdata, "qdata", Q);
     if (s) return s;
+    if (Q.dtype != QLIN_DT_I8 && Q.dtype != QLIN_DT_U8) return fail(QLIN_EUNSUPPORTED, "qdata must be int8/uint8");
+    if ((Q.cols * 8) % bits) return fail(QLIN_EINVAL, "qdata columns do not hold whole codes");
     const int64_t N = Q.rows, K = Q.cols * 8 / bits;
     if (group_size <= 0 || K % group_size) return fail(QLIN_EINVAL, "group_size does not divide K");
     if ((s = as_matrix(s_rel, "s_rel", SR))) return s;
     if (SR.rows != N || SR.cols != K / group_size) return fail(QLIN_EINVAL, "s_rel shape mismatch");
+    if (SR.dtype != QLIN_DT_E4M3 && SR.dtype != QLIN_DT_F16 && SR.dtype != QLIN_DT_BF16 && SR.dtype != QLIN_DT_F32 &&
+        SR.dtype != QLIN_DT_U8)
+        return fail(QLIN_EUNSUPPORTED, "s_rel dtype %d unsupported", SR.dtype);
     if ((s = as_matrix(out, "out", O))) return s;
     if (O.rows != N || O.cols != K || O.ld != K) return fail(QLIN_EINVAL, "out must be a contiguous [N, K]");
     if (O.dtype != QLIN_DT_I8 && O.dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "out must be int8 or float32");
     if (O.dtype == QLIN_DT_I8 && convrot_groupsize) return fail(QLIN_EINVAL, "the int8 grid has no original-basis form");
     int64_t sst;
     if ((s = as_vector(s_channel, "s_channel", N, false, sst))) return s;
+    if (s_channel->dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "s_channel must be float32");
     const float* cb = nullptr;
     if (codebook && codebook->data) {
+        // 6-bit codes reach 63: a 16-entry table is only defined for 4-bit codes
+        if (bits != 4) return fail(QLIN_EUNSUPPORTED, "a codebook is only defined for 4-bit codes");
         int64_t cst;
         if ((s = as_vector(codebook, "codebook", 16, false, cst))) return s;
+        if (codebook->dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "codebook must be float32");
         cb = (const float*)codebook->data;
     }
     if (!valid_group(convrot_groupsize) || (convrot_groupsize && K % convrot_groupsize))
         return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
+    if (N == 0 || K == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     const int srdt = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype;
     if ((s = hip_status(run_dequant_w4a8((const uint8_t*)Q.data, N, K, Q.ld, bits, group_size, SR.data, srdt, SR.ld,

@@ -314,10 +314,24 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
 def dequantize_gguf(weight, qtype, shape, out_dtype=torch.float32):
     """Decode GGUF block bytes to a dense [N, K] tensor; float32 is bit-exact with gguf-py."""
     op = "dequantize_gguf"
-    _check_device(op, weight)
     tid = gguf_type_id(qtype)
     n, k = int(shape[0]), int(shape[1])
+    _, qk, ts = GGUF_TYPES_BY_ID[tid]
+    # the kernel decodes N*K/qk whole blocks from a raw pointer: check the buffer before any launch
+    if weight.dtype != torch.uint8:
+        raise NoCapableBackendError(op, {"hip": "weight must be the uint8 block bytes"})
+    if not weight.is_contiguous():
+        raise NoCapableBackendError(op, {"hip": "weight bytes must be contiguous"})
+    if n < 0 or k < 0 or (n * k) % qk:
+        raise ValueError(f"{op}: shape {tuple(shape)} is not a whole number of {qk}-value blocks")
+    if weight.numel() != n * k // qk * ts:
+        raise ValueError(f"weight has {weight.numel()} bytes, expected {n * k // qk * ts} for {tuple(shape)}")
+    if out_dtype not in _FLOAT:
+        raise NoCapableBackendError(op, {"hip": f"out_dtype {out_dtype} unsupported"})
+    _check_device(op, weight)
     out = torch.empty((n, k), dtype=out_dtype, device=weight.device)
+    if out.numel() == 0:
+        return out
     st = _lib.load().qlin_dequantize_gguf(weight.data_ptr(), tid, n, k, _lib.desc(out), _lib.stream_of(weight.device))
     _lib.check(st, op)
     return out

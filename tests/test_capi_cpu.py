@@ -113,6 +113,50 @@ def test_gradient_and_lora_calls_are_rejected_before_launch():
     assert L.qlin_lora_apply(_d(x), _d(down), _d(up), 1.0, _d(y), None, 0, None) == _lib.QLIN_EWORKSPACE
 
 
+def test_decode_calls_are_rejected_before_launch():
+    """The standalone decodes check their operands like the linears do."""
+    from qlin import _lib
+    L = _lib.load()
+    n, k = 32, 256
+    s = torch.ones(n)
+    q4 = torch.zeros(n, k // 2, dtype=torch.int8)
+    q6 = torch.zeros(n, k * 3 // 4, dtype=torch.int8)
+    sr = torch.ones(n, k // 16)
+    out = torch.zeros(n, k)
+    cb = torch.zeros(16)
+    # a codebook with 6-bit codes (codes reach 63, the table has 16 entries)
+    assert L.qlin_dequantize_w4a8(_d(q6), _d(sr), _d(s), _d(cb), _d(out), 6, 16, 0, None) == _lib.QLIN_EUNSUPPORTED
+    assert b"codebook" in L.qlin_last_error()
+    # a codebook that is not float32
+    assert L.qlin_dequantize_w4a8(_d(q4), _d(sr), _d(s), _d(cb.half()), _d(out), 4, 16, 0, None) == \
+        _lib.QLIN_EUNSUPPORTED
+    # qdata of the wrong dtype, columns that do not hold whole 6-bit codes, s_channel not float32
+    assert L.qlin_dequantize_w4a8(_d(q4.float()), _d(sr), _d(s), None, _d(out), 4, 16, 0, None) == \
+        _lib.QLIN_EUNSUPPORTED
+    q6bad = torch.zeros(n, 191, dtype=torch.int8)
+    assert L.qlin_dequantize_w4a8(_d(q6bad), _d(sr), _d(s), None, _d(out), 6, 16, 0, None) == _lib.QLIN_EINVAL
+    assert L.qlin_dequantize_w4a8(_d(q4), _d(sr), _d(s.half()), None, _d(out), 4, 16, 0, None) == \
+        _lib.QLIN_EUNSUPPORTED
+
+
+def test_dequantize_gguf_checks_the_buffer_on_the_host():
+    """A short, strided or mistyped weight buffer raises before anything is launched."""
+    import qlin
+    raw = torch.zeros(8 * 144, dtype=torch.uint8)          # 8 Q4_K blocks: 8 rows of 256 values
+    with pytest.raises(ValueError):
+        qlin.dequantize_gguf(raw[:-1], "Q4_K", (8, 256))     # one byte short
+    with pytest.raises(ValueError):
+        qlin.dequantize_gguf(raw, "Q4_K", (8, 512))          # shape needs twice the bytes
+    with pytest.raises(ValueError):
+        qlin.dequantize_gguf(raw, "Q4_K", (3, 100))          # not a whole number of blocks
+    with pytest.raises(qlin.NoCapableBackendError):
+        qlin.dequantize_gguf(raw.view(torch.int8), "Q4_K", (8, 256))
+    with pytest.raises(qlin.NoCapableBackendError):
+        qlin.dequantize_gguf(torch.zeros(8, 288, dtype=torch.uint8)[:, ::2], "Q4_K", (8, 256))
+    with pytest.raises(qlin.NoCapableBackendError):         # well-formed, but on the host
+        qlin.dequantize_gguf(raw, "Q4_K", (8, 256))
+
+
 def test_gradient_ops_decline_on_the_host():
     import qlin
     dy = torch.zeros(2, 8, dtype=torch.float16)
