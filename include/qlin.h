@@ -115,6 +115,21 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
                              const qlin_tensor* bias, qlin_tensor* y,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* Bytes of the fixed per-GPU scratch behind qlin_gguf_linear_noalloc. */
+#define QLIN_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* qlin_gguf_linear without a workspace argument and without allocating: the same kernels, with
+ * their workspace (normalized activations, row exponents, K-split partials) in a fixed
+ * QLIN_NOALLOC_SCRATCH_BYTES array per GPU, held until the process ends.  For callers that cannot
+ * call hipMalloc or take a caller-sized buffer: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  A call whose workspace (qlin_workspace_size(QLIN_OP_GGUF_LINEAR,
+ * ...)) exceeds the scratch returns QLIN_EWORKSPACE before launching anything (every M <= 64 at
+ * N, K <= 8192 fits).  Nothing in the scratch needs to start at zero.  All calls on one GPU share
+ * its scratch: calls that overlap in time on that GPU (concurrent streams, or threads) race.
+ * No counterpart in the reference; otherwise identical to qlin_gguf_linear (results bit-identical). */
+qlin_status qlin_gguf_linear_noalloc(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N,
+                                     int64_t K, const qlin_tensor* bias, qlin_tensor* y, void* stream);
+
 /* Unmerged LoRA on a finished linear output: y[m,n] = dtype(y[m,n] + lora_scale * sum_r t[m,r] *
  * lora_up[n,r]) with t = x @ lora_down^T kept in fp32 in the workspace (up to 8 K-split partials of
  * M*R*4 bytes and their sum: qlin_workspace_size(QLIN_OP_LORA, M, N, K, R, x_dtype)).  x is the caller's activation (before

@@ -3,6 +3,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "qlin.h"
@@ -12,7 +13,21 @@
 
 using namespace qlin;
 
+// Workspace of qlin_gguf_linear_noalloc: one copy per GPU, loaded with the code object and held
+// until the process ends.  Host code never passes `scratch` itself to a kernel or a copy (on the
+// host it names a shadow variable, not device memory); it uses the device address that
+// hipGetSymbolAddress returns for the current device (scratch_for_stream below).
+static __device__ __align__(256) uint8_t scratch[QLIN_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the GPU that runs `stream` (the current device for the null
+// stream), looked up once per device with that device current.
+qlin_status scratch_for_stream(hipStream_t stream, void*& ptr);
 
 thread_local std::string g_err;
 
@@ -179,6 +194,27 @@ qlin_status wo_activations(const Mat& X, int G, Carver& ws, hipStream_t st, cons
     ldx = X.cols;
     eo = p.eo;
     return hip_status(run_prologue(p, st), "prologue");
+}
+
+qlin_status scratch_for_stream(hipStream_t stream, void*& ptr) {
+    int cur = 0, dev = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    dev = cur;
+    if (stream && (e = hipStreamGetDevice(stream, &dev)) != hipSuccess) return hip_status(e, "hipStreamGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(QLIN_EUNSUPPORTED, "device %d is beyond the %d supported", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return hip_status(e, "hipSetDevice");
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(QLIN_EHIP, "hipGetSymbolAddress(scratch) returned no address");
+        g_scratch_ptr[dev] = p;
+    }
+    ptr = g_scratch_ptr[dev];
+    return QLIN_OK;
 }
 
 }  // namespace
@@ -412,10 +448,10 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     return hip_status(run_gemm_f16(a, st), "int8 gemm");
 }
 
-// Largest M of the small-M GGUF kernel (the single-row VALU kernel takes M = 1 when it applies)
-qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
-                             const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+// The GGUF linear over a given workspace (the caller's, or the no-allocation entry point's scratch).
+static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                                    const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
     int qk, ts;
     if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
     if (!weight) return fail(QLIN_EINVAL, "weight is missing");
@@ -487,6 +523,31 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
     a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
     a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
     return hip_status(run_gemm_f16(a, st), "gguf gemm");
+}
+
+qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                             const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+    return gguf_linear_impl(x, weight, ggml_type, N, K, bias, y, workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_gguf_linear_noalloc(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                                     const qlin_tensor* bias, qlin_tensor* y, void* stream) {
+    int qk, ts;
+    if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
+    Mat X;
+    qlin_status s = as_matrix(x, "x", X);
+    if (s) return s;
+    if (N < 0 || K < 0) return fail(QLIN_EINVAL, "negative shape");
+    const size_t need = ws_gguf(X.rows, N, K, ggml_type);
+    if (need > QLIN_NOALLOC_SCRATCH_BYTES)
+        return fail(QLIN_EWORKSPACE,
+                    "qlin_gguf_linear_noalloc: this call needs %zu bytes of scratch, more than its fixed %zu; "
+                    "use qlin_gguf_linear with a workspace",
+                    need, (size_t)QLIN_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if ((s = scratch_for_stream((hipStream_t)stream, ws))) return s;
+    return gguf_linear_impl(x, weight, ggml_type, N, K, bias, y, ws, QLIN_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,

@@ -27,7 +27,7 @@ _TORCH_DT = {
 # Every symbol include/qlin.h declares.
 EXPORTS = (
     "qlin_version", "qlin_status_string", "qlin_last_error", "qlin_workspace_size", "qlin_query",
-    "qlin_int8_linear", "qlin_w4a8_linear", "qlin_gguf_linear", "qlin_dequantize_gguf",
+    "qlin_int8_linear", "qlin_w4a8_linear", "qlin_gguf_linear", "qlin_gguf_linear_noalloc", "qlin_dequantize_gguf",
     "qlin_dequantize_int8", "qlin_dequantize_w4a8", "qlin_quantize_act_int8", "qlin_lora_apply",
     "qlin_int8_linear_grad_input", "qlin_w4a8_linear_grad_input",
 )
@@ -66,6 +66,7 @@ def load():
         "qlin_int8_linear": (I, [T, T, T, T, T, I, P, SZ, P]),
         "qlin_w4a8_linear": (I, [T, T, T, T, T, T, T, I, I, I, P, SZ, P]),
         "qlin_gguf_linear": (I, [T, P, I, I64, I64, T, T, P, SZ, P]),
+        "qlin_gguf_linear_noalloc": (I, [T, P, I, I64, I64, T, T, P]),
         "qlin_dequantize_gguf": (I, [P, I, I64, I64, T, P]),
         "qlin_dequantize_int8": (I, [T, T, T, I, P]),
         "qlin_dequantize_w4a8": (I, [T, T, T, T, T, I, I, I, P]),
