@@ -1,23 +1,33 @@
 """Quantized-linear benchmark on one MI355X.
 
-Default workload (one JSON line on stdout): GGUF block-decode linear, K = N = 4096, M in {1, 8, 64},
-one call per (type, M) for Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS -- 21 linear calls per step.
-Weights are N(0, 0.02) quantized with the standard GGUF block layouts, activations fp16 N(0, 1),
-everything resident in HBM before the timed region.  Each step reads a different copy of every
-weight from a pool of >= 1 GiB (4x the 256 MiB Infinity Cache) so the bytes come from HBM.  The
-steps are captured once in a HIP graph and replayed, so launch overhead from Python is not timed.
+One JSON line on stdout.  Its headline (`value`) is the GGUF block-decode linear, K = N = 4096,
+M in {1, 8, 64}, one call per (type, M) for Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS -- 21
+linear calls per step.  Weights are N(0, 0.02) quantized with the standard GGUF block layouts,
+activations fp16 N(0, 1), everything resident in HBM before the timed region.  Each step reads a
+different copy of every weight from a pool of >= 1 GiB (4x the 256 MiB Infinity Cache) so the
+bytes come from HBM.  The steps are captured once in a HIP graph and replayed, so launch
+overhead from Python is not timed.
 
 value = whole-step algorithmic bytes (packed weights + fp16 x + fp16 y) / step time, in GB/s.
-roofline: the kernel with the largest share of the step (by time), its algorithmic bytes per launch over
-its average launch duration (HIP events around graph replays of that call alone), against the 8 TB/s
-HBM peak; `traffic` is its measured HBM bytes per launch from the committed counter summary.
-cpu_baseline: the oracle's dequantize-then-matmul on the host (C decode, fp32 BLAS matmul).
+roofline: the kernel path with the largest share of the step (by time), its algorithmic bytes per
+call over its average call duration (HIP events around graph replays of that call alone, on the
+replay stream), against the 8 TB/s HBM peak; `traffic` is its measured HBM bytes per call from the
+committed counter summary.
+cpu_baseline: the oracle's dequantize-then-matmul on the host (C decode on all host threads,
+fp32 torch matmul on all host threads), median of 5 after 2 warm-ups.
 
-Other suites (--suite int8|w4a8|w6a8|dit|lora|grad|all) print their own JSON lines to stderr.
+`configs` holds the other workloads at their real shapes, each with its own throughput, roofline
+and CPU baseline: INT8-ConvRot M256 K=N=3072; W4A8 M4096 K3072 N12288; W6A8 M in {1024, 9504} for
+5120 -> 13824 and 13824 -> 5120; and one INT8-ConvRot DiT block layer (4 linears at 4608 tokens),
+reported per layer and x60 beside torch's fp16 F.linear on resident fp16 weights.
+
+Other suites (--suite lora|grad) print their own JSON lines to stderr.
 """
 import argparse
+import concurrent.futures as cf
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -30,10 +40,31 @@ INT8_PEAK_TOPS = 5000.0
 METRIC = "quantized-linear TFLOP/s + HBM GB/s (% of MI355X roofline), M=1..4096"
 GGUF_SUITE = ("Q4_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "IQ4_NL", "IQ4_XS")
 POOL_BYTES = 1 << 30
+DIT_LAYERS = 60
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def host_threads():
+    """Host threads for the CPU baseline: every CPU this process may use, capped by
+    OMP_NUM_THREADS when it is set (the share of a shared host)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
 
 
 def gguf_bytes(name, n, k):
@@ -64,8 +95,9 @@ def make_gguf_weights(name, n, k, copies, seed=0, raw=None):
     return out
 
 
-def time_graph(fn_step, steps, warmup, stream=None):
-    """Capture `fn_step` once into a HIP graph, replay warmup + steps times, return ms per replay."""
+def time_graph(fn_step, steps, warmup):
+    """Capture `fn_step` once into a HIP graph, replay warmup + steps times, return ms per replay.
+    The events are recorded on the stream the replays run on."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -90,6 +122,54 @@ def time_graph(fn_step, steps, warmup, stream=None):
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps, g
 
+
+def time_eager(fn, calls=200, warmup=20):
+    """Microseconds per call issued eagerly from Python (descriptors, workspace and launch on every
+    call), back to back on the current stream: when the host is slower than the kernels this is the
+    host's time per call."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(calls):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / calls * 1e3
+
+
+def median_ms(fn, reps=5, warm=2):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts) * 1e3
+
+
+class HostPool:
+    """Row-parallel CPU decode: the oracle's C routines run in threads (ctypes releases the GIL)."""
+
+    def __init__(self, threads):
+        self.threads = threads
+        self.ex = cf.ThreadPoolExecutor(threads)
+
+    def rows(self, fn, n):
+        """fn(r0, r1) -> array of rows r0..r1; returns their concatenation."""
+        import numpy as np
+        step = -(-n // self.threads)
+        spans = [(r, min(n, r + step)) for r in range(0, n, step)]
+        return np.concatenate(list(self.ex.map(lambda sp: fn(*sp), spans)))
+
+
+# ------------------------------------------------------------------------------------------------
+# GGUF decode-linear (the headline)
+# ------------------------------------------------------------------------------------------------
 
 def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
     import torch
@@ -137,55 +217,49 @@ def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
             detail[f"{t}/M{m}"] = {"us": round(us, 2), "bytes": b, "GBps": round(b / (us * 1e-6) / 1e9, 1),
                                    "TFLOPs": round(2 * m * n * k / (us * 1e-6) / 1e12, 2)}
             log(f"[gguf] {t:7s} M={m:3d}: {us:7.2f} us  {detail[f'{t}/M{m}']['GBps']:8.1f} GB/s")
+        if t == "Q4_K":  # eager calls from Python, beside the graph figure
+            for m in ms:
+                us = time_eager(lambda m=m: qlin.gguf_linear(xs[m], ws[0], tid[t], (n, k)))
+                detail[f"{t}/M{m}"]["eager_us"] = round(us, 2)
+                log(f"[gguf] {t:7s} M={m:3d}: eager {us:7.2f} us per call")
+        del ws
     return {
         "ms_per_step": ms_step, "value": gbs, "alg_bytes": alg_bytes, "flops": flops,
-        "launches": len(GGUF_SUITE) * len(ms), "detail": detail, "copies": copies,
+        "launches": len(GGUF_SUITE) * len(ms), "detail": detail, "copies": copies, "bases": bases,
     }
 
 
-def cpu_baseline_gguf(n=4096, k=4096, ms=(1, 8, 64), rows=None):
-    """Oracle decode (C, one thread) + fp32 matmul (torch, all host threads) for the same 21 calls.
-    `rows`: decode only that many weight rows per call (bounded sample), scaled up to N."""
-    import numpy as np
+def cpu_baseline_gguf(pool, bases, n=4096, k=4096, ms=(1, 8, 64)):
+    """The oracle's dequantize (C, row-parallel over all host threads) then fp32 torch matmul for
+    the same 21 calls on the same packed weights, each timed as the median of 5 after 2 warm-ups."""
     import torch
 
     import oracle as O
-    from qlin.quantize import quantize_gguf
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    rows = rows or n
-    rng = np.random.default_rng(0)
-    total_s, dec_s, mm_s, alg = 0.0, 0.0, 0.0, 0
+    torch.set_num_threads(pool.threads)
+    dec_ms, mm_ms, alg = 0.0, 0.0, 0
     for t in GGUF_SUITE:
-        w = (rng.standard_normal((rows, k)) * 0.02).astype(np.float32)
-        raw = quantize_gguf(w, t)
+        raw = bases[t].numpy()
+        wd = None
+
+        def decode(raw=raw, t=t):
+            nonlocal wd
+            wd = torch.from_numpy(pool.rows(lambda r0, r1: O.gguf_dequantize(raw[r0:r1], t, (r1 - r0, k)), n))
+
+        dms = median_ms(decode)
         for m in ms:
             x = torch.randn(m, k).half().float()
-            t0 = time.perf_counter()
-            wd = torch.from_numpy(O.gguf_dequantize(raw, t, (rows, k)))
-            t1 = time.perf_counter()
-            y = x @ wd.T
-            t2 = time.perf_counter()
-            del y
-            dec_s += (t1 - t0) * n / rows
-            mm_s += (t2 - t1) * n / rows
+            mms = median_ms(lambda: x @ wd.T)
+            dec_ms += dms
+            mm_ms += mms
             alg += gguf_bytes(t, n, k) + m * k * 2 + m * n * 2
-    total_s = dec_s + mm_s
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    total = dec_ms + mm_ms
     return {
-        "value": round(alg / total_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"one pass of the 21 calls (7 types x M in {{1,8,64}}, K=N=4096); decode of {rows} of "
-                   f"{n} rows per call by the C oracle on 1 thread, fp32 torch matmul on {threads} threads, "
-                   f"scaled to N={n}"),
-        "decode_ms": round(dec_s * 1e3, 1), "matmul_ms": round(mm_s * 1e3, 1), "cpu_model": cpu_model,
-        "decode_threads": 1,
+        "value": round(alg / (total * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": pool.threads, "kind": "port",
+        "sample": (f"the 21 calls (7 types x M in {{1,8,64}}, K=N=4096) in full: oracle C decode of the whole "
+                   f"weight row-parallel on {pool.threads} threads, then fp32 torch matmul on {pool.threads} "
+                   "threads; each leg the median of 5 after 2 warm-ups"),
+        "decode_ms": round(dec_ms, 2), "matmul_ms": round(mm_ms, 2), "total_ms": round(total, 2),
+        "cpu_model": cpu_model(), "threads": pool.threads,
     }
 
 
@@ -220,11 +294,11 @@ def kernel_breakdown(detail):
     return out
 
 
-def measured_traffic(kernel):
-    """HBM bytes per call of `kernel` (a '+'-joined path adds its kernels) from the committed
+def measured_traffic(kernel, summary="gguf_linear_k4096_counters.md"):
+    """HBM bytes per call of `kernel` (a '+'-joined path adds its kernels) from a committed
     rocprofv3 FETCH_SIZE + WRITE_SIZE summary (counter runs cannot happen inside the timed
     process); None when the summary has no line for one of them."""
-    path = os.path.join(ROOT, "profiles", "gguf_linear_k4096_counters.md")
+    path = os.path.join(ROOT, "profiles", summary)
     per = {}
     try:
         for line in open(path):
@@ -237,19 +311,283 @@ def measured_traffic(kernel):
     return sum(per[k] for k in parts) if all(k in per for k in parts) else None
 
 
-def profile_pass(n=4096, k=4096, ms=(1, 8, 64), reps=3):
-    """Eager launches for counter collection (each dispatch is profiled on its own)."""
+# ------------------------------------------------------------------------------------------------
+# INT8-ConvRot, W4A8, W6A8 and the DiT layer at their benchmark shapes
+# ------------------------------------------------------------------------------------------------
+
+# name -> workload.  INT8: weights N(0, 0.02) rotated by the 128-point block Hadamard and quantized
+# per output channel by the host quantizer, fp16 scales.  W4/W6: random legal symmetric codes and
+# fp16 group scales inside the int8 grid (the offline quantizer takes minutes at these sizes; no
+# kernel's time depends on code values).  Activations fp16 N(0, 1) (W4A8: 1% outliers at 20).
+CONFIGS = {
+    "int8_convrot_m256_k3072_n3072": dict(kind="int8", m=256, k=3072, n=3072, g=128),
+    "w4a8_m4096_k3072_n12288": dict(kind="a8", bits=4, gs=128, g=128, m=4096, k=3072, n=12288, outliers=True),
+    "w6a8_m1024_k5120_n13824": dict(kind="a8", bits=6, gs=64, g=256, m=1024, k=5120, n=13824),
+    "w6a8_m1024_k13824_n5120": dict(kind="a8", bits=6, gs=64, g=256, m=1024, k=13824, n=5120),
+    "w6a8_m9504_k5120_n13824": dict(kind="a8", bits=6, gs=64, g=256, m=9504, k=5120, n=13824),
+    "w6a8_m9504_k13824_n5120": dict(kind="a8", bits=6, gs=64, g=256, m=9504, k=13824, n=5120),
+    "dit_layer_int8_convrot_m4608": dict(kind="dit", m=4608, g=128,
+                                         linears=((9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288))),
+}
+
+# The launches a call makes at these shapes (the C ABI's dispatch), named as in the kernel traces.
+CONFIG_KERNELS = {
+    "int8_convrot_m256_k3072_n3072": "prologue_kernel+gemm_wo_dmas_kernel<64,64,256,3>",
+    "w4a8_m4096_k3072_n12288": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
+    "w6a8_m1024_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
+    "w6a8_m1024_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<128,128>",
+    "w6a8_m9504_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
+    "w6a8_m9504_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
+    "dit_layer_int8_convrot_m4608": "4x (prologue_kernel+gemm_wo_dma_kernel<256,3>)",
+}
+
+
+def int8_weight(n, k, g, seed):
+    import torch
+    from qlin.quantize import quantize_int8_convrot_weight
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(seed)) * 0.02).numpy()
+    q, s = quantize_int8_convrot_weight(w, g)
+    return torch.from_numpy(q), torch.from_numpy(s).half()
+
+
+def a8_weight(n, k, bits, gs, seed):
+    """Random legal symmetric codes (4-bit 1..15, 6-bit 1..63), packed; fp16 group scales that keep
+    level * s_rel inside the int8 grid; fp32 channel scales."""
+    import torch
+    from qlin.quantize import pack_codes
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(1, (15 if bits == 4 else 63) + 1, (n, k), generator=g, dtype=torch.int32)
+    lo, hi = (8.0, 18.0) if bits == 4 else (2.0, 4.1)
+    s_rel = (lo + (hi - lo) * torch.rand(n, k // gs, generator=g)).half()
+    s_ch = (torch.rand(n, generator=g) * 2e-4 + 1e-4).float()
+    return pack_codes(codes, bits), s_rel, s_ch
+
+
+def permuted_copies(tensors, n, copies, seed):
+    """`copies` weights on the GPU made by permuting the rows of `tensors` alike (distinct bytes,
+    still a valid packed weight)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    dev = [t.cuda() for t in tensors]
+    out = [tuple(dev)]
+    for _ in range(copies - 1):
+        p = torch.randperm(n, generator=g).cuda()
+        out.append(tuple(t[p].contiguous() for t in dev))
+    return out
+
+
+def gpu_activations(m, k, seed, outliers=False):
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(m, k, device="cuda", generator=g)
+    if outliers:
+        mask = torch.rand(m, k, device="cuda", generator=g) < 0.01
+        x = torch.where(mask, 20.0 * torch.sign(x), x)
+    return x.half()
+
+
+def cpu_linear_baseline(pool, name, m, k, n, decode_rows, rows_n, rows_m=256):
+    """Dequantize-then-matmul on the host for one call: the oracle's C decode of `rows_n` weight
+    rows (row-parallel on all host threads), then an fp32 torch matmul of `rows_m` activation rows
+    against them; each leg the median of 5 after 2 warm-ups, scaled to the full M and N."""
+    import torch
+    torch.set_num_threads(pool.threads)
+    rows_m = min(rows_m, m)
+    wd = {}
+
+    def decode():
+        wd["w"] = torch.from_numpy(pool.rows(decode_rows, rows_n))
+
+    dms = median_ms(decode)
+    x = torch.randn(rows_m, k).half().float()
+    mms = median_ms(lambda: x @ wd["w"].T)
+    dec_full = dms * n / rows_n
+    mm_full = mms * (m / rows_m) * (n / rows_n)
+    total = dec_full + mm_full
+    return {
+        "value": round(2 * m * n * k / (total * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": pool.threads,
+        "kind": "port",
+        "sample": (f"{name}: oracle C decode of {rows_n} of {n} weight rows to fp32 (original basis) on "
+                   f"{pool.threads} threads, fp32 torch matmul of {rows_m} of {m} activation rows against them "
+                   f"on {pool.threads} threads; medians of 5 after 2 warm-ups, scaled to M={m}, N={n}"),
+        "decode_ms": round(dec_full, 2), "matmul_ms": round(mm_full, 2), "total_ms": round(total, 2),
+    }
+
+
+def run_configs(names, steps, warmup, pool):
+    """Time each named workload; `pool` (a HostPool) also runs its CPU baseline, None skips it."""
     import torch
     import qlin
-    weights = {t: make_gguf_weights(t, n, k, reps * len(ms), seed=i) for i, t in enumerate(GGUF_SUITE)}
-    g = torch.Generator().manual_seed(1)
-    xs = {m: torch.randn(m, k, generator=g).half().cuda() for m in ms}
-    for t in GGUF_SUITE:
-        tid = qlin.GGUF_TYPES[t][0]
-        for j, m in enumerate(ms):
-            for r in range(reps):
-                qlin.gguf_linear(xs[m], weights[t][r * len(ms) + j], tid, (n, k))
-    # reference kernel of known traffic: an elementwise pass reading and writing 64 MiB each
+
+    import oracle as O
+    out = {}
+    for name in names:
+        cfg = CONFIGS[name]
+        log(f"[{name}] building ...")
+        if cfg["kind"] == "int8":
+            m, k, n, g = cfg["m"], cfg["k"], cfg["n"], cfg["g"]
+            q, s = int8_weight(n, k, g, seed=7)
+            copies = max(1, -(-POOL_BYTES // (n * k)))
+            ws = permuted_copies((q, s), n, copies, seed=8)
+            x = gpu_activations(m, k, seed=9)
+
+            def step():
+                for qd, sd in ws:
+                    qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=g)
+
+            msr, _ = time_graph(step, steps, warmup)
+            us = msr / copies * 1e3
+            eager = time_eager(lambda: qlin.int8_linear(x, ws[0][0], ws[0][1], convrot=True, convrot_groupsize=g))
+            flops, nbytes = 2 * m * n * k, n * k + n * 2 + m * k * 2 + m * n * 2
+            tfl = flops / (us * 1e-6) / 1e12
+            qn, sn = q.numpy(), s.float().numpy()
+            cpu = pool and cpu_linear_baseline(pool, name, m, k, n,
+                                               lambda r0, r1: O.rotate(O.dequantize_int8(qn[r0:r1], sn[r0:r1]), g), n)
+            rec = {"us_per_call": round(us, 2), "eager_us_per_call": round(eager, 2), "TFLOPs": round(tfl, 2),
+                   "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "pool_copies": copies,
+                   "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS,
+                                "unit": "TFLOP/s", "frac": round(tfl / FP16_PEAK_TFLOPS, 4),
+                                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "kernel": CONFIG_KERNELS[name], "flops_per_call": flops, "bytes_per_call": nbytes,
+                                "traffic": None},
+                   "cpu_baseline": cpu}
+        elif cfg["kind"] == "a8":
+            m, k, n, bits, gs, g = cfg["m"], cfg["k"], cfg["n"], cfg["bits"], cfg["gs"], cfg["g"]
+            q, sr, sc = a8_weight(n, k, bits, gs, seed=11)
+            wbytes = q.numel() + sr.numel() * 2 + n * 4
+            copies = max(1, -(-POOL_BYTES // wbytes))
+            ws = permuted_copies((q, sr, sc), n, copies, seed=12)
+            x = gpu_activations(m, k, seed=13, outliers=cfg.get("outliers", False))
+
+            def step():
+                for qd, srd, scd in ws:
+                    qlin.w4a8_int8_linear(x, qd, srd, scd, None, None, None, gs, g)
+
+            msr, _ = time_graph(step, steps, warmup)
+            us = msr / copies * 1e3
+            flops, nbytes = 2 * m * n * k, wbytes + m * k * 2 + m * n * 2
+            tops = flops / (us * 1e-6) / 1e12
+            qn, srn, scn = q.view(torch.uint8).numpy(), sr.float().numpy(), sc.numpy()
+            cpu = pool and cpu_linear_baseline(
+                pool, name, m, k, n,
+                lambda r0, r1: O.dequantize_w4a8(qn[r0:r1], srn[r0:r1], scn[r0:r1], None, gs, g, bits=bits), 1024)
+            rec = {"us_per_call": round(us, 2), "TOPs": round(tops, 2),
+                   "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "pool_copies": copies,
+                   "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                                "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "kernel": CONFIG_KERNELS[name], "ops_per_call": flops, "bytes_per_call": nbytes,
+                                "traffic": None},
+                   "cpu_baseline": cpu}
+        else:  # one DiT block layer: QKV, O, MLP up, MLP down
+            m, g = cfg["m"], cfg["g"]
+            layer_bytes = sum(n * k for n, k in cfg["linears"])
+            copies = max(1, -(-POOL_BYTES // layer_bytes))
+            lin = []
+            for i, (n, k) in enumerate(cfg["linears"]):
+                q, s = int8_weight(n, k, g, seed=20 + i)
+                lin.append((n, k, q, s, permuted_copies((q, s), n, copies, seed=30 + i), gpu_activations(m, k, 40 + i)))
+
+            def step():
+                for c in range(copies):
+                    for n, k, _, _, ws, x in lin:
+                        qlin.int8_linear(x, ws[c][0], ws[c][1], convrot=True, convrot_groupsize=g)
+
+            msr, _ = time_graph(step, steps, warmup)
+            layer_ms = msr / copies
+            per_linear = {}
+            for n, k, _, _, ws, x in lin:
+                def one(ws=ws, x=x):
+                    for qd, sd in ws:
+                        qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=g)
+                mo, _ = time_graph(one, steps, warmup)
+                per_linear[f"{k}->{n}"] = round(mo / copies * 1e3, 2)
+            flops = sum(2 * m * n * k for n, k in cfg["linears"])
+            tfl = flops / (layer_ms * 1e-3) / 1e12
+            # torch's fp16 F.linear on resident fp16 weights, the same pool size in weights
+            dense_copies = max(1, -(-POOL_BYTES // (2 * layer_bytes)))
+            dense = [[(torch.randn(n, k, device="cuda").half() * 0.02) for n, k in cfg["linears"]]
+                     for _ in range(dense_copies)]
+            xs = [x for *_, x in lin]
+
+            def dstep():
+                for c in range(dense_copies):
+                    for w, x in zip(dense[c], xs):
+                        torch.nn.functional.linear(x, w)
+
+            dms, _ = time_graph(dstep, steps, warmup)
+            dense_ms = dms / dense_copies
+            del dense
+            # CPU: one layer, each linear sampled as for the single-linear configs, times 60
+            cpu = None
+            if pool:
+                parts = []
+                for n, k, q, s, _, _ in lin:
+                    qn, sn = q.numpy(), s.float().numpy()
+                    parts.append(cpu_linear_baseline(
+                        pool, f"{k}->{n}", m, k, n,
+                        lambda r0, r1, qn=qn, sn=sn: O.rotate(O.dequantize_int8(qn[r0:r1], sn[r0:r1]), g), 512))
+                layer = sum(p["total_ms"] for p in parts)
+                cpu = {"value": round(flops / (layer * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": pool.threads,
+                       "kind": "port",
+                       "sample": (f"one layer's four linears, each: oracle C decode of 512 weight rows to fp32 "
+                                  f"(original basis) on {pool.threads} threads, fp32 torch matmul of 256 of {m} "
+                                  f"activation rows against them on {pool.threads} threads; medians of 5 after 2 "
+                                  f"warm-ups, scaled to the linear's M and N; x{DIT_LAYERS} for the stack"),
+                       "decode_ms": round(sum(p["decode_ms"] for p in parts), 2),
+                       "matmul_ms": round(sum(p["matmul_ms"] for p in parts), 2),
+                       "layer_ms": round(layer, 2), "stack_ms": round(layer * DIT_LAYERS, 1)}
+            rec = {"ms_per_layer": round(layer_ms, 4), "ms_60_layers": round(layer_ms * DIT_LAYERS, 2),
+                   "layers": DIT_LAYERS, "us_per_linear": per_linear, "TFLOPs": round(tfl, 2),
+                   "fp16_torch_ms_per_layer": round(dense_ms, 4),
+                   "vs_fp16_dense": round(layer_ms / dense_ms, 3), "pool_copies": copies,
+                   "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS,
+                                "unit": "TFLOP/s", "frac": round(tfl / FP16_PEAK_TFLOPS, 4),
+                                "kernel": CONFIG_KERNELS[name], "flops_per_layer": flops, "traffic": None},
+                   "cpu_baseline": cpu}
+        if rec["cpu_baseline"] is None:
+            del rec["cpu_baseline"]
+        out[name] = rec
+        log(f"[{name}] " + json.dumps({k: v for k, v in rec.items() if k != "cpu_baseline"}))
+        ws = lin = None
+        torch.cuda.empty_cache()
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# profiling passes and the optional suites
+# ------------------------------------------------------------------------------------------------
+
+def profile_pass(which, reps=3, n=4096, k=4096, ms=(1, 8, 64)):
+    """Eager launches for rocprofv3 kernel-trace and counter runs: `which` is "gguf" or a config
+    name; each call `reps` times on distinct weights, then an elementwise pass over 64 MiB in and
+    64 MiB out as the byte-counter reference."""
+    import torch
+    import qlin
+    if which == "gguf":
+        weights = {t: make_gguf_weights(t, n, k, reps * len(ms), seed=i) for i, t in enumerate(GGUF_SUITE)}
+        g = torch.Generator().manual_seed(1)
+        xs = {m: torch.randn(m, k, generator=g).half().cuda() for m in ms}
+        for t in GGUF_SUITE:
+            tid = qlin.GGUF_TYPES[t][0]
+            for j, m in enumerate(ms):
+                for r in range(reps):
+                    qlin.gguf_linear(xs[m], weights[t][r * len(ms) + j], tid, (n, k))
+    else:
+        cfg = CONFIGS[which]
+        if cfg["kind"] == "a8":
+            q, sr, sc = a8_weight(cfg["n"], cfg["k"], cfg["bits"], cfg["gs"], seed=11)
+            ws = permuted_copies((q, sr, sc), cfg["n"], reps, seed=12)
+            x = gpu_activations(cfg["m"], cfg["k"], 13, cfg.get("outliers", False))
+            for qd, srd, scd in ws:
+                qlin.w4a8_int8_linear(x, qd, srd, scd, None, None, None, cfg["gs"], cfg["g"])
+        else:
+            lins = ((cfg["n"], cfg["k"]),) if cfg["kind"] == "int8" else cfg["linears"]
+            for i, (n_, k_) in enumerate(lins):
+                q, s = int8_weight(n_, k_, cfg["g"], seed=20 + i)
+                x = gpu_activations(cfg["m"], k_, 40 + i)
+                for qd, sd in permuted_copies((q, s), n_, reps, seed=30 + i):
+                    qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=cfg["g"])
     src = torch.ones(16 << 20, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(reps):
@@ -259,7 +597,7 @@ def profile_pass(n=4096, k=4096, ms=(1, 8, 64), reps=3):
 
 
 def other_suites(which, steps, warmup):
-    """INT8-ConvRot, W4A8, W6A8 and the DiT layer stack at their benchmark shapes (stderr JSON lines)."""
+    """LoRA beside the quantized linears and the frozen-weight input gradient (stderr JSON lines)."""
     import torch
     import qlin
     from qlin.quantize import quantize_int8_convrot_weight, quantize_w4a8_int8_weight
@@ -278,59 +616,6 @@ def other_suites(which, steps, warmup):
         log(json.dumps(rec))
         out.append(rec)
 
-    if which in ("int8", "all"):
-        m, n, k = 256, 3072, 3072
-        q, s = quantize_int8_convrot_weight(weight(n, k), 128)
-        qd, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).half().cuda()
-        x = torch.randn(m, k).half().cuda()
-        timed("int8_convrot M256 K3072 N3072", lambda: qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=128),
-              2 * m * n * k, n * k + n * 2 + m * k * 2 + m * n * 2, FP16_PEAK_TFLOPS, "TFLOPs")
-    if which in ("w4a8", "all"):
-        m, n, k = 4096, 12288, 3072
-        log("[w4a8] quantizing 12288x3072 ...")
-        q, sr, sc, cb = quantize_w4a8_int8_weight(weight(n, k), bits=4, group_size=128, convrot_groupsize=128,
-                                                  codebook=None, s_rel_dtype=torch.float16)
-        qd, srd, scd = q.cuda(), sr.cuda(), sc.cuda()
-        g = torch.Generator().manual_seed(2)
-        x = torch.randn(m, k, generator=g)
-        x = torch.where(torch.rand(m, k, generator=g) < 0.01, 20.0 * torch.sign(x), x).half().cuda()
-        timed("w4a8 M4096 K3072 N12288", lambda: qlin.w4a8_int8_linear(x, qd, srd, scd, None, None, None, 128, 128),
-              2 * m * n * k, q.numel() + sr.numel() * 2 + n * 4 + m * k * 2 + m * n * 2, INT8_PEAK_TOPS, "TOPs")
-    if which in ("w6a8", "all"):
-        packed = {}
-        for (n, k) in ((13824, 5120), (5120, 13824)):
-            log(f"[w6a8] quantizing {n}x{k} ...")
-            q, sr, sc, cb = quantize_w4a8_int8_weight(weight(n, k), bits=6, group_size=64, convrot_groupsize=256,
-                                                      codebook=None, s_rel_dtype=torch.float16)
-            packed[(n, k)] = (q, sr, sc)
-        for m in (1024, 9504):
-            for (n, k), (q, sr, sc) in packed.items():
-                qd, srd, scd = q.cuda(), sr.cuda(), sc.cuda()
-                x = torch.randn(m, k).half().cuda()
-                timed(f"w6a8 M{m} K{k} N{n}", lambda: qlin.w4a8_int8_linear(x, qd, srd, scd, None, None, None, 64, 256),
-                      2 * m * n * k, q.numel() + sr.numel() * 2 + n * 4 + m * k * 2 + m * n * 2, INT8_PEAK_TOPS, "TOPs")
-    if which in ("dit", "all"):
-        m, h = 4608, 3072
-        shapes = [(9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288)]
-        layer = []
-        for (n, k) in shapes:
-            q, s = quantize_int8_convrot_weight(weight(n, k), 128)
-            layer.append((torch.from_numpy(q).cuda(), torch.from_numpy(s).half().cuda(),
-                          torch.randn(m, k).half().cuda()))
-        dense = [(torch.randn(n, k).half().cuda() * 0.02, torch.randn(m, k).half().cuda()) for (n, k) in shapes]
-
-        def qstep():
-            for qd, sd, x in layer:
-                qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=128)
-
-        def dstep():
-            for w, x in dense:
-                torch.nn.functional.linear(x, w)
-
-        fl = sum(2 * m * n * k for n, k in shapes)
-        nb = sum(n * k for n, k in shapes)
-        timed("dit_layer int8_convrot (4 linears, M4608)", qstep, fl, nb, FP16_PEAK_TFLOPS, "TFLOPs")
-        timed("dit_layer fp16 torch F.linear (resident weights)", dstep, fl, nb * 2, FP16_PEAK_TFLOPS, "TFLOPs")
     if which in ("lora", "all"):
         # unmerged LoRA beside the quantized linears at the reference's LoRA benchmark shape
         # (M, K, N) = (4608, 6144, 6144), rank 64, bf16 in and out, ConvRot on: the base call, the
@@ -390,12 +675,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--suite", default="gguf", choices=["gguf", "int8", "w4a8", "w6a8", "dit", "lora", "grad", "all"])
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-rows", type=int, default=1024, help="weight rows decoded per call for the CPU baseline")
-    ap.add_argument("--profile", action="store_true",
-                    help="eager launches for rocprofv3 counter runs (no timing, no JSON): each GGUF call three "
-                         "times on distinct weights, then a 64 MiB device copy as the byte-counter reference")
+    ap.add_argument("--suite", default="main", choices=["main", "lora", "grad", "all"],
+                    help="main: the JSON line (GGUF headline + configs); lora / grad: extra suites on stderr")
+    ap.add_argument("--configs", default="all",
+                    help="comma-separated names from CONFIGS for the `configs` object, 'all' or 'none'")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--profile", default=None, choices=["gguf", *CONFIGS],
+                    help="eager launches of one workload for rocprofv3 kernel-trace / counter runs (no timing, "
+                         "no JSON): each call three times on distinct weights, then a 64 MiB elementwise pass as "
+                         "the byte-counter reference")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported: the linear shards by weight "
@@ -409,16 +697,19 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
 
     if a.profile:
-        profile_pass()
+        profile_pass(a.profile)
         return
-    if a.suite != "gguf":
+    if a.suite != "main":
         other_suites(a.suite, a.steps, a.warmup)
         if a.suite != "all":
             return
+    pool = None if a.no_cpu else HostPool(host_threads())
     r = suite_gguf(a.steps, a.warmup)
     kernels = kernel_breakdown(r["detail"])
     dom = max(kernels, key=lambda k: kernels[k]["us_total"])
     dk = kernels[dom]
+    names = list(CONFIGS) if a.configs == "all" else ([] if a.configs == "none" else a.configs.split(","))
+    configs = run_configs(names, a.steps, a.warmup, pool) if names else {}
     line = {
         "metric": METRIC,
         "value": round(r["value"], 1),
@@ -431,7 +722,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic",
+        "data": ("synthetic: GGUF weights N(0, 0.02) quantized on the host; INT8 weights N(0, 0.02) rotated and "
+                 "quantized on the host; W4/W6 random legal codes and group scales; activations fp16 N(0, 1)"),
         "config": {
             "workload": "gguf_decode_linear K=N=4096, M in {1,8,64}, types Q4_0 Q8_0 Q4_K Q5_K Q6_K IQ4_NL IQ4_XS "
                         "(21 calls per step, weights cycled through a >=1 GiB pool, HIP-graph replay)",
@@ -447,10 +739,11 @@ def main():
         },
         "kernels": kernels,
         "detail": r["detail"],
+        "configs": configs,
     }
-    if not a.no_cpu:
-        log("[cpu] oracle dequantize-then-matmul baseline ...")
-        line["cpu_baseline"] = cpu_baseline_gguf(rows=a.cpu_rows)
+    if pool:
+        log("[cpu] oracle dequantize-then-matmul baseline for the headline ...")
+        line["cpu_baseline"] = cpu_baseline_gguf(pool, r["bases"])
     print(json.dumps(line), flush=True)
 
 

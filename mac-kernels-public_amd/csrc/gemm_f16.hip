@@ -10,6 +10,7 @@
 // Global->LDS is double-buffered through registers: the next tile's loads are issued before the
 // current tile's MFMAs.
 #include <type_traits>
+#include <utility>
 
 #include "qlin_internal.h"
 #include "gguf_exact.h"
@@ -600,6 +601,184 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
     }
 }
 
+// Wait until at most (STAGES - 2) stages of this wave's DMAs are outstanding, for a wave that
+// issues `nd` DMAs per stage (wave-uniform, 1..8).
+template <int STAGES>
+__device__ __forceinline__ void wait_stages(int nd) {
+    switch (nd) {
+        case 1: wait_vmcnt<(STAGES - 2) * 1>(); break;
+        case 2: wait_vmcnt<(STAGES - 2) * 2>(); break;
+        case 3: wait_vmcnt<(STAGES - 2) * 3>(); break;
+        case 4: wait_vmcnt<(STAGES - 2) * 4>(); break;
+        case 5: wait_vmcnt<(STAGES - 2) * 5>(); break;
+        case 6: wait_vmcnt<(STAGES - 2) * 6>(); break;
+        case 7: wait_vmcnt<(STAGES - 2) * 7>(); break;
+        default: wait_vmcnt<(STAGES - 2) * 8>(); break;
+    }
+}
+
+// INT8 weight-only GEMM for grids too small for 256 x 256 tiles (a few hundred activation rows):
+// BMT x BNT output tiles of 32 x 32 MFMA sub-tiles, one sub-tile per wave, and when the tile has
+// at most four sub-tiles the two 32-value halves of every 64-value k-block go to two waves (their
+// sums are added through LDS at the end, always in the same order).  Both operands arrive by LDS
+// DMA through a ring of STAGES k-tiles of KT values.  One DMA instruction moves whole runs of
+// KT bytes (weights) or 2 KT bytes (activations) of a few rows, so each weight row is read in long
+// contiguous runs rather than 64-byte pieces of thousands of rows at once.
+// LDS rows hold CH = row bytes / 16 chunks; logical chunk c of row r sits at c ^ sw(r) with
+// sw(r) = (r / (16 / CH)) % CH for CH < 16 and r % 16 otherwise, so the 16 rows one 16-lane group
+// reads at one logical chunk land in 16 distinct 16-byte bank groups.  k order inside a 64-value
+// block b: MFMA step 2p + e of lane half h takes k = 64 b + 32 p + 16 h + 8 e .. + 7 in both
+// operands, so one 16-byte weight read (logical chunk 4 b + 2 p + h) feeds two steps.
+template <int BMT, int BNT>
+constexpr int wo_dmas_waves() {
+    return (BMT / 32) * (BNT / 32) * ((BMT / 32) * (BNT / 32) <= 4 ? 2 : 1);
+}
+
+template <int CH>
+__device__ __forceinline__ int lds_swz(int r) {
+    if constexpr (CH < 16) return (r / (16 / CH)) % CH;
+    else return r % 16;
+}
+
+template <int BMT, int BNT, int KT, int STAGES>
+__global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT>())) void gemm_wo_dmas_kernel(GemmF16Args a) {
+    constexpr int TM = BMT / 32, TILES = TM * (BNT / 32);
+    constexpr int KH = TILES <= 4 ? 2 : 1;
+    constexpr int NW = TILES * KH;
+    constexpr int CA = KT / 8, CB = KT / 16;                  // 16-byte chunks per LDS row
+    constexpr int ASZ = BMT * KT * 2, BSZ = BNT * KT;          // bytes per stage
+    constexpr int WA = BMT * CA / 64, WB = BNT * CB / 64;     // wave-wide DMA instructions per stage
+    constexpr int NA = (WA + NW - 1) / NW, NB = (WB + NW - 1) / NW;
+    static_assert(BMT % 32 == 0 && BNT % 32 == 0 && NW <= 8 && STAGES >= 3, "tile shape");
+    static_assert(KT % 64 == 0 && (BMT * CA) % 64 == 0 && (BNT * CB) % 64 == 0, "whole DMA instructions");
+    static_assert(NA + NB <= 8, "DMAs per wave");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ)];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int t = wave % TILES, kh = wave / TILES;
+    const int tm = t % TM, tn = t / TM;
+    int mt, nt;
+    xcd_tile_f16(blockIdx.x, (int)gridDim.x, (int)((a.M + BMT - 1) / BMT), (int)((a.N + BNT - 1) / BNT), mt, nt);
+    const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
+    const int ktiles = (int)(a.K / KT);
+
+    // DMA instruction j (0 <= j < WA for activations, 0 <= j < WB for weights) is issued by wave
+    // j % NW and fills physical chunks u = 64 j + lane of its operand's stage: row u / CH, position
+    // u % CH, holding logical chunk (u % CH) ^ sw(row).  Rows past M or N re-read the last row
+    // (never stored).
+    const f16* asrc[NA];
+    const int8_t* bsrc[NB];
+    int na = 0, nb = 0;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int j = wave + NW * i, u = 64 * j + lane, row = u / CA;
+        asrc[i] = a.x + min(m0 + row, a.M - 1) * a.ldx + 8 * ((u % CA) ^ lds_swz<CA>(row));
+        na += j < WA;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int j = wave + NW * i, u = 64 * j + lane, row = u / CB;
+        bsrc[i] = (const int8_t*)a.w + min(n0 + row, a.N - 1) * a.ldw + 16 * ((u % CB) ^ lds_swz<CB>(row));
+        nb += j < WB;
+    }
+    const int nd = na + nb;
+    auto dma = [&](int kt, int buf) {
+        const int64_t k0 = (int64_t)min(kt, ktiles - 1) * KT;  // past the end: re-reads the last tile
+        uint8_t* st = smem + buf * (ASZ + BSZ);
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            if (i < na) lds_dma16(asrc[i] + k0, st + 16 * 64 * (wave + NW * i));
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+            if (i < nb) lds_dma16(bsrc[i] + k0, st + ASZ + 16 * 64 * (wave + NW * i));
+    };
+
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const int ra = 32 * tm + r32, rb = 32 * tn + r32;
+    const int swa = lds_swz<CA>(ra), swb = lds_swz<CB>(rb);
+    auto mfmas = [&](int buf) {
+        const uint8_t* as = smem + buf * (ASZ + BSZ) + ra * (KT * 2);
+        const uint8_t* bs = smem + buf * (ASZ + BSZ) + ASZ + rb * KT;
+#pragma unroll
+        for (int b = 0; b < KT / 64; ++b)
+#pragma unroll
+            for (int pp = 0; pp < 2 / KH; ++pp) {
+                const int p = KH == 2 ? kh : pp;
+                const u32x4 q = *reinterpret_cast<const u32x4*>(bs + 16 * ((4 * b + 2 * p + h) ^ swb));
+                const f16x8 a0 = *reinterpret_cast<const f16x8*>(as + 16 * ((8 * b + 4 * p + 2 * h) ^ swa));
+                const f16x8 a1 = *reinterpret_cast<const f16x8*>(as + 16 * ((8 * b + 4 * p + 2 * h + 1) ^ swa));
+                uint32_t o[8];
+                i8x4_to_f16(q.x, o[0], o[1]);
+                i8x4_to_f16(q.y, o[2], o[3]);
+                i8x4_to_f16(q.z, o[4], o[5]);
+                i8x4_to_f16(q.w, o[6], o[7]);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]}),
+                                                             acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, __builtin_bit_cast(f16x8, u32x4{o[4], o[5], o[6], o[7]}),
+                                                             acc, 0, 0, 0);
+            }
+    };
+
+    // Barrier without a memory fence: each wave's wait covers its own DMAs, the loop writes LDS only
+    // by DMA, and the fragment reads of a buffer complete before the barrier after which the next
+    // DMA may overwrite it.
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st) dma(st, st);
+    wait_stages<STAGES>(nd);
+    __builtin_amdgcn_s_barrier();
+    for (int kt = 0; kt < ktiles; ++kt) {
+        dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(kt % STAGES);
+        wait_lgkmcnt0();
+        wait_stages<STAGES>(nd);  // tile kt + 1 has landed
+        __builtin_amdgcn_s_barrier();
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    // Epilogue: the sub-tiles go to LDS as fp32 (row stride BNT + 4 words); with two k halves the
+    // second half is added to the first.  Lane l, register r of a 32 x 32 sub-tile holds row
+    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Then y = ldexp(acc, xexp[m]) * scale[n] + bias[n],
+    // 8 consecutive outputs per thread with 16-byte stores.
+    constexpr int ORW = BNT + 4;
+    static_assert(BMT * ORW * 4 <= (int)sizeof(smem), "output staging must fit");
+    float* ot = reinterpret_cast<float*>(smem);
+    float* op = ot + (32 * tm + 4 * h) * ORW + 32 * tn + r32;
+    if (kh == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) op[(8 * (r / 4) + r % 4) * ORW] = acc[r];
+    }
+    __syncthreads();
+    if constexpr (KH == 2) {
+        if (kh == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) op[(8 * (r / 4) + r % 4) * ORW] += acc[r];
+        }
+        __syncthreads();
+    }
+    constexpr int NT = 64 * NW, CPR = BNT / 8;
+    const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
+    for (int c = tid; c < BMT * CPR; c += NT) {
+        const int row = c / CPR, cc = c % CPR;
+        const int64_t m = m0 + row, nc = n0 + 8 * cc;
+        if (m >= a.M || nc >= a.N) continue;
+        const int ncount = (int)min<int64_t>(8, a.N - nc);
+        const int e2 = a.xexp ? a.xexp[m] : 0;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t n = min(nc + e, a.N - 1);
+            const float cs = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            const float bv = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+            v[e] = __builtin_ldexpf(ot[row * ORW + 8 * cc + e], e2) * cs + bv;
+        }
+        store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
+    }
+}
+
 template <int WK, int GT>
 hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
     if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
@@ -612,6 +791,30 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
         if (vec && tiles(256, 256) >= 160) {
             hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, a);
             return hipGetLastError();
+        }
+        // grids of fewer than 160 tiles of 128 x 128: small tiles through a DMA ring, the one of
+        // 64 x 128, 64 x 64, 32 x 128, 32 x 64 with the most workgroups that still run in one round
+        // on the 256 CUs; the widest k-tile K allows (256 values per weight row per stage measured
+        // 20% faster than 64 at M = 256, K = N = 3072)
+        if (vec && tiles(128, 128) < 160) {
+            int bm = 32, bn = 64, best = 0;
+            for (auto [m_, n_] : {std::pair{64, 128}, {64, 64}, {32, 128}, {32, 64}}) {
+                const int64_t t = tiles(m_, n_);
+                if (t <= 256 && t > best) { best = (int)t; bm = m_; bn = n_; }
+            }
+            int kt = a.K % 256 == 0 ? 256 : a.K % 128 == 0 ? 128 : 64;
+            if (bm == 64 && bn == 128 && kt == 256) kt = 128;  // 64 KB per stage would leave two stages
+            const dim3 grid((unsigned)tiles(bm, bn));
+#define QLIN_WOS(BMV, BNV, KTV, STV)                                                                            \
+    if (bm == BMV && bn == BNV && kt == KTV) {                                                                  \
+        hipLaunchKernelGGL((gemm_wo_dmas_kernel<BMV, BNV, KTV, STV>), grid, dim3(64 * wo_dmas_waves<BMV, BNV>()), 0, st, a); \
+        return hipGetLastError();                                                                               \
+    }
+            QLIN_WOS(64, 128, 128, 4) QLIN_WOS(64, 128, 64, 8)
+            QLIN_WOS(64, 64, 256, 3) QLIN_WOS(64, 64, 128, 4) QLIN_WOS(64, 64, 64, 8)
+            QLIN_WOS(32, 128, 256, 3) QLIN_WOS(32, 128, 128, 6) QLIN_WOS(32, 128, 64, 8)
+            QLIN_WOS(32, 64, 256, 4) QLIN_WOS(32, 64, 128, 8) QLIN_WOS(32, 64, 64, 8)
+#undef QLIN_WOS
         }
         if (vec) {
         // two-deep prefetch for the smaller tiles (at 256 x 256 it spills and measured slower)
