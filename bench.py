@@ -321,6 +321,7 @@ def measured_traffic(kernel, summary="gguf_linear_k4096_counters.md"):
 # kernel's time depends on code values).  Activations fp16 N(0, 1) (W4A8: 1% outliers at 20).
 CONFIGS = {
     "int8_convrot_m256_k3072_n3072": dict(kind="int8", m=256, k=3072, n=3072, g=128),
+    "int8_convrot_m1_k3072_n3072": dict(kind="int8", m=1, k=3072, n=3072, g=128, bound="hbm"),
     "w4a8_m4096_k3072_n12288": dict(kind="a8", bits=4, gs=128, g=128, m=4096, k=3072, n=12288, outliers=True),
     "w6a8_m1024_k5120_n13824": dict(kind="a8", bits=6, gs=64, g=256, m=1024, k=5120, n=13824),
     "w6a8_m1024_k13824_n5120": dict(kind="a8", bits=6, gs=64, g=256, m=1024, k=13824, n=5120),
@@ -333,6 +334,7 @@ CONFIGS = {
 # The launches a call makes at these shapes (the C ABI's dispatch), named as in the kernel traces.
 CONFIG_KERNELS = {
     "int8_convrot_m256_k3072_n3072": "prologue_kernel+gemm_wo_dmas_kernel<64,64,256,3>",
+    "int8_convrot_m1_k3072_n3072": "prologue_kernel+int8_gemv_kernel<1,3>",
     "w4a8_m4096_k3072_n12288": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m1024_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m1024_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<128,128>",
@@ -443,14 +445,17 @@ def run_configs(names, steps, warmup, pool):
             qn, sn = q.numpy(), s.float().numpy()
             cpu = pool and cpu_linear_baseline(pool, name, m, k, n,
                                                lambda r0, r1: O.rotate(O.dequantize_int8(qn[r0:r1], sn[r0:r1]), g), n)
+            gbs = nbytes / (us * 1e-6) / 1e9
+            if cfg.get("bound") == "hbm":
+                roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_frac": round(tfl / FP16_PEAK_TFLOPS, 4)}
+            else:
+                roof = {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tfl / FP16_PEAK_TFLOPS, 4), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+            roof.update({"kernel": CONFIG_KERNELS[name], "flops_per_call": flops, "bytes_per_call": nbytes,
+                         "traffic": None})
             rec = {"us_per_call": round(us, 2), "eager_us_per_call": round(eager, 2), "TFLOPs": round(tfl, 2),
-                   "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "pool_copies": copies,
-                   "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS,
-                                "unit": "TFLOP/s", "frac": round(tfl / FP16_PEAK_TFLOPS, 4),
-                                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                                "kernel": CONFIG_KERNELS[name], "flops_per_call": flops, "bytes_per_call": nbytes,
-                                "traffic": None},
-                   "cpu_baseline": cpu}
+                   "GBps": round(gbs, 1), "pool_copies": copies, "roofline": roof, "cpu_baseline": cpu}
         elif cfg["kind"] == "a8":
             m, k, n, bits, gs, g = cfg["m"], cfg["k"], cfg["n"], cfg["bits"], cfg["gs"], cfg["g"]
             q, sr, sc = a8_weight(n, k, bits, gs, seed=11)

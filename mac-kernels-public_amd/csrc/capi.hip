@@ -140,6 +140,8 @@ size_t ws_int8(int64_t M, int64_t K) { return align_up((size_t)(M * K * 2)) + al
 // MFMA kernels that stream the weights once (K split across workgroups from gguf_split_min_m
 // rows on); more -> row exponents + the tiled fp16 GEMM.
 constexpr int64_t GGUF_SMALLM_MAX_M = 64;
+// Largest M of the INT8 weight-streaming kernels (the GEMV for one or two rows, then small-M MFMA).
+constexpr int64_t INT8_SMALLM_MAX_M = 16;
 // Measured at K = N = 4096: the split kernel costs ~10 us at any M (two launches, partials) and
 // wins from M = 17 on, except Q6_K, whose 16-value units make the per-wave K-split kernel slower
 // (11.8 vs 13.9 us at M = 8).
@@ -437,8 +439,29 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
+    // weight streaming for few rows: the VALU GEMV (one or two rows), then the small-M MFMA kernel
     GemmF16Args a;
     if ((s = wo_activations(X, convrot_groupsize, ws, st, a.x, a.ldx, a.xexp))) return s;
+    if (M <= 2) {
+        Int8GemvArgs g;
+        g.x = a.x; g.ldx = a.ldx; g.xexp = a.xexp;
+        g.w = (const int8_t*)Q.data; g.ldw = Q.ld;
+        g.M = M; g.N = N; g.K = K;
+        g.scale = scale->data; g.scale_dtype = scale->dtype; g.scale_stride = sst;
+        g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
+        g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
+        if (int8_gemv_supported(g)) return hip_status(run_int8_gemv(g, st), "int8 gemv");
+    }
+    if (M <= INT8_SMALLM_MAX_M && int8_smallm_supported(M, K, Q.ld, Q.data)) {
+        GgufSmallMArgs g;
+        g.type = INT8_ROWS;
+        g.x = a.x; g.ldx = a.ldx; g.M = (int)M; g.xexp = a.xexp;
+        g.w = (const uint8_t*)Q.data; g.row_bytes = Q.ld; g.N = (int)N; g.K = (int)K;
+        g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
+        g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
+        g.wscale = scale->data; g.wscale_dtype = scale->dtype; g.wscale_stride = sst;
+        return hip_status(run_int8_smallm(g, st), "int8 small-M");
+    }
     a.wkind = WO_INT8;
     a.M = M; a.N = N; a.K = K;
     a.w = Q.data; a.ldw = Q.ld;

@@ -102,6 +102,22 @@ template <> struct SM<gguf::Q8_0> {
     }
 };
 
+// INT8 weight rows (INT8_ROWS): 256-value "blocks" of raw int8 codes with no stored scale; the
+// codes become exact fp16 (q + 1152 - 1152) and the per-row scale joins the epilogue.
+template <> struct SM<INT8_ROWS> {
+    static constexpr int QK = 256, TS = 256, UNIT = 32, SBLK = 1, KIND = 1;
+    static constexpr bool MIN = false;
+    __device__ static void block(const uint8_t*, int, float& d, float& dmin) {
+        d = 1.0f;
+        dmin = 0.0f;
+    }
+    __device__ static f16x8 get(const uint8_t* s, int o, int v0, f16& mv) {
+        mv = (f16)0.0f;
+        const uint32_t w0 = ld_u32(s, o + v0) ^ 0x80808080u, w1 = ld_u32(s, o + v0 + 4) ^ 0x80808080u;
+        return bytes_to_f16x8(w0, w1, (f16)-1152.0f);
+    }
+};
+
 template <int T> struct SMNib32 {
     static constexpr int QK = 32, TS = (T == gguf::Q4_1) ? 20 : 18, UNIT = 32, SBLK = 8, KIND = 0;
     static constexpr bool MIN = (T == gguf::Q4_1);

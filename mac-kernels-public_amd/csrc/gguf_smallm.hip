@@ -37,7 +37,8 @@ template <int T, int MT>
 __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
     const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K,
-    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy) {
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy,
+    const void* __restrict__ wscale, int wscale_dt, int64_t wscale_stride) {
     using F = SM<T>;
     constexpr int QK = F::QK, TS = F::TS, UNIT = F::UNIT, VPL = UNIT / 4, SBLK = F::SBLK;
     constexpr int SV = SBLK * QK;                    // values per stage
@@ -232,6 +233,7 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
 #pragma unroll
             for (int wv = 0; wv < SM_WAVES; ++wv) sum += red[wv][mt][i][sl];
             float v = xexp ? __builtin_ldexpf(sum, xexp[m]) : sum;
+            if (wscale) v *= load_rt(wscale, wscale_dt, n * wscale_stride);
             if (bias) v += load_rt(bias, bias_dt, n);
             store_rt(y, y_dt, (int64_t)m * ldy + n, v);
         }
@@ -243,7 +245,8 @@ hipError_t launch_t(const GgufSmallMArgs& a, hipStream_t st) {
     dim3 grid((unsigned)((a.N + 15) / 16)), block(SM_THREADS);
 #define QLIN_SM_LAUNCH(MTV)                                                                               \
     hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
-                       a.row_bytes, a.N, a.K, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy)
+                       a.row_bytes, a.N, a.K, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, a.wscale,         \
+                       a.wscale_dtype, a.wscale_stride)
     switch ((a.M + 15) / 16) {
         case 1: QLIN_SM_LAUNCH(1); break;
         case 2: QLIN_SM_LAUNCH(2); break;
@@ -265,6 +268,17 @@ bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes) {
         ok = (K % SV == 0) && (RSB % 4 == 0) && (row_bytes % 4 == 0);
     });
     return ok;
+}
+
+bool int8_smallm_supported(int64_t M, int64_t K, int64_t ldw, const void* w) {
+    constexpr int SV = SM<INT8_ROWS>::SBLK * SM<INT8_ROWS>::QK;
+    return M >= 1 && M <= 64 && K % SV == 0 && ldw % 4 == 0 && (uintptr_t)w % 4 == 0;
+}
+
+hipError_t run_int8_smallm(const GgufSmallMArgs& a, hipStream_t st) {
+    if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if (!int8_smallm_supported(a.M, a.K, a.row_bytes, a.w) || !a.wscale) return hipErrorInvalidValue;
+    return launch_t<INT8_ROWS>(a, st);
 }
 
 hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st) {

@@ -45,6 +45,9 @@ struct GgufSmallMArgs {
     void* y = nullptr;
     int y_dtype = DT_F16;
     int64_t ldy = 0;
+    const void* wscale = nullptr;   // INT8 rows: per-row weight scale (nullptr for GGUF)
+    int wscale_dtype = DT_F32;
+    int64_t wscale_stride = 1;
 };
 bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes);
 hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st);
@@ -72,6 +75,33 @@ int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_byte
 hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st);
 
 // ---- GGUF single-row linear (gguf_gemv.hip) ----
+// INT8 weight rows as a "format" of the small-M MFMA kernel (not a ggml type id): 32-value units
+// of raw int8 codes, the per-row scale applied in the epilogue.
+constexpr int INT8_ROWS = 1000;
+bool int8_smallm_supported(int64_t M, int64_t K, int64_t ldw, const void* w);
+hipError_t run_int8_smallm(const GgufSmallMArgs& a, hipStream_t st);
+
+// INT8 weight-only linear for one or two activation rows (int8_gemv.hip): normalized fp16 x, int8 w.
+struct Int8GemvArgs {
+    const f16* x = nullptr;
+    int64_t ldx = 0;
+    const int32_t* xexp = nullptr;
+    const int8_t* w = nullptr;
+    int64_t ldw = 0;
+    int64_t M = 0, N = 0, K = 0;
+    const void* scale = nullptr;
+    int scale_dtype = DT_F32;
+    int64_t scale_stride = 1;
+    const void* bias = nullptr;
+    int bias_dtype = DT_NONE;
+    void* y = nullptr;
+    int y_dtype = DT_F16;
+    int64_t ldy = 0;
+};
+bool int8_gemv_supported(const Int8GemvArgs& a);
+
+hipError_t run_int8_gemv(const Int8GemvArgs& a, hipStream_t st);
+
 struct GgufGemvArgs {
     int type = 0;
     const f16* x = nullptr;          // one fp16 activation row (16-byte aligned)
