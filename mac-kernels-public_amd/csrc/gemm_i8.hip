@@ -753,9 +753,130 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     }
 }
 
+// A8 linear for few activation rows (up to 32): weight streaming, the decode in the load stage.
+// One 512-thread workgroup per 16 weight rows; the K range is split across the 8 waves in stages
+// of 256 values.  In a stage, lane l decodes the 64 codes k = 64 (l / 16) .. + 63 of weight row
+// n0 + l % 16 (read with 16-byte loads: 32 bytes of nibbles, and for 6 bits 16 bytes of the 2-bit
+// plane; the four lanes of a row cover its stage contiguously) straight into the B operand of four
+// v_mfma_i32_16x16x64_i8 steps: step j takes the lane's values 16 j .. 16 j + 15, and the A
+// operand (the int8 activation rows, lane l holding row l % 16) is read in the same k order, so
+// both operands pair the same k values.  The next stage's codes, scales and activations are
+// requested before the current stage is decoded.  The int32 sums are exact; the waves' sums are
+// added through LDS and the epilogue is y = (f32(acc) * sx[m]) * s_channel[n] + bias[n].
+template <int BITS, bool CB, typename TSrel, int MT>
+__global__ __launch_bounds__(512) void a8_smallm_kernel(GemmI8Args p) {
+    constexpr int NH = BITS == 6 ? 1 : 0;   // 16-byte loads of the 2-bit plane per lane and stage
+    __shared__ int red[8][MT][4][64];
+    __shared__ float cb_s[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nl = lane & 15, g = lane >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    const int64_t n = min(n0 + nl, p.N - 1);   // rows past N re-read row N - 1 (never stored)
+    const int stages = (int)(p.K / 256);
+    const int st0 = (stages * wave) / 8, st1 = (stages * (wave + 1)) / 8;
+    const int last = max(st1 - 1, st0);
+    const uint8_t* qrow = p.q + n * p.ldq;
+    const uint8_t* hrow = qrow + p.K / 2;
+    const int gs = p.group_size;
+    if (CB && tid < 16) cb_s[tid] = p.codebook[tid];
+    const int8_t* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = p.xq + (int64_t)min(16 * mt + nl, (int)p.M - 1) * p.ldx;
+
+    struct Stage {
+        u32x4 nib[2];
+        u32x4 hi[NH > 0 ? NH : 1];
+        uint32_t sb[4];        // raw bits of the scales of the lane's 16-value runs
+        i32x4 x[MT][4];
+    };
+    auto fetch = [&](int st, Stage& S) {
+        st = min(st, last);
+        const int64_t k0 = (int64_t)st * 256 + 64 * g;
+        const u32x4* qp = reinterpret_cast<const u32x4*>(qrow + k0 / 2);
+        S.nib[0] = qp[0];
+        S.nib[1] = qp[1];
+        if constexpr (NH > 0) S.hi[0] = *reinterpret_cast<const u32x4*>(hrow + k0 / 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S.sb[r] = srel_bits<TSrel>(p.s_rel, n * p.ld_srel + (k0 + 16 * r) / gs);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S.x[mt][j] = *reinterpret_cast<const i32x4*>(xrow[mt] + k0 + 16 * j);
+    };
+
+    i32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = i32x4{0, 0, 0, 0};
+    if (CB) __syncthreads();
+    const float* cb = CB ? cb_s : nullptr;
+    Stage cur, nxt;
+    if (st0 < st1) {
+        fetch(st0, cur);
+        for (int st = st0; st < st1; ++st) {
+            fetch(st + 1, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t nib[8] = {cur.nib[0].x, cur.nib[0].y, cur.nib[0].z, cur.nib[0].w,
+                                     cur.nib[1].x, cur.nib[1].y, cur.nib[1].z, cur.nib[1].w};
+            uint32_t hi2[4] = {0u, 0u, 0u, 0u};
+            if constexpr (NH > 0) {
+                hi2[0] = cur.hi[0].x; hi2[1] = cur.hi[0].y; hi2[2] = cur.hi[0].z; hi2[3] = cur.hi[0].w;
+            }
+            uint32_t w8[16];
+            if (gs % 64 == 0) {
+                decode64<BITS, CB>(nib, hi2, srel_from_bits<TSrel>(cur.sb[0]), cb, 0, false, w8);
+            } else {
+#pragma unroll
+                for (int d = 0; d < 8; ++d)  // 8 codes with the scale of their 16-value run
+                    decode8_i8<BITS, CB>(nib[d], (hi2[d >> 1] >> (16 * (d & 1))) & 0xFFFFu,
+                                         srel_from_bits<TSrel>(cur.sb[d >> 1]), cb, w8[2 * d], w8[2 * d + 1]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const i32x4 bf = i32x4{(int)w8[4 * j], (int)w8[4 * j + 1], (int)w8[4 * j + 2], (int)w8[4 * j + 3]};
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.x[mt][j], bf, acc[mt], 0, 0, 0);
+            }
+            cur = nxt;
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][mt][i][lane] = acc[mt][i];
+    __syncthreads();
+    // 16 x 16 outputs per m-tile: lane l, register i of a wave holds row 4 (l / 16) + i, column l % 16
+    {
+#pragma clang fp contract(off)
+    for (int e = tid; e < MT * 256; e += 512) {
+        const int mt = e >> 8, rem = e & 255, i = rem >> 6, sl = rem & 63;
+        const int64_t m = 16 * mt + 4 * (sl >> 4) + i, nn = n0 + (sl & 15);
+        if (m >= p.M || nn >= p.N) continue;
+        int sum = 0;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) sum += red[w][mt][i][sl];
+        float val = (float)sum * p.sx[m];
+        val = val * p.s_ch[nn];
+        if (p.bias) val = val + load_rt(p.bias, p.bias_dtype, nn);
+        store_rt(p.y, p.y_dtype, m * p.ldy + nn, val);
+    }
+    }
+}
+
+inline bool a8_smallm_ok(const GemmI8Args& p) {
+    return p.M <= 32 && p.K % 256 == 0 && p.group_size % 16 == 0 && p.ldq % 16 == 0 && (uintptr_t)p.q % 16 == 0 &&
+           p.ldx % 16 == 0 && (uintptr_t)p.xq % 16 == 0;
+}
+
 template <int BITS, bool CB, typename TSrel>
 hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if (a8_smallm_ok(p)) {
+        const dim3 grid((unsigned)((p.N + 15) / 16)), block(512);
+        if (p.M <= 16) hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 1>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 2>), grid, block, 0, st, p);
+        return hipGetLastError();
+    }
     if (p.w8 && a8_decode_once(p.M, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
         (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0) {
         const int64_t segs = p.N * (p.K / 64);

@@ -1,5 +1,7 @@
-"""GPU parity of the weight-streaming paths for few activation rows (INT8 weight-only: the VALU
-GEMV for 1..4 rows, the small-M MFMA kernel up to 16 rows), against the oracle.
+"""GPU parity of the weight-streaming paths for few activation rows against the oracle: INT8
+weight-only (the VALU GEMV for one or two rows, the small-M MFMA kernel up to 16 rows) and
+W4A8 / W6A8 (the small-M int8 MFMA kernel with the decode in the load stage, up to 32 rows; its
+int32 GEMM and epilogue replayed exactly).
 
 Bar: relative Frobenius error < 1e-3 and max-abs error < 2e-2 of a float64 linear over the same
 dequantized operands (the rotated activation and q * scale).  Shapes cover the reference's
@@ -116,3 +118,64 @@ def test_int8_linear_small_m_extremes():
         den = max(float(np.abs(want).max()), 1e-30)
         assert np.isfinite(got).all(), name
         assert float(np.abs(got - want).max()) / den < 2e-3, f"{name}: max rel {float(np.abs(got - want).max()) / den}"
+
+
+# ------------------------------------------------------------------------------------------------
+# W4A8 / W6A8 for few rows: decode in the load stage, int8 MFMA, exact int32 sums
+# ------------------------------------------------------------------------------------------------
+
+def packed_weight(n, k, bits, gs, seed, srel_dtype, codebook):
+    """Random legal codes packed in the storage format, group scales inside the int8 grid."""
+    from qlin.quantize import FIXED_CODEBOOK, pack_codes
+    g = torch.Generator().manual_seed(seed)
+    lo_code = 0 if codebook else 1
+    codes = torch.randint(lo_code, (15 if bits == 4 else 63) + 1, (n, k), generator=g, dtype=torch.int32)
+    if codebook:
+        lo, hi = 60.0, 127.0     # codebook levels lie in [-1, 1]
+    else:
+        lo, hi = (8.0, 18.0) if bits == 4 else (2.0, 4.1)
+    s_rel = (lo + (hi - lo) * torch.rand(n, k // gs, generator=g)).to(srel_dtype)
+    s_ch = (torch.rand(n, generator=g) * 2e-4 + 1e-4).float()
+    cb = torch.from_numpy(FIXED_CODEBOOK.copy()) if codebook else None
+    return pack_codes(codes, bits), s_rel, s_ch, cb
+
+
+A8_SMALL = [
+    (4, 128, torch.float16, False, 1024),
+    (4, 16, torch.float8_e4m3fn, True, 3072),
+    (6, 64, torch.float16, False, 5120),
+    (6, 32, torch.bfloat16, False, 13824),
+    (4, 64, torch.float32, True, 13824),
+]
+
+
+@pytest.mark.parametrize("bits,gs,srdt,cb,k", A8_SMALL)
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 32])
+def test_w4a8_linear_small_m(bits, gs, srdt, cb, k, m):
+    n, g = 200, 128
+    q, s_rel, s_ch, book = packed_weight(n, k, bits, gs, seed=m + k + bits, srel_dtype=srdt, codebook=cb)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m))
+    x = torch.where(torch.rand(m, k, generator=torch.Generator().manual_seed(m + 1)) < 0.01, 20.0 * torch.sign(x), x)
+    x = x.half()
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(4)) * 0.1).float()
+    dev = lambda t: None if t is None else t.to(DEV)
+    Q = qlin()
+    y = Q.w4a8_int8_linear(x.to(DEV), dev(q), dev(s_rel), dev(s_ch), dev(book), None, dev(b), gs, g)
+    assert y.shape == (m, n)
+    if srdt == torch.float8_e4m3fn:
+        sr32 = O.srel_to_f32(s_rel.view(torch.uint8).numpy(), "e4m3")
+    else:
+        sr32 = s_rel.float().numpy()
+    w8 = O.w4a8_int8_grid(q.numpy(), sr32, None if book is None else book.numpy(), k, bits, gs)
+    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), g)
+    xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
+    # exact replay of the int32 GEMM and the epilogue ((f32(acc) * sx) * s_channel) + bias
+    acc = O.int8_gemm_i64(xq, w8)
+    replay = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * s_ch.numpy()[None, :]).astype(np.float32)
+    replay = (replay + b.numpy()[None, :]).astype(np.float32)
+    got = y.cpu().numpy()
+    bad = got.view(np.uint16) != replay.astype(np.float16).view(np.uint16)
+    assert not bad.any(), f"{int(bad.sum())} outputs differ from the exact replay, first at {np.argwhere(bad)[:3].tolist()}"
+    want = O.linear_ref(xq.astype(np.float32) * sx[:, None], w8.astype(np.float32) * s_ch.numpy()[:, None],
+                        b.numpy())
+    check(y, want, f"w{bits}a8 gs={gs} M={m} K={k}")
