@@ -144,6 +144,16 @@ qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, 
                             float lora_scale, qlin_tensor* y, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* qlin_lora_apply with the base linear's output read from `base` (f32 [M,N], unit column stride)
+ * instead of y: y[m,n] = dtype(base[m,n] + lora_scale * sum_r t[m,r] * lora_up[n,r]).  A caller with
+ * a 16-bit y runs the base linear into an fp32 buffer and passes it here, so the base and LoRA
+ * terms are added in fp32 and rounded once (the reference adds them in one fp32 sum and rounds
+ * once, docs/upstream/comfy-kitchen-mps-backend.md:54-56): a LoRA that cancels the weight gives
+ * exactly 0, and a base beyond the 16-bit range that the LoRA term brings back stays finite. */
+qlin_status qlin_lora_apply_base(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
+                                 float lora_scale, const qlin_tensor* base, qlin_tensor* y, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* Input gradient of the frozen INT8 linear: dx [M,K] = dy [M,N] @ W with W = rotate(q * scale) the
  * weight in the original basis (convrot_groupsize 0 = no rotation), i.e. dx = ((dy * scale) @ q) H.
  * dy * scale is normalized per row by a power of two and rounded once to fp16; the product runs on

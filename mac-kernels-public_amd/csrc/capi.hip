@@ -381,9 +381,11 @@ qlin_status qlin_w4a8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor
     return grad_input(DY, DX, grid, K, N, K, s_channel->data, DT_F32, sst, convrot_groupsize, ws, st);
 }
 
-qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
-                            float lora_scale, qlin_tensor* y, void* workspace, size_t workspace_bytes, void* stream) {
-    Mat X, D, U, Y;
+// y = dtype((base or y) + lora_scale * (x down^T) up^T); base, when given, is an fp32 [M, N] view.
+static qlin_status lora_impl(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
+                             float lora_scale, const qlin_tensor* base, qlin_tensor* y, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    Mat X, D, U, Y, B{};
     qlin_status s;
     if ((s = as_matrix(x, "x", X)) || (s = as_matrix(lora_down, "lora_down", D)) ||
         (s = as_matrix(lora_up, "lora_up", U)) || (s = as_matrix(y, "y", Y)))
@@ -396,6 +398,11 @@ qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, 
     if (U.cols != R) return fail(QLIN_EINVAL, "lora_up has rank %lld, lora_down %lld", (long long)U.cols, (long long)R);
     if (Y.rows != M || Y.cols != N) return fail(QLIN_EINVAL, "y must be [%lld, %lld]", (long long)M, (long long)N);
     if (R < 1) return fail(QLIN_EINVAL, "lora rank must be positive");
+    if (base) {
+        if ((s = as_matrix(base, "base", B))) return s;
+        if (B.dtype != QLIN_DT_F32 || B.rows != M || B.cols != N)
+            return fail(QLIN_EINVAL, "base must be a float32 [%lld, %lld]", (long long)M, (long long)N);
+    }
     const int S = lora_splits(M, K, R);
     const size_t need = align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)R * 4);
     if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
@@ -413,7 +420,20 @@ qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, 
     a.t = (float*)workspace;
     a.S = S;
     a.y = Y.data; a.y_dt = Y.dtype; a.ldy = Y.ld;
+    a.base = base ? (const float*)B.data : nullptr; a.ldb = base ? B.ld : 0;
     return hip_status(run_lora(a, (hipStream_t)stream), "lora");
+}
+
+qlin_status qlin_lora_apply(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
+                            float lora_scale, qlin_tensor* y, void* workspace, size_t workspace_bytes, void* stream) {
+    return lora_impl(x, lora_down, lora_up, lora_scale, nullptr, y, workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_lora_apply_base(const qlin_tensor* x, const qlin_tensor* lora_down, const qlin_tensor* lora_up,
+                                 float lora_scale, const qlin_tensor* base, qlin_tensor* y, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    if (!base || !base->data) return fail(QLIN_EINVAL, "base is missing");
+    return lora_impl(x, lora_down, lora_up, lora_scale, base, y, workspace, workspace_bytes, stream);
 }
 
 qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,

@@ -16,7 +16,8 @@
 //     would leave CUs idle; lora_sum_kernel adds the partials in split order.
 //   lora_up_kernel: 128 x 128 output tiles, 4 waves of 64 x 64, the rank in chunks of 64 staged
 //     in LDS; the tile is staged through LDS, then each output is read, increased by scale * acc
-//     in fp32 and rounded once to y's dtype, 8 outputs per thread.
+//     in fp32 and rounded once to y's dtype, 8 outputs per thread.  When the base linear left its
+//     output in an fp32 buffer (`base`), that is read instead of y, so a 16-bit y is rounded once.
 #include "qlin_internal.h"
 
 namespace qlin {
@@ -250,7 +251,8 @@ __global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
     // memory round trip overlaps the rank loop; 16-bit outputs only (f32 y takes the plain path)
     const bool vec = a.ldy % 8 == 0 && (uintptr_t)a.y % 16 == 0;
     constexpr int YC = UP_T * UP_T / 8 / 256;  // output chunks per thread
-    const bool ypre = vec && a.y_dt != DT_F32 && a.N % 8 == 0;
+    const bool ypre = vec && a.y_dt != DT_F32 && a.N % 8 == 0 && !a.base;
+    const bool bvec = a.base && a.ldb % 4 == 0 && (uintptr_t)a.base % 16 == 0;
     u32x4 yv[YC];
     if (ypre) {
 #pragma unroll
@@ -343,7 +345,14 @@ __global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
         if (m >= a.M || n >= a.N) continue;
         const int cnt = (int)min<int64_t>(8, a.N - n);
         float v[8];
-        if (ypre) {
+        if (a.base) {  // the base output in fp32: one rounding of base + side into y
+            if (bvec && cnt == 8) {
+                raw_to_f32(raw_load<DT_F32, true>(a.base, a.ldb, m, n, a.N), v);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = e < cnt ? a.base[m * a.ldb + n + e] : 0.0f;
+            }
+        } else if (ypre) {
             const u32x4 q = yv[pass * (YC / 2) + j];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {

@@ -192,6 +192,8 @@ struct LoraArgs {
     void* y = nullptr;           // [M, N] f32/f16/bf16, read and rewritten
     int y_dt = DT_F16;
     int64_t ldy = 0;
+    const float* base = nullptr; // optional fp32 [M, N] base output: y = dtype(base + side) instead
+    int64_t ldb = 0;
 };
 hipError_t run_lora(const LoraArgs& a, hipStream_t st);
 

@@ -52,8 +52,18 @@ def _lora_args(op, lora_down, lora_up, lora_scale, n, k):
     return lora_down, lora_up, scale
 
 
-def _apply_lora(op, lora, x2, y):
-    """y += scale * (x2 @ down^T) @ up^T on the GPU (qlin_lora_apply), after the base linear."""
+def _base_out(lora, y):
+    """Where the base linear writes: y itself, or with LoRA and a 16-bit y an fp32 buffer, so that
+    the base and LoRA terms are added in fp32 and rounded once into y (as the reference's single
+    fp32 sum, docs/upstream/comfy-kitchen-mps-backend.md:54-56)."""
+    if lora is None or y.dtype == torch.float32 or y.numel() == 0:
+        return y
+    return torch.empty(y.shape, dtype=torch.float32, device=y.device)
+
+
+def _apply_lora(op, lora, x2, y, base=None):
+    """y = dtype(base + scale * (x2 @ down^T) @ up^T) on the GPU after the base linear; `base` is the
+    fp32 buffer from _base_out, or y itself (updated in place)."""
     if lora is None or y.numel() == 0:
         return
     down, up, scale = lora
@@ -64,8 +74,14 @@ def _apply_lora(op, lora, x2, y):
         up = up.contiguous()
     r = down.shape[0]
     ws = _workspace(_lib.OP_LORA, x2.shape[0], up.shape[0], x2.shape[1], r, x2)
-    _lib.check(_lib.load().qlin_lora_apply(_lib.desc(x2), _lib.desc(down), _lib.desc(up), scale, _lib.desc(y),
-                                           ws.data_ptr(), ws.numel(), _lib.stream_of(x2.device)), op)
+    L = _lib.load()
+    if base is None or base is y:
+        st = L.qlin_lora_apply(_lib.desc(x2), _lib.desc(down), _lib.desc(up), scale, _lib.desc(y), ws.data_ptr(),
+                               ws.numel(), _lib.stream_of(x2.device))
+    else:
+        st = L.qlin_lora_apply_base(_lib.desc(x2), _lib.desc(down), _lib.desc(up), scale, _lib.desc(base),
+                                    _lib.desc(y), ws.data_ptr(), ws.numel(), _lib.stream_of(x2.device))
+    _lib.check(st, op)
 
 
 def _check_device(op, *tensors):
@@ -143,10 +159,11 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     b = _bias(bias, n)
     ws = _workspace(_lib.OP_INT8_LINEAR, x2.shape[0], n, k, g, x2)
     L = _lib.load()
-    st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(y), g,
+    yb = _base_out(lora, y)
+    st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(yb), g,
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
-    _apply_lora(op, lora, x2, y)
+    _apply_lora(op, lora, x2, y, yb)
     return y.reshape(shape)
 
 
@@ -212,11 +229,12 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     b = _bias(bias, n)
     ws = _workspace(_lib.OP_W4A8_LINEAR, x2.shape[0], n, k, bits, x2)
     L = _lib.load()
+    yb = _base_out(lora, y)
     st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
-                            _lib.desc(b), _lib.desc(y), bits, int(group_size), int(convrot_groupsize or 0),
+                            _lib.desc(b), _lib.desc(yb), bits, int(group_size), int(convrot_groupsize or 0),
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
-    _apply_lora(op, lora, x2, y)
+    _apply_lora(op, lora, x2, y, yb)
     return y.reshape(shape)
 
 
@@ -304,10 +322,11 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
         return y.reshape(oshape)
     b = _bias(bias, n)
     ws = _workspace(_lib.OP_GGUF_LINEAR, x2.shape[0], n, k, tid, x2)
-    st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(y),
+    yb = _base_out(lora, y)
+    st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(yb),
                                       ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
-    _apply_lora(op, lora, x2, y)
+    _apply_lora(op, lora, x2, y, yb)
     return y.reshape(oshape)
 
 

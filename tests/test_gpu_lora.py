@@ -174,3 +174,34 @@ def test_lora_arguments():
     # empty activations
     e = Q.int8_linear(torch.empty(0, k, device=DEV).half(), q, s, lora_down=down, lora_up=up)
     assert e.shape == (0, n)
+
+
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 4, 200])
+def test_lora_cancelling_the_weight_is_exactly_zero(odt, m):
+    """The base and LoRA terms are summed in fp32 and rounded once into a 16-bit y
+    (docs/upstream/comfy-kitchen-mps-backend.md:54-56): a LoRA equal to minus the weight gives
+    exactly 0 even where the base output itself is not representable in the output dtype, and a
+    base beyond the 16-bit range that the LoRA brings back stays finite.  All operands are small
+    integers, so both terms are exact in fp32 and only the order of rounding can matter."""
+    k, n = 64, 48
+    g = torch.Generator().manual_seed(m)
+    x = torch.randint(-7, 8, (m, k), generator=g).half()
+    q = torch.randint(-100, 101, (n, k), generator=g).to(torch.int8)
+    s = torch.ones(n)
+    down = torch.eye(k).to(torch.bfloat16)            # t = x exactly
+    Q = qlin()
+    base = x.double() @ q.double().T
+    assert (base.abs() > 2048).any(), "the case must hold outputs that round in 16 bits"
+    y = Q.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV), None, odt, lora_down=down.to(DEV),
+                      lora_up=(-q.float()).to(torch.bfloat16).to(DEV), lora_scale=1.0)
+    assert y.dtype == odt and torch.count_nonzero(y).item() == 0
+    # a base of about 1.9e5 (beyond fp16) brought back to x @ d^T by the LoRA term
+    xb = torch.full((m, k), 30.0).half()
+    d = torch.randint(-1, 2, (n, k), generator=g)
+    qb = torch.full((n, k), 100, dtype=torch.int8)
+    yb = Q.int8_linear(xb.to(DEV), qb.to(DEV), s.to(DEV), None, odt, lora_down=down.to(DEV),
+                       lora_up=(d.float() - 100.0).to(torch.bfloat16).to(DEV), lora_scale=1.0)
+    want = (xb.double() @ d.double().T).to(odt)
+    assert torch.isfinite(yb.float()).all()
+    assert torch.equal(yb.cpu(), want)
