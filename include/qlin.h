@@ -154,6 +154,16 @@ qlin_status qlin_lora_apply_base(const qlin_tensor* x, const qlin_tensor* lora_d
                                  float lora_scale, const qlin_tensor* base, qlin_tensor* y, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* Residual epilogue of a linear: y[m,n] = dtype(residual[m,n] + residual_scale[n] * base[m,n]) with
+ * base the linear's output (bias, and any LoRA term, already added) in an f32 [M,N] buffer; one
+ * rounding into y (f32/f16/bf16).  residual: f32/f16/bf16 [M,N]; residual_scale: optional (NULL = 1)
+ * f32/f16/bf16 [N].  All views need a unit column stride.
+ * Replaces the residual / residual_scale of comfy's linear_input_act on the INT8 kernel
+ * (tests/test_lora_sidepath.py:363-386; tests/test_krea_adapter.py:234-236), whose fused epilogue
+ * adds "bias and residual in eager's order" (docs/upstream/comfy-kitchen-mps-backend.md:52). */
+qlin_status qlin_residual_epilogue(const qlin_tensor* base, const qlin_tensor* residual,
+                                   const qlin_tensor* residual_scale, qlin_tensor* y, void* stream);
+
 /* Input gradient of the frozen INT8 linear: dx [M,K] = dy [M,N] @ W with W = rotate(q * scale) the
  * weight in the original basis (convrot_groupsize 0 = no rotation), i.e. dx = ((dy * scale) @ q) H.
  * dy * scale is normalized per row by a power of two and rounded once to fp16; the product runs on

@@ -436,6 +436,32 @@ qlin_status qlin_lora_apply_base(const qlin_tensor* x, const qlin_tensor* lora_d
     return lora_impl(x, lora_down, lora_up, lora_scale, base, y, workspace, workspace_bytes, stream);
 }
 
+qlin_status qlin_residual_epilogue(const qlin_tensor* base, const qlin_tensor* residual,
+                                   const qlin_tensor* residual_scale, qlin_tensor* y, void* stream) {
+    Mat B, R, Y;
+    qlin_status s;
+    if ((s = as_matrix(base, "base", B)) || (s = as_matrix(residual, "residual", R)) || (s = as_matrix(y, "y", Y)))
+        return s;
+    if (B.dtype != QLIN_DT_F32) return fail(QLIN_EUNSUPPORTED, "base must be float32");
+    if (!is_float(R.dtype) || !is_float(Y.dtype)) return fail(QLIN_EUNSUPPORTED, "residual and y must be f32/f16/bf16");
+    if (R.rows != B.rows || R.cols != B.cols || Y.rows != B.rows || Y.cols != B.cols)
+        return fail(QLIN_EINVAL, "base, residual and y must all be [%lld, %lld]", (long long)B.rows, (long long)B.cols);
+    ResidualArgs a;
+    if (residual_scale && residual_scale->data) {
+        int64_t rst;
+        if ((s = as_vector(residual_scale, "residual_scale", B.cols, true, rst))) return s;
+        if (!is_float(residual_scale->dtype)) return fail(QLIN_EUNSUPPORTED, "residual_scale must be f32/f16/bf16");
+        if (rst == 0 && B.cols > 1) return fail(QLIN_EUNSUPPORTED, "residual_scale must have N elements");
+        a.rscale = residual_scale->data;
+        a.rscale_dt = residual_scale->dtype;
+    }
+    a.base = (const float*)B.data; a.ldb = B.ld;
+    a.res = R.data; a.res_dt = R.dtype; a.ldr = R.ld;
+    a.y = Y.data; a.y_dt = Y.dtype; a.ldy = Y.ld;
+    a.M = B.rows; a.N = B.cols;
+    return hip_status(run_residual(a, (hipStream_t)stream), "residual epilogue");
+}
+
 qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
                              const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize, void* workspace,
                              size_t workspace_bytes, void* stream) {

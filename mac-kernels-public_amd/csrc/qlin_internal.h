@@ -197,6 +197,22 @@ struct LoraArgs {
 };
 hipError_t run_lora(const LoraArgs& a, hipStream_t st);
 
+// Residual epilogue (epilogue.hip): y = dtype(res + rscale[n] * base), base fp32 [M, N].
+struct ResidualArgs {
+    const float* base = nullptr;
+    int64_t ldb = 0;
+    const void* res = nullptr;
+    int res_dt = DT_F32;
+    int64_t ldr = 0;
+    const void* rscale = nullptr;   // [N] or nullptr (1)
+    int rscale_dt = DT_F32;
+    void* y = nullptr;
+    int y_dt = DT_F16;
+    int64_t ldy = 0;
+    int64_t M = 0, N = 0;
+};
+hipError_t run_residual(const ResidualArgs& a, hipStream_t st);
+
 // ---- frozen-weight input gradient (backward.hip) ----
 struct BwdGemmArgs {
     const f16* a = nullptr;      // [M][lda] normalized dy * s, zero past N (lda = N rounded up to 128)

@@ -8,6 +8,7 @@ decoded inside the kernels).  Everything runs in libqlin.so (HIP, C ABI in inclu
 from .autograd import int8_linear_grad_input, int8_linear_trainable, w4a8_linear_grad_input, w4a8_linear_trainable
 from .exceptions import NoCapableBackendError, QlinError
 from .gguf import GGUF_TYPES, gguf_type_id
+from .layouts import AsymW4A8Int8Layout, QuantizedTensor, TensorWiseINT8Layout
 from .loader import PackedLinear, gguf_header, load_gguf, load_safetensors, quantized_linears, safetensors_header
 from .ops import (
     dequantize_gguf,
@@ -27,5 +28,6 @@ __all__ = [
     "dequantize_int8_convrot_weight", "dequantize_w4a8_int8_weight", "gguf_linear", "int8_linear",
     "quantize_int8_rowwise", "w4a8_int8_grid", "w4a8_int8_linear", "registry", "PackedLinear", "gguf_header",
     "load_gguf", "load_safetensors", "quantized_linears", "safetensors_header", "int8_linear_grad_input",
-    "int8_linear_trainable", "w4a8_linear_grad_input", "w4a8_linear_trainable",
+    "int8_linear_trainable", "w4a8_linear_grad_input", "w4a8_linear_trainable", "AsymW4A8Int8Layout",
+    "QuantizedTensor", "TensorWiseINT8Layout",
 ]

@@ -29,6 +29,7 @@ EXPORTS = (
     "qlin_version", "qlin_status_string", "qlin_last_error", "qlin_workspace_size", "qlin_query",
     "qlin_int8_linear", "qlin_w4a8_linear", "qlin_gguf_linear", "qlin_gguf_linear_noalloc", "qlin_dequantize_gguf",
     "qlin_dequantize_int8", "qlin_dequantize_w4a8", "qlin_quantize_act_int8", "qlin_lora_apply", "qlin_lora_apply_base",
+    "qlin_residual_epilogue",
     "qlin_int8_linear_grad_input", "qlin_w4a8_linear_grad_input",
 )
 
@@ -73,6 +74,7 @@ def load():
         "qlin_quantize_act_int8": (I, [T, T, T, I, T, P]),
         "qlin_lora_apply": (I, [T, T, T, ctypes.c_float, T, P, SZ, P]),
         "qlin_lora_apply_base": (I, [T, T, T, ctypes.c_float, T, T, P, SZ, P]),
+        "qlin_residual_epilogue": (I, [T, T, T, T, P]),
         "qlin_int8_linear_grad_input": (I, [T, T, T, I, T, P, SZ, P]),
         "qlin_w4a8_linear_grad_input": (I, [T, T, T, T, T, T, I, I, I, P, SZ, P]),
     }

@@ -52,13 +52,48 @@ def _lora_args(op, lora_down, lora_up, lora_scale, n, k):
     return lora_down, lora_up, scale
 
 
-def _base_out(lora, y):
-    """Where the base linear writes: y itself, or with LoRA and a 16-bit y an fp32 buffer, so that
-    the base and LoRA terms are added in fp32 and rounded once into y (as the reference's single
-    fp32 sum, docs/upstream/comfy-kitchen-mps-backend.md:54-56)."""
-    if lora is None or y.dtype == torch.float32 or y.numel() == 0:
+def _base_out(lora, y, residual=None):
+    """Where the base linear writes: y itself, or an fp32 buffer when a residual follows or LoRA
+    meets a 16-bit y, so that the base, LoRA and residual terms are added in fp32 and rounded once
+    into y (as the reference's single fp32 sum, docs/upstream/comfy-kitchen-mps-backend.md:52-56)."""
+    if y.numel() == 0 or (residual is None and (lora is None or y.dtype == torch.float32)):
         return y
     return torch.empty(y.shape, dtype=torch.float32, device=y.device)
+
+
+def _residual_args(op, residual, residual_scale, shape, n):
+    """Validated residual [.., N] (flattened to [M, N]) and residual_scale [N] (or None)."""
+    if residual is None:
+        if residual_scale is not None:
+            raise ValueError(f"{op}: residual_scale given without residual")
+        return None
+    if tuple(residual.shape) != tuple(shape):
+        raise ValueError(f"{op}: residual has shape {tuple(residual.shape)}, the output is {tuple(shape)}")
+    for t in (residual, residual_scale):
+        if t is not None and t.dtype not in _FLOAT:
+            raise NoCapableBackendError(op, {"hip": f"residual dtype {t.dtype} unsupported"})
+    r = residual.reshape(-1, n)
+    if r.shape[0] > 1 and (r.stride(1) != 1 or r.stride(0) < n):
+        r = r.contiguous()
+    rs = None
+    if residual_scale is not None:
+        if residual_scale.numel() != n:
+            raise ValueError(f"{op}: residual_scale has {residual_scale.numel()} elements, expected {n}")
+        rs = residual_scale.reshape(n).contiguous()
+    return r, rs
+
+
+def _finish(op, lora, res, x2, y, yb):
+    """After the base linear wrote yb: the LoRA term, then the residual epilogue, into y."""
+    if res is None:
+        _apply_lora(op, lora, x2, y, yb)
+        return
+    _apply_lora(op, lora, x2, yb, yb)  # in place on the fp32 base
+    r, rs = res
+    _check_device(op, r, rs)
+    st = _lib.load().qlin_residual_epilogue(_lib.desc(yb), _lib.desc(r), _lib.desc(rs), _lib.desc(y),
+                                            _lib.stream_of(y.device))
+    _lib.check(st, op)
 
 
 def _apply_lora(op, lora, x2, y, base=None):
@@ -138,9 +173,10 @@ def _bias(bias, n):
 # ------------------------------------------------------------------------------------------------
 
 def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, convrot_groupsize=256,
-                lora_down=None, lora_up=None, lora_scale=None):
+                lora_down=None, lora_up=None, lora_scale=None, residual=None, residual_scale=None):
     """y = rot(x) @ (qdata * scale)^T + bias.  qdata int8 [N, K] (rotated basis when convrot),
-    scale [N] / [N, 1] / scalar (fp32 or fp16).  fp16 MFMA, fp32 accumulate."""
+    scale [N] / [N, 1] / scalar (fp32 or fp16).  fp16 MFMA, fp32 accumulate.  With `residual`
+    ([.., N]): y = residual + residual_scale * (linear + bias + LoRA), one rounding."""
     op = "int8_linear"
     _disabled(op)
     _check_device(op, x, qdata, scale, bias)
@@ -152,6 +188,7 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     lora = _lora_args(op, lora_down, lora_up, lora_scale, n, k)
     x2, lead = _as_2d(x, k)
     y, shape = _out(x2, lead, n, out_dtype, x)
+    res = _residual_args(op, residual, residual_scale, shape, n)
     if x2.shape[0] == 0 or n == 0:
         return y.reshape(shape)
     g = int(convrot_groupsize) if convrot else 0
@@ -159,11 +196,11 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     b = _bias(bias, n)
     ws = _workspace(_lib.OP_INT8_LINEAR, x2.shape[0], n, k, g, x2)
     L = _lib.load()
-    yb = _base_out(lora, y)
+    yb = _base_out(lora, y, res)
     st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(yb), g,
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
-    _apply_lora(op, lora, x2, y, yb)
+    _finish(op, lora, res, x2, y, yb)
     return y.reshape(shape)
 
 
@@ -206,9 +243,11 @@ def _bits_of(qdata, s_rel, group_size):
 
 
 def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None, bias=None, group_size=16,
-                     convrot_groupsize=256, out_dtype=None, *, lora_down=None, lora_up=None, lora_scale=None):
+                     convrot_groupsize=256, out_dtype=None, *, lora_down=None, lora_up=None, lora_scale=None,
+                     residual=None, residual_scale=None):
     """A8 linear: per-token int8 activations (quantize_int8_rowwise of the rotated x), int8 MFMA
-    against the int8 weight grid, y = acc * sx[m] * s_channel[n] + bias."""
+    against the int8 weight grid, y = acc * sx[m] * s_channel[n] + bias (then LoRA and residual as
+    for int8_linear)."""
     op = "w4a8_int8_linear"
     _disabled(op)
     if correction is not None:
@@ -221,6 +260,7 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     lora = _lora_args(op, lora_down, lora_up, lora_scale, n, k)
     x2, lead = _as_2d(x, k)
     y, shape = _out(x2, lead, n, out_dtype, x)
+    res = _residual_args(op, residual, residual_scale, shape, n)
     if x2.shape[0] == 0 or n == 0:
         return y.reshape(shape)
     q = qdata if qdata.dtype in (torch.int8, torch.uint8) else qdata.view(torch.int8)
@@ -229,12 +269,12 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     b = _bias(bias, n)
     ws = _workspace(_lib.OP_W4A8_LINEAR, x2.shape[0], n, k, bits, x2)
     L = _lib.load()
-    yb = _base_out(lora, y)
+    yb = _base_out(lora, y, res)
     st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
                             _lib.desc(b), _lib.desc(yb), bits, int(group_size), int(convrot_groupsize or 0),
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
-    _apply_lora(op, lora, x2, y, yb)
+    _finish(op, lora, res, x2, y, yb)
     return y.reshape(shape)
 
 
@@ -298,9 +338,11 @@ def quantize_int8_rowwise(x, convrot_groupsize=0, return_rotated=False):
 # GGUF
 # ------------------------------------------------------------------------------------------------
 
-def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=None, lora_up=None, lora_scale=None):
+def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=None, lora_up=None, lora_scale=None,
+                *, residual=None, residual_scale=None):
     """y = x @ W^T + bias with W [N, K] decoded from GGUF blocks of `qtype` (ggml type id or name).
-    `weight` is the tensor's raw bytes (uint8, [N, K/qk*ts] or flat)."""
+    `weight` is the tensor's raw bytes (uint8, [N, K/qk*ts] or flat).  LoRA and residual as for
+    int8_linear."""
     op = "gguf_linear"
     _disabled(op)
     _check_device(op, x, weight, bias)
@@ -318,15 +360,16 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
         raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
     x2, lead = _as_2d(x, k)
     y, oshape = _out(x2, lead, n, out_dtype, x)
+    res = _residual_args(op, residual, residual_scale, oshape, n)
     if x2.shape[0] == 0 or n == 0:
         return y.reshape(oshape)
     b = _bias(bias, n)
     ws = _workspace(_lib.OP_GGUF_LINEAR, x2.shape[0], n, k, tid, x2)
-    yb = _base_out(lora, y)
+    yb = _base_out(lora, y, res)
     st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(yb),
                                       ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
     _lib.check(st, op)
-    _apply_lora(op, lora, x2, y, yb)
+    _finish(op, lora, res, x2, y, yb)
     return y.reshape(oshape)
 
 
