@@ -7,6 +7,8 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
+import threading
 
 import torch
 
@@ -57,7 +59,7 @@ def load():
                         "(the HIP library is the only implementation; there is no fallback)")
     L = ctypes.CDLL(LIB_PATH)
     P, I, I64, SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
-    T = ctypes.POINTER(QlinTensor)
+    T = ctypes.c_void_p  # the address of a qlin_tensor (see desc)
     sigs = {
         "qlin_version": (I, []),
         "qlin_status_string": (ctypes.c_char_p, [I]),
@@ -86,26 +88,70 @@ def load():
     return L
 
 
+# qlin_tensor {void* data; int32 dtype; int32 ndim; int64 shape[4]; int64 stride[4]}: 80 bytes.
+_DESC = struct.Struct("=Qii8q")
+assert _DESC.size == ctypes.sizeof(QlinTensor)
+_DESC_SLOTS = 32
+_tls = threading.local()
+
+
 def desc(t: torch.Tensor | None, dtype_override: int | None = None):
-    """qlin_tensor descriptor of a torch tensor (None -> NULL pointer)."""
+    """Address of a qlin_tensor descriptor of a torch tensor (None -> NULL).  Descriptors are
+    packed into a per-thread ring of 32 slots, so one is valid until 32 more have been made on the
+    same thread: build them right before the call that reads them."""
     if t is None:
         return None
-    if t.dim() > 4:
+    nd = t.dim()
+    if nd > 4:
         raise ValueError("at most 4 dims")
-    d = QlinTensor()
-    d.data = t.data_ptr()
-    d.dtype = dtype_override if dtype_override is not None else _TORCH_DT[t.dtype]
-    d.ndim = max(t.dim(), 1)
-    if t.dim() == 0:
-        d.shape[0], d.stride[0] = 1, 1
-    for i in range(t.dim()):
-        d.shape[i] = t.shape[i]
-        d.stride[i] = t.stride(i)
-    return ctypes.byref(d)
+    ring = _tls.__dict__.get("ring")
+    if ring is None:
+        buf = ctypes.create_string_buffer(_DESC.size * _DESC_SLOTS)
+        ring = _tls.ring = [buf, ctypes.addressof(buf), 0]
+    i = ring[2]
+    ring[2] = (i + 1) % _DESC_SLOTS
+    dt = dtype_override if dtype_override is not None else _TORCH_DT[t.dtype]
+    sh, st = t.shape, t.stride()
+    if nd == 2:
+        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, 2, sh[0], sh[1], 0, 0, st[0], st[1], 0, 0)
+    elif nd == 1:
+        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, 1, sh[0], 0, 0, 0, st[0], 0, 0, 0)
+    elif nd == 0:
+        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, 1, 1, 0, 0, 0, 1, 0, 0, 0)
+    else:
+        pad = (0,) * (4 - nd)
+        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, nd, *sh, *pad, *st, *pad)
+    return ring[1] + _DESC.size * i
 
 
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of the current stream of `device`."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
+
+
+_ws_cache: dict = {}
+
+
+def workspace(nbytes: int, device: torch.device, stream: int) -> torch.Tensor:
+    """A device byte buffer of at least `nbytes` for one call on `stream`.  Outside graph capture
+    one buffer per (device, stream) is kept and grown, so eager calls do not allocate: calls on one
+    stream run in order, so they can share it.  During capture every call gets its own tensor from
+    the graph's pool."""
+    nbytes = max(int(nbytes), 1)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index, stream)
+    w = _ws_cache.get(key)
+    if w is None or w.numel() < nbytes:
+        w = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _ws_cache[key] = w
+    return w
+
+
+def release_workspaces() -> None:
+    """Drop the cached per-stream workspaces (their memory returns to torch's allocator)."""
+    _ws_cache.clear()
 
 
 def check(status: int, op: str):

@@ -157,7 +157,7 @@ def _out(x2, lead, n, out_dtype, x):
 
 def _workspace(op, m, n, k, param, x2):
     nbytes = _lib.load().qlin_workspace_size(op, m, n, k, param, _lib._TORCH_DT[x2.dtype])
-    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x2.device)
+    return _lib.workspace(nbytes, x2.device, _lib.stream_of(x2.device))
 
 
 def _bias(bias, n):
