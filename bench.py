@@ -221,6 +221,7 @@ def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
             for m in ms:
                 us = time_eager(lambda m=m: qlin.gguf_linear(xs[m], ws[0], tid[t], (n, k)))
                 detail[f"{t}/M{m}"]["eager_us"] = round(us, 2)
+                detail[f"{t}/M{m}"]["eager_host_overhead_us"] = round(us - detail[f"{t}/M{m}"]["us"], 2)
                 log(f"[gguf] {t:7s} M={m:3d}: eager {us:7.2f} us per call")
         del ws
     return {
@@ -454,7 +455,8 @@ def run_configs(names, steps, warmup, pool):
                         "frac": round(tfl / FP16_PEAK_TFLOPS, 4), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
             roof.update({"kernel": CONFIG_KERNELS[name], "flops_per_call": flops, "bytes_per_call": nbytes,
                          "traffic": None})
-            rec = {"us_per_call": round(us, 2), "eager_us_per_call": round(eager, 2), "TFLOPs": round(tfl, 2),
+            rec = {"us_per_call": round(us, 2), "eager_us_per_call": round(eager, 2),
+                   "eager_host_overhead_us": round(eager - us, 2), "TFLOPs": round(tfl, 2),
                    "GBps": round(gbs, 1), "pool_copies": copies, "roofline": roof, "cpu_baseline": cpu}
         elif cfg["kind"] == "a8":
             m, k, n, bits, gs, g = cfg["m"], cfg["k"], cfg["n"], cfg["bits"], cfg["gs"], cfg["g"]

@@ -43,6 +43,21 @@ __device__ __forceinline__ float srel_at(const void* s, int64_t i) {
     else return load_f((const TSrel*)s + i);
 }
 
+// The grid value clamp(rne(v), -127, 127) of an fp32 v, as the low byte of the result: adding
+// 1.5 * 2^23 rounds v to an integer in the low mantissa bits (ties to even; |v| < 2^22), the float
+// clamp keeps it within +-127 (any larger v, infinities included, lands on a bound), and the low
+// byte of M + w8 is w8 in two's complement (M's low byte is 0).  tests/grid_decode_check.c checks
+// this against clamp(rne(fp32(level * s))) for every code and every 16-bit scale.
+constexpr float GRID_MAGIC = 12582912.0f;
+__device__ __forceinline__ uint32_t grid_bits(float v) {
+#pragma clang fp contract(off)
+    return __float_as_uint(__builtin_amdgcn_fmed3f(v + GRID_MAGIC, GRID_MAGIC - 127.0f, GRID_MAGIC + 127.0f));
+}
+__device__ __forceinline__ uint32_t grid_byte(float level, float s) {
+#pragma clang fp contract(off)
+    return grid_bits(level * s) & 0xFFu;  // the product rounded to fp32 first
+}
+
 // Decode 8 codes packed as nibbles in w (code i = nibble i) [+ 2-bit high parts in hi8, bits
 // 2i..2i+1] to the int8 grid; returns two dwords of int8.
 template <int BITS, bool CB>
@@ -56,9 +71,7 @@ __device__ __forceinline__ void decode8_i8(uint32_t w, uint32_t hi8, float s, co
         float level;
         if constexpr (CB) level = cb[code];
         else level = (float)(code - (1 << (BITS - 1)));
-        float t = __builtin_rintf(level * s);
-        t = fminf(fmaxf(t, -127.0f), 127.0f);
-        r[i] = (int8_t)(int)t;
+        r[i] = (int8_t)grid_byte(level, s);
     }
     o0 = (uint32_t)(uint8_t)r[0] | ((uint32_t)(uint8_t)r[1] << 8) | ((uint32_t)(uint8_t)r[2] << 16) |
          ((uint32_t)(uint8_t)r[3] << 24);
@@ -234,11 +247,6 @@ __device__ __forceinline__ uint32_t lut16(uint32_t idx, uint32_t t0, uint32_t t1
     return (hi & mask) | (lo & ~mask);
 }
 
-__device__ __forceinline__ uint32_t grid_byte(float level, float s) {
-    const float t = __builtin_amdgcn_fmed3f(__builtin_rintf(level * s), -127.0f, 127.0f);
-    return (uint32_t)((int)t & 0xFF);
-}
-
 // 64 codes of one weight row (nibble dwords nib[0..7], 2-bit plane hi2[0..3] for 6-bit) -> 64
 // int8 grid values in out[0..15].  4-bit: a 16-entry table per scale.  When the thread pair that
 // shares the row also shares the scale (`pair`, wave-uniform), each builds half of it (entries
@@ -278,6 +286,9 @@ __device__ __forceinline__ void decode64(const uint32_t* nib, const uint32_t* hi
         }
     } else {
         (void)h;
+        // (c - 32) * s as fma(c, s, -32 s): the exact product rounded once, the reference's fp32
+        // product; s clamped to +-2^20 (every clamped grid value is unchanged, -32 s stays finite)
+        const float sc = __builtin_amdgcn_fmed3f(s, -0x1p20f, 0x1p20f), off = -32.0f * sc;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
             const uint32_t w = nib[d];
@@ -285,8 +296,8 @@ __device__ __forceinline__ void decode64(const uint32_t* nib, const uint32_t* hi
             uint32_t o0 = 0, o1 = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int code = (int)(((w >> (4 * i)) & 0xFu) | (((h16 >> (2 * i)) & 3u) << 4));
-                const uint32_t bb = grid_byte((float)(code - 32), s);
+                const uint32_t code = ((w >> (4 * i)) & 0xFu) | (((h16 >> (2 * i)) & 3u) << 4);
+                const uint32_t bb = grid_bits(__builtin_fmaf((float)code, sc, off)) & 0xFFu;
                 if (i < 4) o0 |= bb << (8 * i);
                 else o1 |= bb << (8 * (i - 4));
             }
