@@ -618,20 +618,26 @@ __device__ __forceinline__ void wait_stages(int nd) {
 }
 
 // INT8 weight-only GEMM for grids too small for 256 x 256 tiles (a few hundred activation rows):
-// BMT x BNT output tiles of 32 x 32 MFMA sub-tiles, one sub-tile per wave, and when the tile has
-// at most four sub-tiles the two 32-value halves of every 64-value k-block go to two waves (their
-// sums are added through LDS at the end, always in the same order).  Both operands arrive by LDS
-// DMA through a ring of STAGES k-tiles of KT values.  One DMA instruction moves whole runs of
-// KT bytes (weights) or 2 KT bytes (activations) of a few rows, so each weight row is read in long
-// contiguous runs rather than 64-byte pieces of thousands of rows at once.
+// BMT x BNT output tiles of 32 x 32 MFMA sub-tiles.  Each wave owns one 32-column sub-tile for all
+// BMT rows on one of KH parts of every k-tile, so each weight chunk is converted to fp16 once per
+// workgroup and feeds BMT / 32 MFMAs; the KH partial sums are added through LDS at the end, always
+// in the same order.  Both operands arrive by LDS DMA through a ring of STAGES k-tiles of KT
+// values.  One DMA instruction moves whole runs of KT bytes (weights) or 2 KT bytes (activations)
+// of a few rows, so each weight row is read in long contiguous runs rather than 64-byte pieces of
+// thousands of rows at once.
 // LDS rows hold CH = row bytes / 16 chunks; logical chunk c of row r sits at c ^ sw(r) with
 // sw(r) = (r / (16 / CH)) % CH for CH < 16 and r % 16 otherwise, so the 16 rows one 16-lane group
-// reads at one logical chunk land in 16 distinct 16-byte bank groups.  k order inside a 64-value
-// block b: MFMA step 2p + e of lane half h takes k = 64 b + 32 p + 16 h + 8 e .. + 7 in both
-// operands, so one 16-byte weight read (logical chunk 4 b + 2 p + h) feeds two steps.
-template <int BMT, int BNT>
+// reads at one logical chunk land in 16 distinct 16-byte bank groups.  k order: 32-value step s of
+// a k-tile, MFMA e of lane half h takes k = 32 s + 16 h + 8 e .. + 7 in both operands, so one
+// 16-byte weight read (logical chunk 2 s + h) feeds both MFMAs of the step; the activation chunk
+// is 4 s + 2 h + e.
+template <int BMT, int BNT, int KT>
+constexpr int wo_dmas_kparts() {
+    return (8 / (BNT / 32)) < (KT / 32) ? (8 / (BNT / 32)) : (KT / 32);
+}
+template <int BMT, int BNT, int KT>
 constexpr int wo_dmas_waves() {
-    return (BMT / 32) * (BNT / 32) * ((BMT / 32) * (BNT / 32) <= 4 ? 2 : 1);
+    return (BNT / 32) * wo_dmas_kparts<BMT, BNT, KT>();
 }
 
 template <int CH>
@@ -641,22 +647,23 @@ __device__ __forceinline__ int lds_swz(int r) {
 }
 
 template <int BMT, int BNT, int KT, int STAGES>
-__global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT>())) void gemm_wo_dmas_kernel(GemmF16Args a) {
-    constexpr int TM = BMT / 32, TILES = TM * (BNT / 32);
-    constexpr int KH = TILES <= 4 ? 2 : 1;
-    constexpr int NW = TILES * KH;
+__global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_dmas_kernel(GemmF16Args a) {
+    constexpr int TM = BMT / 32, TN = BNT / 32;
+    constexpr int KH = wo_dmas_kparts<BMT, BNT, KT>();
+    constexpr int NW = TN * KH;
+    constexpr int SPW = KT / 32 / KH;                          // 32-value k steps per wave per k-tile
     constexpr int CA = KT / 8, CB = KT / 16;                  // 16-byte chunks per LDS row
     constexpr int ASZ = BMT * KT * 2, BSZ = BNT * KT;          // bytes per stage
     constexpr int WA = BMT * CA / 64, WB = BNT * CB / 64;     // wave-wide DMA instructions per stage
     constexpr int NA = (WA + NW - 1) / NW, NB = (WB + NW - 1) / NW;
     static_assert(BMT % 32 == 0 && BNT % 32 == 0 && NW <= 8 && STAGES >= 3, "tile shape");
-    static_assert(KT % 64 == 0 && (BMT * CA) % 64 == 0 && (BNT * CB) % 64 == 0, "whole DMA instructions");
+    static_assert(KT % 64 == 0 && (KT / 32) % KH == 0, "k parts");
+    static_assert((BMT * CA) % 64 == 0 && (BNT * CB) % 64 == 0, "whole DMA instructions");
     static_assert(NA + NB <= 8, "DMAs per wave");
     __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ)];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, h = lane >> 5;
-    const int t = wave % TILES, kh = wave / TILES;
-    const int tm = t % TM, tn = t / TM;
+    const int tn = wave % TN, kh = wave / TN;
     int mt, nt;
     xcd_tile_f16(blockIdx.x, (int)gridDim.x, (int)((a.M + BMT - 1) / BMT), (int)((a.N + BNT - 1) / BNT), mt, nt);
     const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
@@ -693,32 +700,46 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT>())) void gemm_wo_dmas
             if (i < nb) lds_dma16(bsrc[i] + k0, st + ASZ + 16 * 64 * (wave + NW * i));
     };
 
-    f32x16 acc;
+    f32x16 acc[TM];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-    const int ra = 32 * tm + r32, rb = 32 * tn + r32;
-    const int swa = lds_swz<CA>(ra), swb = lds_swz<CB>(rb);
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    const int rb = 32 * tn + r32, swb = lds_swz<CB>(rb);
+    int swa[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) swa[i] = lds_swz<CA>(32 * i + r32);
     auto mfmas = [&](int buf) {
-        const uint8_t* as = smem + buf * (ASZ + BSZ) + ra * (KT * 2);
+        const uint8_t* as = smem + buf * (ASZ + BSZ) + r32 * (KT * 2);
         const uint8_t* bs = smem + buf * (ASZ + BSZ) + ASZ + rb * KT;
+        // every fragment of the k-tile is read before the first MFMA
+        u32x4 q[SPW];
+        f16x8 av[SPW][TM][2];
 #pragma unroll
-        for (int b = 0; b < KT / 64; ++b)
+        for (int j = 0; j < SPW; ++j) {
+            const int s = kh * SPW + j;
+            q[j] = *reinterpret_cast<const u32x4*>(bs + 16 * ((2 * s + h) ^ swb));
 #pragma unroll
-            for (int pp = 0; pp < 2 / KH; ++pp) {
-                const int p = KH == 2 ? kh : pp;
-                const u32x4 q = *reinterpret_cast<const u32x4*>(bs + 16 * ((4 * b + 2 * p + h) ^ swb));
-                const f16x8 a0 = *reinterpret_cast<const f16x8*>(as + 16 * ((8 * b + 4 * p + 2 * h) ^ swa));
-                const f16x8 a1 = *reinterpret_cast<const f16x8*>(as + 16 * ((8 * b + 4 * p + 2 * h + 1) ^ swa));
-                uint32_t o[8];
-                i8x4_to_f16(q.x, o[0], o[1]);
-                i8x4_to_f16(q.y, o[2], o[3]);
-                i8x4_to_f16(q.z, o[4], o[5]);
-                i8x4_to_f16(q.w, o[6], o[7]);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]}),
-                                                             acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, __builtin_bit_cast(f16x8, u32x4{o[4], o[5], o[6], o[7]}),
-                                                             acc, 0, 0, 0);
-            }
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    av[j][i][e] = *reinterpret_cast<const f16x8*>(as + 32 * i * (KT * 2) +
+                                                                  16 * ((4 * s + 2 * h + e) ^ swa[i]));
+        }
+#pragma unroll
+        for (int j = 0; j < SPW; ++j) {
+            uint32_t o[8];
+            i8x4_to_f16(q[j].x, o[0], o[1]);
+            i8x4_to_f16(q[j].y, o[2], o[3]);
+            i8x4_to_f16(q[j].z, o[4], o[5]);
+            i8x4_to_f16(q[j].w, o[6], o[7]);
+            const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+            const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{o[4], o[5], o[6], o[7]});
+#pragma unroll
+            for (int i = 0; i < TM; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[j][i][0], b0, acc[i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[j][i][1], b1, acc[i], 0, 0, 0);
+        }
     };
 
     // Barrier without a memory fence: each wave's wait covers its own DMAs, the loop writes LDS only
@@ -739,23 +760,24 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT>())) void gemm_wo_dmas
     wait_vmcnt<0>();
     __syncthreads();
 
-    // Epilogue: the sub-tiles go to LDS as fp32 (row stride BNT + 4 words); with two k halves the
-    // second half is added to the first.  Lane l, register r of a 32 x 32 sub-tile holds row
-    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Then y = ldexp(acc, xexp[m]) * scale[n] + bias[n],
-    // 8 consecutive outputs per thread with 16-byte stores.
+    // Epilogue: the sub-tiles go to LDS as fp32 (row stride BNT + 4 words), k part 0 first, then
+    // parts 1 .. KH - 1 added in order.  Lane l, register r of a 32 x 32 sub-tile holds row
+    // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Then y = ldexp(acc, xexp[m]) * scale[n] +
+    // bias[n], 8 consecutive outputs per thread with 16-byte stores.
     constexpr int ORW = BNT + 4;
     static_assert(BMT * ORW * 4 <= (int)sizeof(smem), "output staging must fit");
     float* ot = reinterpret_cast<float*>(smem);
-    float* op = ot + (32 * tm + 4 * h) * ORW + 32 * tn + r32;
-    if (kh == 0) {
+    float* op = ot + 4 * h * ORW + 32 * tn + r32;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) op[(8 * (r / 4) + r % 4) * ORW] = acc[r];
-    }
-    __syncthreads();
-    if constexpr (KH == 2) {
-        if (kh == 1) {
+    for (int part = 0; part < KH; ++part) {
+        if (kh == part) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) op[(8 * (r / 4) + r % 4) * ORW] += acc[r];
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float* d = op + (32 * i + 8 * (r / 4) + r % 4) * ORW;
+                    *d = part == 0 ? acc[i][r] : *d + acc[i][r];
+                }
         }
         __syncthreads();
     }
@@ -807,7 +829,7 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
             const dim3 grid((unsigned)tiles(bm, bn));
 #define QLIN_WOS(BMV, BNV, KTV, STV)                                                                            \
     if (bm == BMV && bn == BNV && kt == KTV) {                                                                  \
-        hipLaunchKernelGGL((gemm_wo_dmas_kernel<BMV, BNV, KTV, STV>), grid, dim3(64 * wo_dmas_waves<BMV, BNV>()), 0, st, a); \
+        hipLaunchKernelGGL((gemm_wo_dmas_kernel<BMV, BNV, KTV, STV>), grid, dim3(64 * wo_dmas_waves<BMV, BNV, KTV>()), 0, st, a); \
         return hipGetLastError();                                                                               \
     }
             QLIN_WOS(64, 128, 128, 4) QLIN_WOS(64, 128, 64, 8)
