@@ -312,6 +312,19 @@ def measured_traffic(kernel, summary="gguf_linear_k4096_counters.md"):
     return sum(per[k] for k in parts) if all(k in per for k in parts) else None
 
 
+def config_traffic(name, summary="linear_configs_counters.md"):
+    """HBM bytes per call of config `name` (every kernel of the call) from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE summary; None when it has no line for the config."""
+    try:
+        for line in open(os.path.join(ROOT, "profiles", summary)):
+            f = line.split()
+            if len(f) >= 3 and f[0] == "traffic_call" and f[1] == name:
+                return int(f[2])
+    except OSError:
+        pass
+    return None
+
+
 # ------------------------------------------------------------------------------------------------
 # INT8-ConvRot, W4A8, W6A8 and the DiT layer at their benchmark shapes
 # ------------------------------------------------------------------------------------------------
@@ -454,7 +467,7 @@ def run_configs(names, steps, warmup, pool):
                 roof = {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tfl / FP16_PEAK_TFLOPS, 4), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
             roof.update({"kernel": CONFIG_KERNELS[name], "flops_per_call": flops, "bytes_per_call": nbytes,
-                         "traffic": None})
+                         "traffic": config_traffic(name)})
             rec = {"us_per_call": round(us, 2), "eager_us_per_call": round(eager, 2),
                    "eager_host_overhead_us": round(eager - us, 2), "TFLOPs": round(tfl, 2),
                    "GBps": round(gbs, 1), "pool_copies": copies, "roofline": roof, "cpu_baseline": cpu}
@@ -484,7 +497,7 @@ def run_configs(names, steps, warmup, pool):
                                 "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
                                 "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                 "kernel": CONFIG_KERNELS[name], "ops_per_call": flops, "bytes_per_call": nbytes,
-                                "traffic": None},
+                                "traffic": config_traffic(name)},
                    "cpu_baseline": cpu}
         else:  # one DiT block layer: QKV, O, MLP up, MLP down
             m, g = cfg["m"], cfg["g"]
@@ -550,7 +563,7 @@ def run_configs(names, steps, warmup, pool):
                    "vs_fp16_dense": round(layer_ms / dense_ms, 3), "pool_copies": copies,
                    "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS,
                                 "unit": "TFLOP/s", "frac": round(tfl / FP16_PEAK_TFLOPS, 4),
-                                "kernel": CONFIG_KERNELS[name], "flops_per_layer": flops, "traffic": None},
+                                "kernel": CONFIG_KERNELS[name], "flops_per_layer": flops, "traffic": config_traffic(name)},
                    "cpu_baseline": cpu}
         if rec["cpu_baseline"] is None:
             del rec["cpu_baseline"]
@@ -601,6 +614,82 @@ def profile_pass(which, reps=3, n=4096, k=4096, ms=(1, 8, 64)):
         torch.mul(src, 1.0, out=dst)
     torch.cuda.synchronize()
     log("[profile] done")
+
+
+def floors_suite(steps, warmup):
+    """Hardware floors on this GPU (libqlin_floors.so, built from probe/floors.hip), one JSON line on
+    stderr: the issue rate of the four MFMA shapes the kernels use (2 waves per SIMD, independent
+    accumulators, no memory traffic); a streaming read of one GGUF weight's size (9 MiB Q4_K and
+    18 MiB Q8_0 at K = N = 4096) from a >= 1 GiB pool, so every read misses the caches, and of a
+    whole GiB; a 512 MiB copy; and an empty launch.  Reads, copies and empty launches are
+    HIP-graph replays (the bench's own timing); MFMA rates are the median of 5 event-timed
+    launches after 2 warm-ups."""
+    import ctypes
+    import torch
+    L = ctypes.CDLL(os.path.join(ROOT, "mac-kernels-public_amd", "qlin", "libqlin_floors.so"))
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(16 * cus * 256, dtype=torch.float32, device="cuda")
+    rec = {"suite": "floors", "cus": cus}
+
+    def check(rc):
+        assert rc == 0, f"floors launch failed: {rc}"
+
+    # MFMA: kind -> (name, operations per instruction, accumulators per round)
+    shapes = {0: ("mfma_f32_32x32x16_f16", 2 * 32 * 32 * 16, 4), 1: ("mfma_f32_16x16x32_f16", 2 * 16 * 16 * 32, 8),
+              2: ("mfma_i32_32x32x32_i8", 2 * 32 * 32 * 32, 4), 3: ("mfma_i32_16x16x64_i8", 2 * 16 * 16 * 64, 8)}
+    blocks, iters = 2 * cus, 4000
+    mf = {}
+    for kind, (name, ops, acc) in shapes.items():
+        def launch(kind=kind):
+            check(L.qlin_floor_mfma(kind, blocks, iters, ctypes.c_void_p(out.data_ptr()), cur()))
+        def timed(launch=launch):
+            st = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            launch()
+            e1.record(st)
+            torch.cuda.synchronize()
+            t.append(e0.elapsed_time(e1))
+        t = []
+        for _ in range(7):
+            timed()
+        ms = statistics.median(t[2:])
+        total = blocks * 4 * iters * acc * ops
+        mf[name] = {"T_per_s": round(total / (ms * 1e-3) / 1e12, 1), "ms": round(ms, 4)}
+    rec["mfma"] = mf
+
+    pool = torch.empty(POOL_BYTES, dtype=torch.uint8, device="cuda")
+    words = torch.empty(16 * cus * 256, dtype=torch.int32, device="cuda")
+    rd = {}
+    for label, nbytes in (("read_9MiB", 9437184), ("read_18MiB", 18874368), ("read_1GiB", POOL_BYTES)):
+        copies = max(1, POOL_BYTES // nbytes)
+        rblocks = 4 * cus
+
+        def step(nbytes=nbytes, copies=copies, rblocks=rblocks):
+            for c in range(copies):
+                check(L.qlin_floor_read(ctypes.c_void_p(pool.data_ptr() + c * nbytes), ctypes.c_int64(nbytes),
+                                        rblocks, ctypes.c_void_p(words.data_ptr()), cur()))
+        ms, _ = time_graph(step, max(2, steps // 4), warmup)
+        us = ms / copies * 1e3
+        rd[label] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    half = POOL_BYTES // 2
+
+    def copy_step():
+        check(L.qlin_floor_copy(ctypes.c_void_p(pool.data_ptr()), ctypes.c_void_p(pool.data_ptr() + half),
+                                ctypes.c_int64(half), 4 * cus, cur()))
+    ms, _ = time_graph(copy_step, max(2, steps // 4), warmup)
+    rd["copy_512MiB"] = {"bytes_moved": 2 * half, "us": round(ms * 1e3, 1),
+                         "GBps": round(2 * half / (ms * 1e-3) / 1e9, 1)}
+
+    def empty_step():
+        for _ in range(100):
+            check(L.qlin_floor_empty(cus, ctypes.c_void_p(words.data_ptr()), cur()))
+    ms, _ = time_graph(empty_step, steps, warmup)
+    rd["empty_launch_us"] = round(ms / 100 * 1e3, 3)
+    rec["memory"] = rd
+    log(json.dumps(rec))
+    return rec
 
 
 def other_suites(which, steps, warmup):
@@ -682,8 +771,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--suite", default="main", choices=["main", "lora", "grad", "all"],
-                    help="main: the JSON line (GGUF headline + configs); lora / grad: extra suites on stderr")
+    ap.add_argument("--suite", default="main", choices=["main", "lora", "grad", "floors", "all"],
+                    help="main: the JSON line (GGUF headline + configs); lora / grad / floors: extra suites on "
+                         "stderr (floors: MFMA issue rates, HBM read / copy floors, empty launch)")
     ap.add_argument("--configs", default="all",
                     help="comma-separated names from CONFIGS for the `configs` object, 'all' or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -706,10 +796,12 @@ def main():
     if a.profile:
         profile_pass(a.profile)
         return
-    if a.suite != "main":
+    if a.suite in ("floors", "all"):
+        floors_suite(a.steps, a.warmup)
+    if a.suite not in ("main", "floors"):
         other_suites(a.suite, a.steps, a.warmup)
-        if a.suite != "all":
-            return
+    if a.suite != "main" and a.suite != "all":
+        return
     pool = None if a.no_cpu else HostPool(host_threads())
     r = suite_gguf(a.steps, a.warmup)
     kernels = kernel_breakdown(r["detail"])

@@ -3,8 +3,9 @@
     python mac-kernels-public_amd/build_lib.py [--jobs N]
 
 Each .hip translation unit is compiled to an object in parallel, then linked into
-mac-kernels-public_amd/qlin/libqlin.so.  Packed-FP32 VALU instructions are disabled for all
-device code (-Xclang -target-feature -Xclang -packed-fp32-ops).
+mac-kernels-public_amd/qlin/libqlin.so.  The hardware-floor probes of the measurement suite
+(probe/floors.hip) go into a library of their own, qlin/libqlin_floors.so.  Packed-FP32 VALU
+instructions are disabled for all device code (-Xclang -target-feature -Xclang -packed-fp32-ops).
 """
 import argparse
 import concurrent.futures as cf
@@ -17,6 +18,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "qlin", "libqlin.so")
+FLOORS_OUT = os.path.join(HERE, "qlin", "libqlin_floors.so")
 BUILD = os.path.join(HERE, "_build")
 ARCH = os.environ.get("QLIN_ARCH", "gfx950")
 
@@ -66,7 +68,21 @@ def build(jobs=None, verbose=False, force=True):
         print(r.stderr, file=sys.stderr)
         raise RuntimeError("link failed")
     os.replace(tmp, OUT)
+    build_floors()
     return OUT
+
+
+def build_floors():
+    """libqlin_floors.so: the hardware-floor probes of the measurement suite (probe/floors.hip);
+    a separate library that nothing in libqlin uses."""
+    src = os.path.join(HERE, "probe", "floors.hip")
+    tmp = FLOORS_OUT + ".tmp"
+    r = subprocess.run([HIPCC, *FLAGS, "-shared", "-o", tmp, src], capture_output=True, text=True)
+    if r.returncode:
+        print(r.stderr, file=sys.stderr)
+        raise RuntimeError("hipcc failed on probe/floors.hip")
+    os.replace(tmp, FLOORS_OUT)
+    return FLOORS_OUT
 
 
 if __name__ == "__main__":
