@@ -458,13 +458,14 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
 template <int BMT, int STAGES>
 __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
     constexpr int NT = 512, BNT = 256, KT = 64;
-    constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
+    // waves 2 (M) x 4 (N): each converted weight fragment feeds TI = 4 activation sub-tiles
+    constexpr int WM = BMT / 2, WN = BNT / 4, TI = WM / 32, TJ = WN / 32;
     constexpr int ASZ = BMT * KT * 2, BSZ = BNT * KT;   // bytes per stage
     constexpr int NA = ASZ / 16 / NT, NB = BSZ / 16 / NT;
     static_assert(TI >= 1 && NA * 16 * NT == ASZ && NB * 16 * NT == BSZ, "tile shape");
     __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ)];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, r32 = lane & 31, h = lane >> 5;
+    const int wm = wave & 1, wn = wave >> 1, r32 = lane & 31, h = lane >> 5;
     int mt, nt;
     xcd_tile_f16(blockIdx.x, (int)gridDim.x, (int)((a.M + BMT - 1) / BMT), (int)((a.N + BNT - 1) / BNT), mt, nt);
     const int64_t n0 = (int64_t)nt * BNT, m0 = (int64_t)mt * BMT;
