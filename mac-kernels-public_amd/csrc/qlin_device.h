@@ -101,11 +101,13 @@ __device__ __forceinline__ float swz_xor(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), pattern));
 }
 
-// DPP quad permutation (lane r of each quad reads lane SEL[r]).
+// DPP quad permutation (lane r of each quad reads lane SEL[r]).  Every lane is written and every
+// source lane exists, so the old value (0) and bound_ctrl never show; with them in this form the
+// compiler folds the permutation into the consuming add (v_add_f32 with a DPP source).
 template <int A, int B, int C, int D>
 __device__ __forceinline__ float dpp_quad(float v) {
     constexpr int ctrl = A | (B << 2) | (C << 4) | (D << 6);
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, true));
 }
 
 template <int MASK>
