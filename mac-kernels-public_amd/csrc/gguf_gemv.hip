@@ -4,7 +4,8 @@
 // the decode, so this path decodes straight into packed fp16 pairs and uses v_dot2_f32_f16:
 //   * each lane owns one contiguous "chunk" of a weight row (64 or 128 values: a run of whole
 //     32-value blocks, or part of a 256-value super-block) and loads it with 16-byte global loads
-//     (only 4-byte alignment is needed); a row is covered by 16..64 lanes, a wave covers 1..4 rows;
+//     (only 4-byte alignment is needed); a row is covered by 16..64 lanes, a wave covers 1..4 rows,
+//     and the grid has one wave per such group of rows (its loads issued before anything else);
 //   * the activation row is read once per workgroup with coalesced loads and staged in LDS in a
 //     swizzled order (a lane's own chunk, read with a 256-byte lane stride straight from global
 //     memory, would touch a different cache line per lane and per load); each lane keeps its
@@ -430,20 +431,16 @@ __global__ __launch_bounds__(GV_THREADS) void gguf_gemv_kernel(const f16* __rest
 #pragma unroll
     for (int j = 0; j < GV_MAX_K / 8 / GV_THREADS; ++j)
         xst[j] = reinterpret_cast<const u32x4*>(x)[min(tid + GV_THREADS * j, KU - 1)];
-    // 2. the weight chunks of this wave's first two passes (rows past N re-read row N - 1)
+    // 2. the weight chunks of this wave's first pass (rows past N re-read row N - 1)
     auto row_of = [&](int p) { return min(p * RPP + rp, N - 1); };
     int p = gw;
-    uint32_t r0[F::LD], r1[F::LD];
+    uint32_t r0[F::LD];
     __builtin_amdgcn_sched_barrier(0);
     F::load(w + (int64_t)row_of(p) * row_bytes, c, r0);
-    F::load(w + (int64_t)row_of(p + waves_total) * row_bytes, c, r1);
     // epilogue operands, fetched now rather than after the reduction
     const int xe = xexp ? xexp[0] : 0;
-    uint32_t bv0 = 0, bv1 = 0;  // raw bits (0 reads as +0 in every dtype)
-    if (bias) {
-        bv0 = load_bits_rt(bias, bias_dt, row_of(p));
-        bv1 = load_bits_rt(bias, bias_dt, row_of(p + waves_total));
-    }
+    uint32_t bv0 = 0;  // raw bits (0 reads as +0 in every dtype)
+    if (bias) bv0 = load_bits_rt(bias, bias_dt, row_of(p));
     __builtin_amdgcn_sched_barrier(0);
     // 3. activations into LDS: unit i of chunk c at i * LPR + (c ^ i), so that the per-lane reads
     //    below (fixed i, consecutive c) and these writes both spread over the banks.  The fences
@@ -482,20 +479,14 @@ __global__ __launch_bounds__(GV_THREADS) void gguf_gemv_kernel(const f16* __rest
         for (int m = 1; m < LPR; m <<= 1) v += __shfl_xor(v, m, 64);
         if (c == 0 && n < N) store_rt(y, y_dt, n, __builtin_ldexpf(v, xe) + bits_to_f32_rt(bv, bias_dt));
     };
-    // The first two passes are computed unconditionally (their stores are guarded), so their
-    // loads are not moved into a branch behind the barrier; the launch normally sizes the grid so
-    // that they are all there is.
+    // The first pass is computed unconditionally (its store is guarded), so its loads are not
+    // moved into a branch behind the barrier; the launch sizes the grid so that it is all there is.
     for (;;) {
         finish(r0, p, bv0);
-        finish(r1, p + waves_total, bv1);
-        p += 2 * waves_total;
+        p += waves_total;
         if (p >= passes) break;
         F::load(w + (int64_t)row_of(p) * row_bytes, c, r0);
-        F::load(w + (int64_t)row_of(p + waves_total) * row_bytes, c, r1);
-        if (bias) {
-            bv0 = load_bits_rt(bias, bias_dt, row_of(p));
-            bv1 = load_bits_rt(bias, bias_dt, row_of(p + waves_total));
-        }
+        if (bias) bv0 = load_bits_rt(bias, bias_dt, row_of(p));
     }
 }
 
@@ -505,8 +496,10 @@ hipError_t launch(const GgufGemvArgs& a, hipStream_t st) {
     const int lpr = a.K / F::VC;
     const int rpp = 64 / lpr;
     const int passes = (a.N + rpp - 1) / rpp;
-    // about two passes per wave: every wave issues its loads up front, the second pass overlaps
-    int waves = (passes + 1) / 2;
+    // One pass per wave, every wave's loads issued up front.  Two passes per wave (half the
+    // waves, the second pass's loads also up front) measured 5-14% slower at K = N = 4096: with
+    // eight waves per CU instead of four, one wave's decode overlaps another's loads.
+    int waves = passes;
     int blocks = (waves + 3) / 4;
     if (blocks < 1) blocks = 1;
     dim3 grid((unsigned)blocks), block(GV_THREADS);

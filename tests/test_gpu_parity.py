@@ -132,11 +132,13 @@ def test_gguf_linear(name, m):
     ("Q4_0", 64, 131, 1280),    # five splits, N % 4 != 0 in the reduction
     ("Q8_0", 20, 12800, 1280),  # 100 row tiles: three splits over five stages (uneven)
     ("Q3_K", 64, 200, 2048),    # two-block stages, sub-block minimum MFMA
-    ("IQ4_XS", 47, 256, 4096),
+    ("Q2_K", 40, 136, 1024),    # four splits, 16-value units with minimums
+    ("IQ4_XS", 47, 256, 4096),  # eight splits
     # N a multiple of 1024: each row block's partials are added by workgroups of the XCD that wrote them
     ("Q4_K", 64, 1024, 2048),   # 8 row blocks, 8 splits
-    ("Q6_K", 24, 2048, 1024),   # 16 row blocks, 4 splits
+    ("Q6_K", 24, 2048, 1024),   # 16 row blocks, 2 splits
     ("Q8_0", 40, 3072, 512),    # 24 row blocks, 2 splits
+    ("Q5_K", 64, 16384, 1024),  # 128 row blocks, 2 splits
 ])
 def test_gguf_linear_split_k(name, m, n, k):
     """The K-split kernel (M = 17..64): ragged N, uneven and single splits, bias."""
@@ -147,6 +149,81 @@ def test_gguf_linear_split_k(name, m, n, k):
     want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
     got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), bias=b.to(DEV))
     check_linear(got, want, f"{name} M={m} N={n} K={k}")
+
+
+def _split_call(raw, name, n, k, x, ws=None):
+    """qlin_gguf_linear through the C ABI with a caller-owned workspace (None: the cached one)."""
+    Q = qlin()
+    if ws is None:
+        return Q.gguf_linear(x, raw, name, (n, k))
+    from qlin import _lib
+    L = _lib.load()
+    tid = Q.GGUF_TYPES[name][0]
+    y = torch.empty(x.shape[0], n, dtype=torch.float16, device=DEV)
+    st = L.qlin_gguf_linear(_lib.desc(x), raw.data_ptr(), tid, n, k, _lib.desc(None), _lib.desc(y),
+                            ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+    _lib.check(st, "gguf_linear")
+    return y
+
+
+@pytest.mark.parametrize("fill", ["ff", "random", "repeat"])
+def test_gguf_linear_split_k_workspace_contents(fill):
+    """The K split keeps its partials in the caller's workspace without clearing it first: whatever
+    the workspace holds (all ones, random bytes, a previous call's leftovers), every call is right
+    and bit-identical to the others (the partials are added in split order)."""
+    Q = qlin()
+    name, m, n, k = "Q4_K", 64, 4096, 4096  # 32 row blocks x 8 splits
+    raw = qz().random_gguf_blocks(name, n, k, seed=51)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = x_fp16(m, k, seed=52)
+    want = O.linear_ref(x.float().numpy(), w)
+    rawd, xd = torch.from_numpy(raw).to(DEV), x.to(DEV)
+    tid = Q.GGUF_TYPES[name][0]
+    from qlin import _lib
+    nbytes = _lib.load().qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, k, tid, _lib._TORCH_DT[torch.float16])
+    g = torch.Generator().manual_seed(53)
+    if fill == "ff":
+        ws = torch.full((nbytes,), 255, dtype=torch.uint8)
+    else:
+        ws = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=g)
+    ws = ws.to(DEV)
+    outs = []
+    for rep in range(3):
+        if fill == "random" and rep:
+            ws.copy_(torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=g).to(DEV))
+        outs.append(_split_call(rawd, name, n, k, xd, ws))
+    torch.cuda.synchronize()
+    check_linear(outs[0], want, f"{name} M={m} workspace {fill}")
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0]), f"workspace {fill}: calls differ"
+
+
+def test_gguf_linear_split_k_graph_replays():
+    """A captured K-split call replayed several times, with eager calls (their own workspace) and new
+    activations between the replays: every replay equals the eager call on the same input."""
+    Q = qlin()
+    name, m, n, k = "Q6_K", 48, 4096, 2048
+    raw = torch.from_numpy(qz().random_gguf_blocks(name, n, k, seed=61)).to(DEV)
+    xs = [x_fp16(m, k, seed=62 + i).to(DEV) for i in range(4)]
+    xin = xs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        Q.gguf_linear(xin, raw, name, (n, k))
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        yg = Q.gguf_linear(xin, raw, name, (n, k))
+    torch.cuda.synchronize()
+    for i in range(8):
+        xin.copy_(xs[i % 4])
+        g.replay()
+        torch.cuda.synchronize()
+        got = yg.clone()
+        want = Q.gguf_linear(xs[i % 4], raw, name, (n, k))
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i} differs from the eager call"
 
 
 # Long rows.  One activation row with K / (values per lane chunk) in {16, 32, 64} takes the GEMV
