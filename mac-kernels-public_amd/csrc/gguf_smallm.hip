@@ -1,8 +1,8 @@
 // GGUF linear for small M (1..64 activation rows): the weight-streaming (HBM-bound) regime.
 //
-// Grid: one 512-thread workgroup (8 waves) per 16 weight rows n; the K range is split across the
-// 8 waves in stages (256 values, or 512 for the 210/110-byte K-quant blocks), and the partial sums
-// are reduced through LDS at the end.  Each wave keeps one or two stages of weight loads in
+// Grid: one workgroup of W waves (8, or 16 up to 16 activation rows when K has a stage for each
+// wave) per 16 weight rows n; the K range is split across the waves in stages (256 values, or 512
+// for the 210/110-byte K-quant blocks), and the partial sums are reduced through LDS at the end.  Each wave keeps one or two stages of weight loads in
 // flight (16-, 8- or 4-byte units as the block size allows) and, separately, the activation
 // fragments of the next D scale units; no load sits behind a lane-dependent branch, so the
 // memory latencies overlap instead of adding up.  Per stage a wave copies its weight registers
@@ -27,14 +27,25 @@ namespace {
 
 using namespace gguf_mfma;
 
+// Waves per workgroup.  The grid has one workgroup per 16 weight rows (256 at N = 4096), so a CU
+// holds one: 16 waves (4 per SIMD) hide the weight and activation latencies of a K = 4096 call
+// better than 8 (each wave then owns one stage; 13-18% faster at M = 8 and 16).
 constexpr int SM_WAVES = 8;
-constexpr int SM_THREADS = SM_WAVES * 64;
+constexpr int SM_WAVES_WIDE = 16;
+
+// Formats that fit the 128 registers of 16 waves without spilling: 256-value stages, and no
+// per-unit offset term (Q4_1, Q5_1 carry a second MFMA and its sums).
+template <int T>
+constexpr bool wide_ok() {
+    using F = SM<T>;
+    return F::SBLK * F::QK == 256 && !(F::KIND == 0 && F::MIN);
+}
 
 constexpr int pow2_floor(int v) { return v >= 2 ? 2 * pow2_floor(v / 2) : 1; }
 
 // --------------------------------------------------------------------------------------------
-template <int T, int MT>
-__global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
+template <int T, int MT, int W>
+__global__ __launch_bounds__(64 * W) void gguf_smallm_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
     const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy,
@@ -54,8 +65,9 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     constexpr int UNITS = 16 * UPR;                  // load units per stage
     constexpr int NPF = (UNITS + 63) / 64;           // load units per lane per stage
     // stages held in registers: two when a stage is small, else one (two stages in flight at
-    // MT >= 3 measured slower: the activation stream already fills the memory pipeline)
-    constexpr int PF = (NPF <= 12 && MT <= 2) ? 2 : 1;
+    // MT >= 3 measured slower: the activation stream already fills the memory pipeline); one with
+    // 16 waves, where a wave usually owns a single stage
+    constexpr int PF = W == SM_WAVES_WIDE ? 1 : (NPF <= 12 && MT <= 2) ? 2 : 1;
     constexpr int UPS = SV / UNIT;                   // scale units per stage
     constexpr int UPB = QK / UNIT;                   // scale units per block
     // activation fragments in flight: D units ahead of the MFMAs (at most 64 VGPRs of them)
@@ -65,8 +77,8 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     typedef typename FragT<VPL>::type V;
     typedef uint32_t LU __attribute__((ext_vector_type(4), aligned(4)));
 
-    constexpr int STAGE_BYTES = SM_WAVES * 16 * RS;
-    constexpr int RED_BYTES = SM_WAVES * MT * 4 * 64 * 4;
+    constexpr int STAGE_BYTES = W * 16 * RS;
+    constexpr int RED_BYTES = W * MT * 4 * 64 * 4;
     __shared__ __attribute__((aligned(16))) uint8_t smem[STAGE_BYTES > RED_BYTES ? STAGE_BYTES : RED_BYTES];
     float (*red)[MT][4][64] = reinterpret_cast<float (*)[MT][4][64]>(smem);
 
@@ -74,14 +86,17 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
     const int n0 = blockIdx.x * 16;
     const int nl = lane & 15, g = lane >> 4;
     const int stages = K / SV;
-    const int st0 = (stages * wave) / SM_WAVES, st1 = (stages * (wave + 1)) / SM_WAVES;
+    const int st0 = (stages * wave) / W, st1 = (stages * (wave + 1)) / W;
     uint8_t* my = smem + wave * 16 * RS;
     // rows of the 4 outputs this lane holds per m-tile: 4*g + i; skip FMAs for rows past M when M <= 4
     const int ilim = (MT == 1 && M < 4) ? M : 4;
 
     // No load below branches on the lane: activation rows past M re-read row M - 1 and weight rows
-    // past N re-read row N - 1 (their results are never stored); stages past this wave's range
-    // re-read its last stage (never committed).
+    // past N re-read row N - 1 (their results are never stored).  With 8 waves, stages past this
+    // wave's range re-read its last stage (never committed); with 16 (one stage per wave at
+    // K = 4096) such refills are skipped instead, by a branch uniform across the wave: the
+    // re-reads only delayed the final barrier, which waits for every load in flight.
+    constexpr bool SKIP = W == SM_WAVES_WIDE;
     const f16* xrow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xrow[mt] = x + (int64_t)min(mt * 16 + nl, M - 1) * ldx + VPL * g;
@@ -144,12 +159,12 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                issue(st + PF, pf[j]);  // refill the freed registers with the stage PF ahead
+                if (!SKIP || st + PF < st1) issue(st + PF, pf[j]);  // refill with the stage PF ahead
                 const uint8_t* srow = my + nl * RS;
                 // unit u's activations sit in xr[u % D]; once used, the slot takes unit u + D
                 auto next_x = [&](int u) {
                     if (u + D < UPS) load_xu(st, u + D, xr[u % D]);
-                    else load_xu(st + 1, u + D - UPS, xr[u % D]);
+                    else if (!SKIP || st + 1 < st1) load_xu(st + 1, u + D - UPS, xr[u % D]);
                 };
                 if constexpr (F::KIND == 0) {
 #pragma unroll
@@ -224,14 +239,14 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
         for (int i = 0; i < 4; ++i) red[wave][mt][i][lane] = acc[mt][i];
     __syncthreads();
     // 16 x 16 outputs per m-tile; thread e handles element (i = e/64, source lane = e%64).
-    for (int e = tid; e < MT * 256; e += SM_THREADS) {
+    for (int e = tid; e < MT * 256; e += 64 * W) {
         const int mt = e >> 8, rem = e & 255, i = rem >> 6, sl = rem & 63;
         const int m = mt * 16 + 4 * (sl >> 4) + i;
         const int n = n0 + (sl & 15);
         if (m < M && n < N) {
             float sum = 0.0f;
 #pragma unroll
-            for (int wv = 0; wv < SM_WAVES; ++wv) sum += red[wv][mt][i][sl];
+            for (int wv = 0; wv < W; ++wv) sum += red[wv][mt][i][sl];
             float v = xexp ? __builtin_ldexpf(sum, xexp[m]) : sum;
             if (wscale) v *= load_rt(wscale, wscale_dt, n * wscale_stride);
             if (bias) v += load_rt(bias, bias_dt, n);
@@ -242,9 +257,18 @@ __global__ __launch_bounds__(SM_THREADS) void gguf_smallm_kernel(
 
 template <int T>
 hipError_t launch_t(const GgufSmallMArgs& a, hipStream_t st) {
-    dim3 grid((unsigned)((a.N + 15) / 16)), block(SM_THREADS);
+    dim3 grid((unsigned)((a.N + 15) / 16));
+    if constexpr (wide_ok<T>()) {
+        if (a.M <= 16 && a.K / (SM<T>::SBLK * SM<T>::QK) >= SM_WAVES_WIDE) {
+            hipLaunchKernelGGL((gguf_smallm_kernel<T, 1, SM_WAVES_WIDE>), grid, dim3(64 * SM_WAVES_WIDE), 0, st,
+                               a.x, a.ldx, a.M, a.xexp, a.w, a.row_bytes, a.N, a.K, a.bias, a.bias_dtype, a.y,
+                               a.y_dtype, a.ldy, a.wscale, a.wscale_dtype, a.wscale_stride);
+            return hipGetLastError();
+        }
+    }
+    const dim3 block(64 * SM_WAVES);
 #define QLIN_SM_LAUNCH(MTV)                                                                               \
-    hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
+    hipLaunchKernelGGL((gguf_smallm_kernel<T, MTV, SM_WAVES>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
                        a.row_bytes, a.N, a.K, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, a.wscale,         \
                        a.wscale_dtype, a.wscale_stride)
     switch ((a.M + 15) / 16) {
