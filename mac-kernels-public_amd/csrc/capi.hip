@@ -367,7 +367,7 @@ qlin_status qlin_w4a8_linear_grad_input(const qlin_tensor* dy, const qlin_tensor
     Carver ws{(uint8_t*)workspace, workspace_bytes};
     int8_t* grid = (int8_t*)ws.take((size_t)(N * K));
     const int srdt = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype;
-    GemmI8Args g;  // the forward's grid decode (one thread per 64 codes) when its layout allows
+    GemmI8Args g;  // the forward's grid decode (four threads per 64 codes) when its layout allows
     g.N = N; g.K = K; g.q = (const uint8_t*)Q.data; g.ldq = Q.ld; g.bits = bits; g.group_size = group_size;
     g.s_rel = SR.data; g.s_rel_dtype = srdt; g.ld_srel = SR.ld; g.s_ch = (const float*)s_channel->data;
     g.codebook = cb; g.w8 = grid;

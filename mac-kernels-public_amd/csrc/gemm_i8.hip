@@ -545,32 +545,73 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
 // here the decode VALU work leaves the GEMM loop, whose MFMAs interleave with fragment reads only.
 // ------------------------------------------------------------------------------------------------
 
-// One thread per (weight row, 64-code segment): w8[n][64 s .. 64 s + 63].  Needs group_size % 64 == 0.
+// Four threads per (weight row, 64-code segment): thread q of a quad writes w8[n][64 s + 16 q ..
+// + 15], so the lanes of a wave load contiguous runs (8 bytes of nibbles and, for 6 bits, 4 bytes
+// of high bits each) and store 16 contiguous bytes each.  The 4-bit level table (one grid byte per
+// code) is built a quarter per thread and exchanged within the quad.  Needs group_size % 64 == 0.
 template <int BITS, bool CB, typename TSrel>
 __global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __restrict__ w8) {
-    const int64_t segs = p.K / 64;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= p.N * segs) return;
-    const int64_t n = t / segs;
-    const int sg = (int)(t % segs);
+#pragma clang fp contract(off)
+    // 32-bit indices: N * K / 64 < 2^32 for every shape the entry points accept (K <= 32768)
+    const uint32_t segs = (uint32_t)p.K / 64u, total = (uint32_t)p.N * segs;
+    const uint32_t u = (blockIdx.x * 256u + threadIdx.x) >> 2;
+    const int q = threadIdx.x & 3;
+    // Threads past the end work on the last segment (all four lanes of a quad take part in the
+    // table exchange) and skip only the store.
+    const bool live = u < total;
+    const uint32_t uu = live ? u : total - 1;
+    const uint32_t n32 = uu / segs;
+    const int sg = (int)(uu - n32 * segs);
+    const int64_t n = n32;
     const uint8_t* row = p.q + n * p.ldq;
-    uint32_t nib[8], hi2[4] = {0, 0, 0, 0};
-    const u32x4 n_0 = *reinterpret_cast<const u32x4*>(row + 32 * sg), n_1 = *reinterpret_cast<const u32x4*>(row + 32 * sg + 16);
-    nib[0] = n_0.x; nib[1] = n_0.y; nib[2] = n_0.z; nib[3] = n_0.w;
-    nib[4] = n_1.x; nib[5] = n_1.y; nib[6] = n_1.z; nib[7] = n_1.w;
-    if constexpr (BITS == 6) {
-        const u32x4 hv = *reinterpret_cast<const u32x4*>(row + p.K / 2 + 16 * sg);
-        hi2[0] = hv.x; hi2[1] = hv.y; hi2[2] = hv.z; hi2[3] = hv.w;
-    }
+    const u32x2 nv = *reinterpret_cast<const u32x2*>(row + 32 * sg + 8 * q);  // codes 16 q .. 16 q + 15
     const void* srow;
     if constexpr (sizeof(TSrel) == 1) srow = (const uint8_t*)p.s_rel + n * p.ld_srel;
     else srow = (const TSrel*)p.s_rel + n * p.ld_srel;
-    const float sv = srel_from_bits<TSrel>(srel_bits<TSrel>(srow, (unsigned)(64 * sg) / (unsigned)p.group_size));
-    uint32_t o[16];
-    decode64<BITS, CB>(nib, hi2, sv, p.codebook, 0, false, o);
-    u32x4* dst = reinterpret_cast<u32x4*>(w8 + n * p.K + 64 * sg);
+    const float s = srel_from_bits<TSrel>(srel_bits<TSrel>(srow, (unsigned)(64 * sg) / (unsigned)p.group_size));
+    uint32_t o[4];
+    if constexpr (BITS == 4) {
+        uint32_t mine = 0;  // grid bytes of codes 4 q .. 4 q + 3
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        for (int b = 0; b < 4; ++b) {
+            const int c = 4 * q + b;
+            const float level = CB ? p.codebook[c] : (float)(c - 8);
+            mine |= grid_byte(level, s) << (8 * b);
+        }
+        const uint32_t t0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0x00, 0xF, 0xF, false);
+        const uint32_t t1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0x55, 0xF, 0xF, false);
+        const uint32_t t2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xAA, 0xF, 0xF, false);
+        const uint32_t t3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xFF, 0xF, 0xF, false);
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {  // nibble dword d: codes 16 q + 8 d .. + 7
+            const uint32_t w = nv[d];
+            const uint32_t ev = lut16(w & 0x0F0F0F0Fu, t0, t1, t2, t3);         // codes 0, 2, 4, 6
+            const uint32_t od = lut16((w >> 4) & 0x0F0F0F0Fu, t0, t1, t2, t3);  // codes 1, 3, 5, 7
+            o[2 * d] = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+            o[2 * d + 1] = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+        }
+    } else {
+        const uint32_t hv = *reinterpret_cast<const uint32_t*>(row + p.K / 2 + 16 * sg + 4 * q);
+        // (c - 32) * s as fma(c, s, -32 s): the exact product rounded once, the reference's fp32
+        // product; s clamped to +-2^20 (every clamped grid value is unchanged, -32 s stays finite)
+        const float sc = __builtin_amdgcn_fmed3f(s, -0x1p20f, 0x1p20f), off = -32.0f * sc;
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const uint32_t w = nv[d];
+            const uint32_t h16 = (hv >> (16 * d)) & 0xFFFFu;  // 2 bits per code
+            uint32_t o0 = 0, o1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t code = ((w >> (4 * i)) & 0xFu) | (((h16 >> (2 * i)) & 3u) << 4);
+                const uint32_t bb = grid_bits(__builtin_fmaf((float)code, sc, off)) & 0xFFu;
+                if (i < 4) o0 |= bb << (8 * i);
+                else o1 |= bb << (8 * (i - 4));
+            }
+            o[2 * d] = o0;
+            o[2 * d + 1] = o1;
+        }
+    }
+    if (live) *reinterpret_cast<u32x4*>(w8 + n * p.K + 64 * sg + 16 * q) = u32x4{o[0], o[1], o[2], o[3]};
 }
 
 // int8 GEMM y = epilogue(xq[M, K] . w8[N, K]^T), tile BMT x BNT x BK, 8 waves 4 (M) x 2 (N),
@@ -891,7 +932,8 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.w8 && a8_decode_once(p.M, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
         (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0) {
         const int64_t segs = p.N * (p.K / 64);
-        hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, TSrel>), dim3((unsigned)((segs + 255) / 256)), dim3(256), 0, st,
+        if (4 * segs + 256 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // the grid kernel's 32-bit indices
+        hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, TSrel>), dim3((unsigned)((4 * segs + 255) / 256)), dim3(256), 0, st,
                            p, p.w8);
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
@@ -899,7 +941,9 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         if (tiles(256, 256) >= 192)
             hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2, false>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p,
                                p.w8);
-        else if (tiles(128, 256) >= 192)
+        // 128 x 256 also when it fits one round on the 256 CUs and 128 x 128 would not: one round of
+        // the larger tile beats 1.25 rounds of the smaller (M1024 K13824 N5120: 150.6 vs 157.1 us)
+        else if (tiles(128, 256) >= 192 || (tiles(128, 256) <= 256 && tiles(128, 128) > 256))
             hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2, false>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p,
                                p.w8);
         else
@@ -936,7 +980,8 @@ hipError_t launch_s(const GemmI8Args& p, hipStream_t st) {
 template <int BITS, bool CB>
 hipError_t launch_grid(const GemmI8Args& p, hipStream_t st) {
     const int64_t segs = p.N * (p.K / 64);
-    const dim3 grid((unsigned)((segs + 255) / 256));
+    if (4 * segs + 256 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // the kernel's 32-bit indices
+    const dim3 grid((unsigned)((4 * segs + 255) / 256));
     switch (p.s_rel_dtype) {
         case DT_E4M3: hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, uint8_t>), grid, dim3(256), 0, st, p, p.w8); break;
         case DT_F16: hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, f16>), grid, dim3(256), 0, st, p, p.w8); break;
