@@ -348,7 +348,7 @@ CONFIGS = {
 # The launches a call makes at these shapes (the C ABI's dispatch), named as in the kernel traces.
 CONFIG_KERNELS = {
     "int8_convrot_m256_k3072_n3072": "prologue_kernel+gemm_wo_dmas_kernel<64,64,256,3>",
-    "int8_convrot_m1_k3072_n3072": "prologue_kernel+int8_gemv_kernel<1,3>",
+    "int8_convrot_m1_k3072_n3072": "int8_gemv_kernel<1,3,2>",
     "w4a8_m4096_k3072_n12288": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m1024_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m1024_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<128,256>",

@@ -485,7 +485,18 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
-    // weight streaming for few rows: the VALU GEMV (one or two rows), then the small-M MFMA kernel
+    // weight streaming for few rows: the VALU GEMV (one or two rows), then the small-M MFMA kernel.
+    // With a rotation, the GEMV rotates and normalizes fp16 / bf16 rows itself (no prologue launch).
+    if (M <= 2 && convrot_groupsize) {
+        Int8GemvArgs g;
+        g.xraw = X.data; g.x_dtype = X.dtype; g.ldx = X.ld; g.G = convrot_groupsize;
+        g.w = (const int8_t*)Q.data; g.ldw = Q.ld;
+        g.M = M; g.N = N; g.K = K;
+        g.scale = scale->data; g.scale_dtype = scale->dtype; g.scale_stride = sst;
+        g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
+        g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
+        if (int8_gemv_supported(g)) return hip_status(run_int8_gemv(g, st), "int8 gemv");
+    }
     GemmF16Args a;
     if ((s = wo_activations(X, convrot_groupsize, ws, st, a.x, a.ldx, a.xexp))) return s;
     if (M <= 2) {

@@ -83,9 +83,12 @@ hipError_t run_int8_smallm(const GgufSmallMArgs& a, hipStream_t st);
 
 // INT8 weight-only linear for one or two activation rows (int8_gemv.hip): normalized fp16 x, int8 w.
 struct Int8GemvArgs {
-    const f16* x = nullptr;
-    int64_t ldx = 0;
+    const f16* x = nullptr;          // the prologue's normalized fp16 rows (xraw == nullptr)
+    int64_t ldx = 0;                 // row stride of x, or of xraw
     const int32_t* xexp = nullptr;
+    const void* xraw = nullptr;      // raw fp16 / bf16 rows, rotated and normalized in the kernel
+    int x_dtype = DT_F16;            // dtype of xraw
+    int G = 0;                       // ConvRot group applied to xraw
     const int8_t* w = nullptr;
     int64_t ldw = 0;
     int64_t M = 0, N = 0, K = 0;

@@ -54,6 +54,39 @@ def test_int8_linear_small_m(m, k, n, g):
     check(y, want, f"M={m} K={k} N={n} G={g}")
 
 
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("g", [64, 128, 256])
+@pytest.mark.parametrize("m,k", [(1, 1024), (1, 3072), (1, 5120), (1, 8192), (2, 3072), (2, 4096)])
+def test_int8_gemv_fused_prologue_matches_prologue_kernel(m, k, g, xdt):
+    """One or two fp16 / bf16 rows with a rotation: the GEMV rotates and normalizes them itself.
+    The same rows in a view whose row stride is not a multiple of 8 take the prologue kernel and
+    the plain GEMV instead; both paths must give the same output bit for bit (the normalized
+    operand and the exponent come from the same arithmetic), and both meet the oracle's bar."""
+    n = 520
+    q, s = int8_weight(n, k, seed=k + g)
+    gen = torch.Generator().manual_seed(k + m)
+    x = (torch.randn(m, k, generator=gen) * 3)
+    x[:, 5] = 900.0  # a large value: the row exponent differs from 0
+    x = x.to(xdt)
+    b = (torch.randn(n, generator=gen) * 0.1).half()
+    Q = qlin()
+    xd = x.to(DEV)
+    padded = torch.zeros(m, k + 4, dtype=xdt, device=DEV)
+    padded[:, :k] = xd
+    xs = padded[:, :k]
+    assert xs.stride(0) % 8 != 0
+    args = (q.to(DEV), s.to(DEV), b.to(DEV))
+    y_fused = Q.int8_linear(xd, *args, convrot=True, convrot_groupsize=g)
+    y_plain = Q.int8_linear(xs, *args, convrot=True, convrot_groupsize=g)
+    torch.cuda.synchronize()
+    assert torch.equal(y_fused, y_plain), f"M={m} K={k} G={g} {xdt}: fused and prologue paths differ"
+    y32 = Q.int8_linear(xd, *args, torch.float32, convrot=True, convrot_groupsize=g)
+    want = O.linear_ref(O.rotate(x.float().numpy(), g), O.dequantize_int8(q.numpy(), s.numpy()), b.float().numpy())
+    check(y32, want, f"fused M={m} K={k} G={g} {xdt}")
+    # the default output dtype is the input's: the same fp32 value, rounded once (RNE)
+    assert torch.equal(y_fused, y32.to(xdt)), f"M={m} K={k} G={g} {xdt}: output rounding differs"
+
+
 @pytest.mark.parametrize("xdt,odt,sdt", [(torch.bfloat16, torch.bfloat16, torch.float16),
                                          (torch.float32, torch.float32, torch.float32),
                                          (torch.float16, torch.float32, torch.float16)])
