@@ -262,19 +262,19 @@ qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x
         case QLIN_OP_INT8_LINEAR:
             if (!valid_group(param)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", param);
             if (param && K % param) return fail(QLIN_EUNSUPPORTED, "K %% group != 0");
-            if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+            if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
             return QLIN_OK;
         case QLIN_OP_W4A8_LINEAR:
             if (param != 4 && param != 6) return fail(QLIN_EUNSUPPORTED, "bits %d unsupported", param);
             if (K % 64) return fail(QLIN_EUNSUPPORTED, "K %% 64 != 0");
-            if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+            if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
             return QLIN_OK;
         case QLIN_OP_GGUF_LINEAR: {
             int qk, ts;
             if (!gguf::type_info(param, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", param);
             if (K % qk) return fail(QLIN_EUNSUPPORTED, "K %% block != 0 (rows straddle blocks)");
             if (K % 32) return fail(QLIN_EUNSUPPORTED, "K %% 32 != 0");
-            if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+            if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
             return QLIN_OK;
         }
     }
@@ -474,7 +474,7 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     if (!valid_group(convrot_groupsize)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
     if (convrot_groupsize && K % convrot_groupsize)
         return fail(QLIN_EINVAL, "K=%lld is not a multiple of the ConvRot group %d", (long long)K, convrot_groupsize);
-    if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
     int64_t sst;
     if ((s = as_vector(scale, "scale", N, true, sst))) return s;
     if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype %d unsupported", scale->dtype);
@@ -537,7 +537,7 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
     if (!weight) return fail(QLIN_EINVAL, "weight is missing");
     if (K % qk) return fail(QLIN_EUNSUPPORTED, "K=%lld is not a whole number of %d-value blocks", (long long)K, qk);
     if (K % 32) return fail(QLIN_EUNSUPPORTED, "K %% 32 != 0");
-    if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
     Mat X, Y;
     qlin_status s = check_xy(x, y, N, K, X, Y);
     if (s) return s;
@@ -645,7 +645,7 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     if (group_size <= 0 || group_size % 8 || K % group_size)
         return fail(QLIN_EUNSUPPORTED, "group_size %d unsupported for K=%lld", group_size, (long long)K);
     if (K % 64) return fail(QLIN_EUNSUPPORTED, "K %% 64 != 0");
-    if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
     if (Q.ld % 16 || (uintptr_t)Q.data % 16) return fail(QLIN_EUNSUPPORTED, "qdata rows must be 16-byte aligned");
     if (!valid_group(convrot_groupsize)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
     if (convrot_groupsize && K % convrot_groupsize) return fail(QLIN_EINVAL, "K %% ConvRot group != 0");
@@ -807,7 +807,7 @@ qlin_status qlin_quantize_act_int8(const qlin_tensor* x, qlin_tensor* q, qlin_te
     if (scale->dtype != QLIN_DT_F32) return fail(QLIN_EINVAL, "scale must be float32");
     if (!valid_group(convrot_groupsize) || (convrot_groupsize && X.cols % convrot_groupsize))
         return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
-    if (X.cols > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+    if (X.cols > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
     void* xr = nullptr;
     if (xrot && xrot->data) {
         Mat XR;

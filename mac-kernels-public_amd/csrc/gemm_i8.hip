@@ -552,7 +552,7 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
 template <int BITS, bool CB, typename TSrel>
 __global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __restrict__ w8) {
 #pragma clang fp contract(off)
-    // 32-bit indices: N * K / 64 < 2^32 for every shape the entry points accept (K <= 32768)
+    // 32-bit indices: the launchers refuse grids of 2^32 threads or more (4 per 64-code segment)
     const uint32_t segs = (uint32_t)p.K / 64u, total = (uint32_t)p.N * segs;
     const uint32_t u = (blockIdx.x * 256u + threadIdx.x) >> 2;
     const int q = threadIdx.x & 3;

@@ -49,6 +49,112 @@ __device__ __forceinline__ void load16(const TIn* row, int64_t e0, int K, bool v
 // Largest workgroup per slot count (keeps 16 x SLOTS row values in registers without spilling).
 constexpr int prologue_max_threads(int slots) { return slots <= 2 ? 1024 : slots == 4 ? 512 : 256; }
 
+// One 16-value unit of a row: load, rotate by the normalized Hadamard, and for A8 round to the
+// input dtype (the value a rotated x.dtype tensor holds).
+template <typename TIn, int MODE, int G>
+__device__ __forceinline__ void rotate_unit(const TIn* row, int64_t e0, int K, bool vec_ok, int lane, float* v) {
+    load16<TIn>(row, e0, K, vec_ok, v);
+    if constexpr (G > 0) {
+        hadamard16<G>(v, lane);
+        const float nrm = hadamard_norm<G>();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] *= nrm;
+    }
+    if constexpr (MODE == 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = round_to<TIn>(v[i]);
+    }
+}
+
+// Largest |value| over the workgroup (every thread gets it); red holds one float per wave.
+__device__ __forceinline__ float block_max(float amax, float* red, int NT, int lane, int wave) {
+    amax = wave_max(amax);
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    amax = red[0];
+    for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, red[w]);
+    return amax;
+}
+
+// Weight-only output of one unit: fp16(v * 2^-E), 16-byte stores where the row allows.
+__device__ __forceinline__ void emit_wo(const float* v, int E, int64_t e0, int K, bool vec_ok, f16* dst) {
+    f16 h[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = (f16)__builtin_ldexpf(v[i], -E);
+    if (e0 + 16 <= K && vec_ok) {
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, h[2 * i]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, h[2 * i + 1]) << 16);
+        }
+        u32x4* d = reinterpret_cast<u32x4*>(dst);
+        d[0] = u32x4{w[0], w[1], w[2], w[3]};
+        d[1] = u32x4{w[4], w[5], w[6], w[7]};
+    } else {
+        for (int i = 0; i < 16; ++i)
+            if (e0 + i < K) dst[i] = h[i];
+    }
+}
+
+// A8 row scale from the row's max |value| (quantize_int8_rowwise): scale = max(amax / 127, 1e-30)
+// in fp32, st = dtype(scale), 0 -> the dtype's smallest normal.
+template <typename TIn>
+__device__ __forceinline__ void a8_scale(float amax, float& scale, float& st) {
+    scale = amax / 127.0f;
+    if (!(scale >= 1e-30f)) scale = (scale != scale) ? scale : 1e-30f;
+    st = round_to<TIn>(scale);
+    if (st == 0.0f) st = dtype_traits<TIn>::tiny();
+}
+
+// A8 output of one unit: q = clamp(rne(dtype(x / st)), -128, 127).  x / st: for 16-bit inputs and a
+// finite normal st, the reciprocal y = 1/st with one residual correction, q = fma(fma(-x y, st, x),
+// y, x y) (Markstein).  Checked against the IEEE quotient for every pair of finite fp16 (bf16)
+// values x, st with |x| <= 130 st (tests/quotient_check.c): identical fp32 quotients for fp16,
+// identical int8 results for bf16.  Otherwise (fp32 inputs, subnormal or infinite st) the IEEE
+// division.  xd (optional) receives the rotated values in x's dtype.
+template <typename TIn, bool FAST>
+__device__ __forceinline__ void emit_a8(const float* v, float st, float y, int64_t e0, int K, bool vec_ok,
+                                        int8_t* dst, TIn* xd) {
+    int8_t qq[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float qt;
+        {
+#pragma clang fp contract(off)
+            if constexpr (FAST) {
+                const float q0 = v[i] * y;
+                qt = __builtin_fmaf(__builtin_fmaf(-q0, st, v[i]), y, q0);
+            } else {
+                qt = v[i] / st;
+            }
+        }
+        float t = __builtin_rintf(round_to<TIn>(qt));
+        t = fminf(fmaxf(t, -128.0f), 127.0f);
+        qq[i] = (int8_t)(int)t;
+    }
+    if (e0 + 16 <= K && vec_ok) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)(uint8_t)qq[4 * i] | ((uint32_t)(uint8_t)qq[4 * i + 1] << 8) |
+                   ((uint32_t)(uint8_t)qq[4 * i + 2] << 16) | ((uint32_t)(uint8_t)qq[4 * i + 3] << 24);
+        *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+        for (int i = 0; i < 16; ++i)
+            if (e0 + i < K) dst[i] = qq[i];
+    }
+    if (xd) {
+        for (int i = 0; i < 16; ++i)
+            if (e0 + i < K) xd[i] = dtype_traits<TIn>::from_f32(v[i]);
+    }
+}
+
+__device__ __forceinline__ void emit_f32(const float* v, int64_t e0, int K, float* dst) {
+    for (int i = 0; i < 16; ++i)
+        if (e0 + i < K) dst[i] = v[i];
+}
+
 template <typename TIn, int MODE, int G, int SLOTS>
 __global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) void prologue_kernel(const TIn* __restrict__ x, int64_t ldx, int K,
                                                        bool vec_ok, f16* __restrict__ xo, int64_t ldo,
@@ -64,28 +170,11 @@ __global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) vo
     float amax = 0.0f;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
-        const int64_t e0 = ((int64_t)s * NT + tid) * 16;
-        load16<TIn>(row, e0, K, vec_ok, v[s]);
-        if constexpr (G > 0) {
-            hadamard16<G>(v[s], lane);
-            const float nrm = hadamard_norm<G>();
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[s][i] *= nrm;
-        }
-        if constexpr (MODE == 1) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[s][i] = round_to<TIn>(v[s][i]);
-        }
+        rotate_unit<TIn, MODE, G>(row, ((int64_t)s * NT + tid) * 16, K, vec_ok, lane, v[s]);
 #pragma unroll
         for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[s][i]));
     }
-    if constexpr (MODE != 2) {
-        amax = wave_max(amax);
-        if (lane == 0) red[wave] = amax;
-        __syncthreads();
-        amax = red[0];
-        for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, red[w]);
-    }
+    if constexpr (MODE != 2) amax = block_max(amax, red, NT, lane, wave);
 
     if constexpr (MODE == 0) {
         const int E = frexp_exp(amax);
@@ -93,82 +182,23 @@ __global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) vo
         for (int s = 0; s < SLOTS; ++s) {
             const int64_t e0 = ((int64_t)s * NT + tid) * 16;
             if (e0 >= K) break;
-            f16 h[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) h[i] = (f16)__builtin_ldexpf(v[s][i], -E);
-            f16* dst = xo + (int64_t)m * ldo + e0;
-            if (e0 + 16 <= K && vec_ok) {
-                u32x4* d = reinterpret_cast<u32x4*>(dst);
-                u32x4 a, b;
-                uint32_t w[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    w[i] = (uint32_t)__builtin_bit_cast(uint16_t, h[2 * i]) |
-                           ((uint32_t)__builtin_bit_cast(uint16_t, h[2 * i + 1]) << 16);
-                }
-                a = u32x4{w[0], w[1], w[2], w[3]};
-                b = u32x4{w[4], w[5], w[6], w[7]};
-                d[0] = a;
-                d[1] = b;
-            } else {
-                for (int i = 0; i < 16; ++i)
-                    if (e0 + i < K) dst[i] = h[i];
-            }
+            emit_wo(v[s], E, e0, K, vec_ok, xo + (int64_t)m * ldo + e0);
         }
         if (tid == 0) eo[m] = E;
     } else if constexpr (MODE == 1) {
-        float scale = amax / 127.0f;
-        if (!(scale >= 1e-30f)) scale = (scale != scale) ? scale : 1e-30f;
-        float st = round_to<TIn>(scale);
-        if (st == 0.0f) st = dtype_traits<TIn>::tiny();
-        // x / st: for 16-bit inputs and a finite normal st, the reciprocal y = 1/st with one
-        // residual correction, q = fma(fma(-x y, st, x), y, x y) (Markstein).  Checked against the
-        // IEEE quotient for every pair of finite fp16 (bf16) values x, st with |x| <= 130 st
-        // (tests/quotient_check.c): identical fp32 quotients for fp16, identical int8 results for
-        // bf16.  Otherwise (fp32 inputs, subnormal or infinite st) the IEEE division.
+        float scale, st;
+        a8_scale<TIn>(amax, scale, st);
         const bool fast = sizeof(TIn) == 2 && st >= 0x1p-126f && st <= 0x1.fffffep127f;
         const float y = 1.0f / st;
         // the row-uniform choice is made once, outside the element loops
         auto quantize_row = [&]<bool FAST>() {
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-            const int64_t e0 = ((int64_t)s * NT + tid) * 16;
-            if (e0 >= K) break;
-            int8_t qq[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float qt;
-                {
-#pragma clang fp contract(off)
-                    if constexpr (FAST) {
-                        const float q0 = v[s][i] * y;
-                        qt = __builtin_fmaf(__builtin_fmaf(-q0, st, v[s][i]), y, q0);
-                    } else {
-                        qt = v[s][i] / st;
-                    }
-                }
-                float t = __builtin_rintf(round_to<TIn>(qt));
-                t = fminf(fmaxf(t, -128.0f), 127.0f);
-                qq[i] = (int8_t)(int)t;
+            for (int s = 0; s < SLOTS; ++s) {
+                const int64_t e0 = ((int64_t)s * NT + tid) * 16;
+                if (e0 >= K) break;
+                emit_a8<TIn, FAST>(v[s], st, y, e0, K, vec_ok, qo + (int64_t)m * ldo + e0,
+                                   xr ? xr + (int64_t)m * ldo + e0 : nullptr);
             }
-            int8_t* dst = qo + (int64_t)m * ldo + e0;
-            if (e0 + 16 <= K && vec_ok) {
-                uint32_t w[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    w[i] = (uint32_t)(uint8_t)qq[4 * i] | ((uint32_t)(uint8_t)qq[4 * i + 1] << 8) |
-                           ((uint32_t)(uint8_t)qq[4 * i + 2] << 16) | ((uint32_t)(uint8_t)qq[4 * i + 3] << 24);
-                *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
-            } else {
-                for (int i = 0; i < 16; ++i)
-                    if (e0 + i < K) dst[i] = qq[i];
-            }
-            if (xr) {
-                TIn* xd = xr + (int64_t)m * ldo + e0;
-                for (int i = 0; i < 16; ++i)
-                    if (e0 + i < K) xd[i] = dtype_traits<TIn>::from_f32(v[s][i]);
-            }
-        }
         };
         if (fast) quantize_row.template operator()<true>();
         else quantize_row.template operator()<false>();
@@ -178,10 +208,68 @@ __global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) vo
         for (int s = 0; s < SLOTS; ++s) {
             const int64_t e0 = ((int64_t)s * NT + tid) * 16;
             if (e0 >= K) break;
-            float* dst = fo + (int64_t)m * ldo + e0;
-            for (int i = 0; i < 16; ++i)
-                if (e0 + i < K) dst[i] = v[s][i];
+            emit_f32(v[s], e0, K, fo + (int64_t)m * ldo + e0);
         }
+    }
+}
+
+// Rows longer than one workgroup's registers hold (K > 32768): the row is processed in chunks of
+// WIDE_CAP values, twice -- the first pass rotates each chunk only for the row's max |value|, the
+// second rotates it again (same arithmetic, same values) and writes the outputs.  Rotate-only
+// rows need no max and take one pass.
+constexpr int WIDE_NT = 512, WIDE_SLOTS = 4, WIDE_CAP = WIDE_NT * WIDE_SLOTS * 16;
+
+template <typename TIn, int MODE, int G>
+__global__ __launch_bounds__(WIDE_NT) void prologue_wide_kernel(const TIn* __restrict__ x, int64_t ldx, int K,
+                                                             bool vec_ok, f16* __restrict__ xo, int64_t ldo,
+                                                             int32_t* __restrict__ eo, int8_t* __restrict__ qo,
+                                                             float* __restrict__ so, TIn* __restrict__ xr,
+                                                             float* __restrict__ fo) {
+    __shared__ float red[16];
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const TIn* row = x + (int64_t)m * ldx;
+    float amax = 0.0f;
+    if constexpr (MODE != 2) {
+        for (int64_t c0 = 0; c0 < K; c0 += WIDE_CAP) {
+#pragma unroll
+            for (int s = 0; s < WIDE_SLOTS; ++s) {
+                float v[16];
+                rotate_unit<TIn, MODE, G>(row, c0 + ((int64_t)s * WIDE_NT + tid) * 16, K, vec_ok, lane, v);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+            }
+        }
+        amax = block_max(amax, red, WIDE_NT, lane, wave);
+    }
+    int E = 0;
+    float scale = 0.0f, st = 1.0f;
+    if constexpr (MODE == 0) E = frexp_exp(amax);
+    if constexpr (MODE == 1) a8_scale<TIn>(amax, scale, st);
+    const bool fast = MODE == 1 && sizeof(TIn) == 2 && st >= 0x1p-126f && st <= 0x1.fffffep127f;
+    const float y = 1.0f / st;
+    for (int64_t c0 = 0; c0 < K; c0 += WIDE_CAP) {
+#pragma unroll
+        for (int s = 0; s < WIDE_SLOTS; ++s) {
+            const int64_t e0 = c0 + ((int64_t)s * WIDE_NT + tid) * 16;
+            float v[16];
+            rotate_unit<TIn, MODE, G>(row, e0, K, vec_ok, lane, v);
+            if (e0 >= K) continue;
+            if constexpr (MODE == 0) {
+                emit_wo(v, E, e0, K, vec_ok, xo + (int64_t)m * ldo + e0);
+            } else if constexpr (MODE == 1) {
+                int8_t* dst = qo + (int64_t)m * ldo + e0;
+                TIn* xd = xr ? xr + (int64_t)m * ldo + e0 : nullptr;
+                if (fast) emit_a8<TIn, true>(v, st, y, e0, K, vec_ok, dst, xd);
+                else emit_a8<TIn, false>(v, st, y, e0, K, vec_ok, dst, xd);
+            } else {
+                emit_f32(v, e0, K, fo + (int64_t)m * ldo + e0);
+            }
+        }
+    }
+    if (tid == 0) {
+        if constexpr (MODE == 0) eo[m] = E;
+        if constexpr (MODE == 1) so[m] = scale;
     }
 }
 
@@ -202,6 +290,9 @@ static void prologue_shape(int K, int& nt, int& slots) {
     }
 }
 
+// Longest row one workgroup holds in registers (the one-pass kernel).
+constexpr int PROLOGUE_ROW_MAX = 32768;
+
 template <typename TIn, int MODE>
 static hipError_t launch_prologue(const PrologueArgs& a, hipStream_t st) {
     int nt = 0, slots = 0;
@@ -209,13 +300,16 @@ static hipError_t launch_prologue(const PrologueArgs& a, hipStream_t st) {
     const bool vec_ok = (a.K % 16 == 0) && (a.ldx % 16 == 0) && (a.ldo % 16 == 0) &&
                         ((uintptr_t)a.x % 64 == 0);
     bool ok = false;
+    const bool wide = a.K > PROLOGUE_ROW_MAX;
+    if (wide) nt = WIDE_NT;
     auto go = [&]<int G>() {
         auto launch = [&](auto kern) {
             hipLaunchKernelGGL(kern, dim3((unsigned)a.M), dim3((unsigned)nt), 0, st, (const TIn*)a.x, a.ldx, a.K,
                                vec_ok, a.xo, a.ldo, a.eo, a.qo, a.so, (TIn*)a.xr, a.fo);
             ok = true;
         };
-        if (slots <= 1) launch(prologue_kernel<TIn, MODE, G, 1>);
+        if (wide) launch(prologue_wide_kernel<TIn, MODE, G>);
+        else if (slots <= 1) launch(prologue_kernel<TIn, MODE, G, 1>);
         else if (slots <= 2) launch(prologue_kernel<TIn, MODE, G, 2>);
         else if (slots <= 4) launch(prologue_kernel<TIn, MODE, G, 4>);
         else if (slots <= 8) launch(prologue_kernel<TIn, MODE, G, 8>);
@@ -226,7 +320,7 @@ static hipError_t launch_prologue(const PrologueArgs& a, hipStream_t st) {
 
 hipError_t run_prologue(const PrologueArgs& a, hipStream_t st) {
     if (a.M == 0) return hipSuccess;
-    if (a.K > 32768) return hipErrorInvalidValue;
+    if (a.K > QLIN_MAX_K) return hipErrorInvalidValue;
     switch (a.mode) {
         case PROLOGUE_WO:
             if (a.x_dtype == DT_F16) return launch_prologue<f16, 0>(a, st);
