@@ -61,6 +61,8 @@ typedef enum {
     QLIN_OP_LORA = 3,   /* qlin_lora_apply: param = the LoRA rank R */
     QLIN_OP_INT8_GRAD_INPUT = 4,  /* qlin_int8_linear_grad_input: M rows of dy, N outputs, K inputs */
     QLIN_OP_W4A8_GRAD_INPUT = 5,  /* qlin_w4a8_linear_grad_input (holds the decoded int8 grid, N*K bytes) */
+    QLIN_OP_INT8_LINEAR_LORA = 6, /* qlin_int8_linear_lora: param = the LoRA rank R */
+    QLIN_OP_W4A8_LINEAR_LORA = 7, /* qlin_w4a8_linear_lora: param = the LoRA rank R */
 } qlin_op;
 
 /* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
@@ -114,6 +116,29 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
 qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                              const qlin_tensor* bias, qlin_tensor* y,
                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* qlin_int8_linear / qlin_w4a8_linear with unmerged LoRA fused into the linear: t = x @ lora_down^T
+ * (fp32, in the workspace), then the large-M GEMM adds lora_scale * t @ lora_up^T to its own output
+ * tile in fp32 after the bias and rounds once into y.  Same operand rules as the plain linears and
+ * qlin_lora_apply (lora_down [R, K], lora_up [N, R], f32/f16/bf16; x is the caller's activation,
+ * before any ConvRot rotation).  The kernels that carry the term are the 256 x 256 INT8 GEMM (M > 16,
+ * grids of 160 tiles or more, 16-byte aligned operands) and the A8 decode-once GEMM (M >= 1024), for a
+ * rank that is a multiple of 8 with 16-byte aligned lora_up rows; other calls return
+ * QLIN_EUNSUPPORTED before launching anything, and the caller runs the plain linear and
+ * qlin_lora_apply_base instead.  Workspace: qlin_workspace_size(QLIN_OP_INT8_LINEAR_LORA or
+ * QLIN_OP_W4A8_LINEAR_LORA, M, N, K, R, x_dtype).
+ * Replaces the lora_down / lora_up / lora_scale keywords of comfy_kitchen int8_linear and
+ * w4a8_int8_linear (bench/bench_lora_sidepath_kernel.py:77-80; bench/bench_lora_fused_rank.py:39-44;
+ * semantics docs/upstream/comfy-kitchen-mps-backend.md:54-57). */
+qlin_status qlin_int8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                  const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize,
+                                  const qlin_tensor* lora_down, const qlin_tensor* lora_up, float lora_scale,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                  const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                                  qlin_tensor* y, int bits, int group_size, int convrot_groupsize,
+                                  const qlin_tensor* lora_down, const qlin_tensor* lora_up, float lora_scale,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of the fixed per-GPU scratch behind qlin_gguf_linear_noalloc. */
 #define QLIN_NOALLOC_SCRATCH_BYTES (16u << 20)

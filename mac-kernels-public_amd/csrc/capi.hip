@@ -169,6 +169,54 @@ size_t ws_w4a8(int64_t M, int64_t N, int64_t K) {
     return align_up((size_t)(M * K)) + align_up((size_t)M * 4) + (a8_decode_once(M, K) ? align_up((size_t)(N * K)) : 0);
 }
 
+// LoRA's low-rank activation t = x down^T: S fp32 K-split partials and their sum, or one [M, R].
+size_t ws_lora(int64_t M, int64_t K, int64_t R) {
+    const int S = lora_splits(M, K, R);
+    return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(R > 0 ? R : 0) * 4);
+}
+
+// LoRA operands of a fused linear call (qlin_int8_linear_lora, qlin_w4a8_linear_lora).
+struct LoraIn {
+    const qlin_tensor* down;
+    const qlin_tensor* up;
+    float scale;
+};
+
+// down [R, K] and up [N, R], float dtypes, unit column stride.
+qlin_status lora_operands(const LoraIn& L, int64_t N, int64_t K, Mat& D, Mat& U) {
+    qlin_status s;
+    if ((s = as_matrix(L.down, "lora_down", D)) || (s = as_matrix(L.up, "lora_up", U))) return s;
+    if (!is_float(D.dtype) || !is_float(U.dtype)) return fail(QLIN_EUNSUPPORTED, "lora operands must be f32/f16/bf16");
+    if (D.rows < 1) return fail(QLIN_EINVAL, "lora rank must be positive");
+    if (D.cols != K) return fail(QLIN_EINVAL, "lora_down is [%lld, %lld], x has K=%lld", (long long)D.rows,
+                                 (long long)D.cols, (long long)K);
+    if (U.rows != N || U.cols != D.rows)
+        return fail(QLIN_EINVAL, "lora_up must be [%lld, %lld]", (long long)N, (long long)D.rows);
+    return QLIN_OK;
+}
+
+bool vec8(const Mat& A) {  // 16-byte loads of 8 values along the rows
+    const int es = A.dtype == QLIN_DT_F32 ? 4 : 2;
+    return A.cols >= 8 && A.cols % 8 == 0 && (A.ld * es) % 16 == 0 && (uintptr_t)A.data % 16 == 0;
+}
+
+// Arguments of the t = x down^T kernels writing into `t` (S partials, then their sum).
+LoraArgs lora_down_args(const Mat& X, const Mat& D, float* t) {
+    LoraArgs a;
+    a.x = X.data; a.x_dt = X.dtype; a.ldx = X.ld; a.vec_x = vec8(X);
+    a.down = D.data; a.down_dt = D.dtype; a.ld_down = D.ld; a.vec_down = vec8(D);
+    a.M = X.rows; a.K = X.cols; a.R = D.rows;
+    a.t = t;
+    a.S = lora_splits(X.rows, X.cols, D.rows);
+    return a;
+}
+
+// The final t of lora_down_args(X, D, t): the sum after the S partials when K is split.
+float* lora_t_final(float* t, int64_t M, int64_t K, int64_t R) {
+    const int S = lora_splits(M, K, R);
+    return S > 1 ? t + (int64_t)S * M * R : t;
+}
+
 // Runs the weight-only prologue unless x is already usable as the fp16 MFMA operand (fp16, no
 // rotation, aligned rows), in which case x itself is used and no exponents are needed.
 qlin_status wo_activations(const Mat& X, int G, Carver& ws, hipStream_t st, const f16*& xo, int64_t& ldx,
@@ -247,6 +295,8 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param);
         case QLIN_OP_INT8_GRAD_INPUT: return ws_grad(M, N, K, false);
         case QLIN_OP_W4A8_GRAD_INPUT: return ws_grad(M, N, K, true);
+        case QLIN_OP_INT8_LINEAR_LORA: return ws_int8(M, K) + ws_lora(M, K, param);
+        case QLIN_OP_W4A8_LINEAR_LORA: return ws_w4a8(M, N, K) + ws_lora(M, K, param);
         case QLIN_OP_LORA: {  // the split partials, then their sum
             const int S = lora_splits(M, K, param);
             return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(param > 0 ? param : 0) * 4);
@@ -462,9 +512,11 @@ qlin_status qlin_residual_epilogue(const qlin_tensor* base, const qlin_tensor* r
     return hip_status(run_residual(a, (hipStream_t)stream), "residual epilogue");
 }
 
-qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
-                             const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+// The INT8 weight-only linear; with L, the LoRA term joins the epilogue of the large-M DMA GEMM
+// (QLIN_EUNSUPPORTED, before anything is launched, when another kernel would take the call).
+static qlin_status int8_linear_impl(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                    const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize, const LoraIn* L,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
     Mat Q, X, Y;
     qlin_status s = as_matrix(qdata, "qdata", Q);
     if (s) return s;
@@ -480,11 +532,40 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype %d unsupported", scale->dtype);
     int bdt;
     if ((s = check_bias(bias, N, bdt))) return s;
+    Mat D{}, U{};
+    if (L && (s = lora_operands(*L, N, K, D, U))) return s;
     const int64_t M = X.rows;
-    if (workspace_bytes < ws_int8(M, K)) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_int8(M, K));
+    const size_t need = ws_int8(M, K) + (L ? ws_lora(M, K, D.rows) : 0);
+    if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
+    if (L) {
+        // the GEMM's operands are known before anything is launched: the activations are x itself
+        // or the prologue's rows at the start of the workspace, t follows
+        const bool direct = convrot_groupsize == 0 && X.dtype == QLIN_DT_F16 && X.ld % 8 == 0 && (uintptr_t)X.data % 16 == 0;
+        Carver lay = ws;
+        const f16* xo = (const f16*)lay.take((size_t)(M * K * 2));
+        (void)lay.take((size_t)M * 4);
+        float* t = (float*)lay.take(ws_lora(M, K, D.rows));
+        GemmF16Args a;
+        a.wkind = WO_INT8;
+        a.x = direct ? (const f16*)X.data : xo; a.ldx = direct ? X.ld : K;
+        a.M = M; a.N = N; a.K = K;
+        a.w = Q.data; a.ldw = Q.ld;
+        a.scale = scale->data; a.scale_dtype = scale->dtype; a.scale_stride = sst;
+        a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
+        a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+        a.lora.t = lora_t_final(t, M, K, D.rows); a.lora.up = U.data; a.lora.up_dt = U.dtype; a.lora.ld_up = U.ld;
+        a.lora.R = D.rows; a.lora.scale = L->scale;
+        if (M <= INT8_SMALLM_MAX_M || !gemm_f16_fuses_lora(a))
+            return fail(QLIN_EUNSUPPORTED, "the LoRA term is fused only into the large-M GEMM (rank a multiple of 8, "
+                                           "16-byte aligned lora_up rows)");
+        const float* tf = nullptr;
+        if ((s = hip_status(run_lora_t(lora_down_args(X, D, t), st, &tf), "lora down"))) return s;
+        if ((s = wo_activations(X, convrot_groupsize, ws, st, a.x, a.ldx, a.xexp))) return s;
+        return hip_status(run_gemm_f16(a, st), "int8 gemm with LoRA");
+    }
     // weight streaming for few rows: the VALU GEMV (one or two rows), then the small-M MFMA kernel.
     // With a rotation, the GEMV rotates and normalizes fp16 / bf16 rows itself (no prologue launch).
     if (M <= 2 && convrot_groupsize) {
@@ -526,6 +607,20 @@ qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
     a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
     return hip_status(run_gemm_f16(a, st), "int8 gemm");
+}
+
+qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                             const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    return int8_linear_impl(x, qdata, scale, bias, y, convrot_groupsize, nullptr, workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_int8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                  const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize,
+                                  const qlin_tensor* lora_down, const qlin_tensor* lora_up, float lora_scale,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    const LoraIn L{lora_down, lora_up, lora_scale};
+    return int8_linear_impl(x, qdata, scale, bias, y, convrot_groupsize, &L, workspace, workspace_bytes, stream);
 }
 
 // The GGUF linear over a given workspace (the caller's, or the no-allocation entry point's scratch).
@@ -630,10 +725,12 @@ qlin_status qlin_gguf_linear_noalloc(const qlin_tensor* x, const void* weight, i
     return gguf_linear_impl(x, weight, ggml_type, N, K, bias, y, ws, QLIN_NOALLOC_SCRATCH_BYTES, stream);
 }
 
-qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
-                             const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
-                             qlin_tensor* y, int bits, int group_size, int convrot_groupsize, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+// The A8 linear; with L, the LoRA term joins the epilogue of the decode-once DMA GEMM
+// (QLIN_EUNSUPPORTED, before anything is launched, when another kernel would take the call).
+static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                    const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                                    qlin_tensor* y, int bits, int group_size, int convrot_groupsize, const LoraIn* L,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
     if (bits != 4 && bits != 6) return fail(QLIN_EUNSUPPORTED, "bits=%d unsupported (4 or 6)", bits);
     Mat Q, X, Y, SR;
     qlin_status s = as_matrix(qdata, "qdata", Q);
@@ -668,12 +765,37 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     }
     int bdt;
     if ((s = check_bias(bias, N, bdt))) return s;
+    Mat D{}, U{};
+    if (L && (s = lora_operands(*L, N, K, D, U))) return s;
     const int64_t M = X.rows;
-    if (workspace_bytes < ws_w4a8(M, N, K))
-        return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, ws_w4a8(M, N, K));
+    const size_t need = ws_w4a8(M, N, K) + (L ? ws_lora(M, K, D.rows) : 0);
+    if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
+    // workspace: int8 activations, their scales, the decoded weight grid (M >= 1024), then LoRA's t
+    int8_t* qo = (int8_t*)ws.take((size_t)(M * K));
+    float* so = (float*)ws.take((size_t)M * 4);
+    GemmI8Args g;
+    g.xq = qo; g.ldx = K; g.sx = so;
+    g.M = M; g.N = N; g.K = K;
+    g.q = (const uint8_t*)Q.data; g.ldq = Q.ld; g.bits = bits; g.group_size = group_size;
+    g.s_rel = SR.data; g.s_rel_dtype = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype; g.ld_srel = SR.ld;
+    g.s_ch = (const float*)s_channel->data; g.codebook = cb;
+    g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
+    g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
+    if (a8_decode_once(M, K)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
+    float* t = nullptr;
+    if (L) {
+        t = (float*)ws.take(ws_lora(M, K, D.rows));
+        g.lora.t = lora_t_final(t, M, K, D.rows); g.lora.up = U.data; g.lora.up_dt = U.dtype; g.lora.ld_up = U.ld;
+        g.lora.R = D.rows; g.lora.scale = L->scale;
+        if (!gemm_i8_fuses_lora(g))
+            return fail(QLIN_EUNSUPPORTED, "the LoRA term is fused only into the decode-once GEMM (M >= 1024, rank a "
+                                           "multiple of 8, 16-byte aligned lora_up rows)");
+        const float* tf = nullptr;
+        if ((s = hip_status(run_lora_t(lora_down_args(X, D, t), st, &tf), "lora down"))) return s;
+    }
     PrologueArgs p;
     p.mode = PROLOGUE_A8;
     p.x_dtype = X.dtype;
@@ -682,20 +804,29 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
     p.M = M;
     p.K = (int)K;
     p.G = convrot_groupsize;
-    p.qo = (int8_t*)ws.take((size_t)(M * K));
+    p.qo = qo;
     p.ldo = K;
-    p.so = (float*)ws.take((size_t)M * 4);
+    p.so = so;
     if ((s = hip_status(run_prologue(p, st), "A8 prologue"))) return s;
-    GemmI8Args g;
-    g.xq = p.qo; g.ldx = K; g.sx = p.so;
-    g.M = M; g.N = N; g.K = K;
-    g.q = (const uint8_t*)Q.data; g.ldq = Q.ld; g.bits = bits; g.group_size = group_size;
-    g.s_rel = SR.data; g.s_rel_dtype = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype; g.ld_srel = SR.ld;
-    g.s_ch = (const float*)s_channel->data; g.codebook = cb;
-    g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
-    g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
-    if (a8_decode_once(M, K)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
-    return hip_status(run_gemm_i8(g, st), "A8 gemm");
+    return hip_status(run_gemm_i8(g, st), L ? "A8 gemm with LoRA" : "A8 gemm");
+}
+
+qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                             const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                             qlin_tensor* y, int bits, int group_size, int convrot_groupsize, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    return w4a8_linear_impl(x, qdata, s_rel, s_channel, codebook, bias, y, bits, group_size, convrot_groupsize, nullptr,
+                            workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                  const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                                  qlin_tensor* y, int bits, int group_size, int convrot_groupsize,
+                                  const qlin_tensor* lora_down, const qlin_tensor* lora_up, float lora_scale,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+    const LoraIn L{lora_down, lora_up, lora_scale};
+    return w4a8_linear_impl(x, qdata, s_rel, s_channel, codebook, bias, y, bits, group_size, convrot_groupsize, &L,
+                            workspace, workspace_bytes, stream);
 }
 
 qlin_status qlin_dequantize_gguf(const void* weight, int ggml_type, int64_t N, int64_t K, qlin_tensor* out,

@@ -13,6 +13,7 @@
 #include <utility>
 
 #include "qlin_internal.h"
+#include "lora_frag.h"
 #include "gguf_exact.h"
 
 namespace qlin {
@@ -455,7 +456,17 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
 // in registers after the read.  LDS rows: activations 128 bytes (8 chunks, chunk c of row r stored
 // at c ^ (r / 2) % 8), weights 64 bytes (4 chunks, at c ^ (r / 4) % 4): the 16 rows a 16-lane group
 // reads land in 16 distinct bank groups.
-template <int BMT, int STAGES>
+// LDU >= 0: the LoRA term of a.lora (up of dtype LDU) joins the epilogue: the accumulators become
+// their fp32 base values ldexp(acc, E) * scale + bias, then base + lora_scale * t up^T with t and up
+// staged through LDS (lora_tile_epilogue), the order of the separate LoRA kernel; the staged values
+// are final, so the output is rounded once.
+// Largest LoRA rank the 256 x 256, 3-stage kernel stages in its LDS (the row exponents aside).
+constexpr int wo_dma_lora_rank(int du) {
+    constexpr int lds = 3 * (256 * 64 * 2 + 256 * 64) - 256 * 4;
+    return du == DT_F32 ? lora_max_rank<DT_F32, 256, 256>(lds) : lora_max_rank<DT_BF16, 256, 256>(lds);
+}
+
+template <int BMT, int STAGES, int LDU = -1>
 __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
     constexpr int NT = 512, BNT = 256, KT = 64;
     // waves 2 (M) x 4 (N): each converted weight fragment feeds TI = 4 activation sub-tiles
@@ -564,14 +575,39 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
     const int cc = tid % CPR;
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, a.N - nc));
-    float cs[8], bv[8];
+    // the store loop's scales and bias (with a LoRA term the staged values are final)
+    constexpr int CB8 = LDU >= 0 ? 1 : 8;
+    float cs[CB8], bv[CB8];
+    if constexpr (LDU < 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const int64_t n = min(nc + e, a.N - 1);
-        cs[e] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-        bv[e] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+        for (int e = 0; e < 8; ++e) {
+            const int64_t n = min(nc + e, a.N - 1);
+            cs[e] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            bv[e] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+        }
     }
     const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
+    if constexpr (LDU >= 0) {
+        // the tile's row exponents at the end of LDS, past the LoRA chunks
+        constexpr int RC = lora_max_rank<LDU, BMT, BNT>((int)sizeof(smem) - BMT * 4);
+        static_assert(RC == wo_dma_lora_rank(LDU), "the host's rank limit must match");
+        int* erow = reinterpret_cast<int*>(smem + sizeof(smem) - BMT * 4);
+        __syncthreads();  // every wave is past the main loop: the operand buffers are free
+        if (tid < BMT) erow[tid] = a.xexp ? a.xexp[min(m0 + tid, a.M - 1)] : 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int64_t n = min(n0 + wn * WN + 32 * j + r32, a.N - 1);
+            const float csn = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            const float bvn = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    acc[i][j][r] = __builtin_ldexpf(acc[i][j][r], erow[wm * WM + 32 * i + 8 * (r / 4) + 4 * h + r % 4]) * csn + bvn;
+        }
+        lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(a.lora, smem, m0, n0, a.M, a.N, wm * WM, wn * WN, tid, lane, acc);
+    }
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
         __syncthreads();  // the operand buffers (or the previous pass) are no longer read
@@ -593,10 +629,15 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
             if (m >= a.M || ncount == 0) continue;
             const f32x4 v0 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc);
             const f32x4 v1 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc + 4);
-            const int e2 = a.xexp ? a.xexp[m] : 0;
             float v[8];
+            if constexpr (LDU >= 0) {  // staged final values
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
+                for (int e = 0; e < 8; ++e) v[e] = e < 4 ? v0[e] : v1[e - 4];
+            } else {
+                const int e2 = a.xexp ? a.xexp[m] : 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
+            }
             store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
         }
     }
@@ -812,9 +853,15 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
                          (uintptr_t)a.w % 16 == 0;
         auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
         if (vec && tiles(256, 256) >= 160) {
-            hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, a);
+            const dim3 grid((unsigned)tiles(256, 256));
+            if (!a.lora.t) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), grid, dim3(512), 0, st, a);
+            else if (a.lora.up_dt == DT_BF16) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3, DT_BF16>), grid, dim3(512), 0, st, a);
+            else if (a.lora.up_dt == DT_F16) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3, DT_F16>), grid, dim3(512), 0, st, a);
+            else if (a.lora.up_dt == DT_F32) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3, DT_F32>), grid, dim3(512), 0, st, a);
+            else return hipErrorInvalidValue;
             return hipGetLastError();
         }
+        if (a.lora.t) return hipErrorInvalidValue;  // only the 256 x 256 DMA kernel adds a LoRA term
         // grids of fewer than 160 tiles of 128 x 128: small tiles through a DMA ring, the one of
         // 64 x 128, 64 x 64, 32 x 128, 32 x 64 with the most workgroups that still run in one round
         // on the 256 CUs; the widest k-tile K allows (256 values per weight row per stage measured
@@ -886,6 +933,21 @@ __global__ __launch_bounds__(256) void gguf_row_exp_kernel(const uint8_t* __rest
 }
 
 }  // namespace
+
+// The operand conditions under which launch1 takes the 256 x 256 DMA kernel, and the LoRA operands it
+// reads with 16-byte loads.
+bool gemm_f16_fuses_lora(const GemmF16Args& a) {
+    if (a.wkind != WO_INT8 || a.M <= 0 || a.N <= 0) return false;
+    const bool vec = a.K % WBK == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 16 == 0 &&
+                     (uintptr_t)a.w % 16 == 0;
+    const int64_t tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256);
+    const LoraTile& L = a.lora;
+    const int es = L.up_dt == DT_F32 ? 4 : 2;
+    return vec && tiles >= 160 && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= wo_dma_lora_rank(L.up_dt) &&
+           (uintptr_t)L.t % 16 == 0 &&
+           (uintptr_t)L.up % 16 == 0 && (L.ld_up * es) % 16 == 0 &&
+           (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);
+}
 
 hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st) {
     if (a.M == 0 || a.N == 0) return hipSuccess;

@@ -11,6 +11,7 @@
 // registers.  4-bit codes: nibble plane [N, K/2]; 6-bit: the same plane plus a 2-bit plane
 // [N, K/4] (byte j holds bits 4-5 of codes 4j..4j+3).
 #include "qlin_internal.h"
+#include "lora_frag.h"
 
 namespace qlin {
 namespace {
@@ -621,7 +622,24 @@ __global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __re
 // step waits only for the oldest DMA in flight.  L2PF: one step earlier still, every 64-byte half
 // line of k-tile kt + STAGES is touched with a 4-byte DMA into a sink, so that the tile's own DMA
 // finds it in L2 (a second tile of look-ahead for the price of two instructions per thread).
-template <int BMT, int BNT, int BK, int STAGES, bool L2PF>
+// LDU >= 0: the LoRA term of p.lora (up of dtype LDU) joins the epilogue: the accumulators become
+// (the bits of) their fp32 base values, formed as below, then base + lora_scale * t up^T with t and
+// up staged through LDS (lora_tile_epilogue); the staged values are final, so the output is rounded
+// once.
+// Largest LoRA rank every decode-once DMA tile shape (256 x 256, 128 x 256, 128 x 128; 2 stages of
+// 128-value k-tiles) stages in its LDS, the row scales aside.
+template <int DU>
+constexpr int i8dma_lora_rank_t() {
+    constexpr int a = lora_max_rank<DU, 256, 256>(2 * (256 * 128 + 256 * 128) - 256 * 4);
+    constexpr int b = lora_max_rank<DU, 128, 256>(2 * (128 * 128 + 256 * 128) - 128 * 4);
+    constexpr int c = lora_max_rank<DU, 128, 128>(2 * (128 * 128 + 128 * 128) - 128 * 4);
+    return a < b ? (a < c ? a : c) : (b < c ? b : c);
+}
+constexpr int i8dma_lora_rank(int du) {
+    return du == DT_F32 ? i8dma_lora_rank_t<DT_F32>() : i8dma_lora_rank_t<DT_BF16>();
+}
+
+template <int BMT, int BNT, int BK, int STAGES, bool L2PF, int LDU = -1>
 __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int8_t* __restrict__ w8) {
     constexpr int NT = 512;
     constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
@@ -759,14 +777,44 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     const int cc = tid % CPR;
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, p.N - nc));
-    float sc[8], bv[8];
+    // the store loop's scales and bias (with a LoRA term the staged values are final)
+    constexpr int CB8 = LDU >= 0 ? 1 : 8;
+    float sc[CB8], bv[CB8];
+    if constexpr (LDU < 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const int64_t n = min(nc + e, p.N - 1);
-        sc[e] = p.s_ch[n];
-        bv[e] = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+        for (int e = 0; e < 8; ++e) {
+            const int64_t n = min(nc + e, p.N - 1);
+            sc[e] = p.s_ch[n];
+            bv[e] = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+        }
     }
     const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
+    if constexpr (LDU >= 0) {
+        // the tile's activation scales at the end of LDS, past the LoRA chunks
+        constexpr int RC = lora_max_rank<LDU, BMT, BNT>((int)sizeof(smem) - BMT * 4);
+        static_assert(RC >= i8dma_lora_rank(LDU), "the host's rank limit must fit every tile shape");
+        float* srow = reinterpret_cast<float*>(smem + sizeof(smem) - BMT * 4);
+        __syncthreads();  // every wave is past the main loop: the operand buffers are free
+        if (tid < BMT) srow[tid] = p.sx[min(m0 + tid, p.M - 1)];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int64_t n = min(n0 + wn * WN + 32 * j + r32, p.N - 1);
+            const float scn = p.s_ch[n];
+            const float bvn = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+#pragma clang fp contract(off)
+                    float base = (float)acc[i][j][r] * srow[wm * WM + 32 * i + 8 * (r / 4) + 4 * h + r % 4];
+                    base = base * scn;
+                    if (p.bias) base = base + bvn;
+                    acc[i][j][r] = __float_as_int(base);
+                }
+        }
+        lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(p.lora, smem, m0, n0, p.M, p.N, wm * WM, wn * WN, tid, lane, acc);
+    }
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
         __syncthreads();  // the operand buffers (or the previous pass) are no longer read
@@ -788,10 +836,13 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
             if (m >= p.M || ncount == 0) continue;
             const i32x4 a0 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc);
             const i32x4 a1 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc + 4);
-            const float sxm = p.sx[m];
             float v[8];
-            {
+            if constexpr (LDU >= 0) {  // staged final values
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = __int_as_float(e < 4 ? a0[e] : a1[e - 4]);
+            } else {
 #pragma clang fp contract(off)
+                const float sxm = p.sx[m];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     float val = (float)(e < 4 ? a0[e] : a1[e - 4]) * sxm;
@@ -923,6 +974,7 @@ inline bool a8_smallm_ok(const GemmI8Args& p) {
 template <int BITS, bool CB, typename TSrel>
 hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if (p.lora.t && !gemm_i8_fuses_lora(p)) return hipErrorInvalidValue;  // only the DMA GEMM adds LoRA
     if (a8_smallm_ok(p)) {
         const dim3 grid((unsigned)((p.N + 15) / 16)), block(512);
         if (p.M <= 16) hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 1>), grid, block, 0, st, p);
@@ -938,17 +990,26 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
         auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
+        // LoRA term in the epilogue by up dtype (none: -1)
+        const int ldu = !p.lora.t ? -1 : p.lora.up_dt;
+        auto go = [&]<int BMV, int BNV>() {
+            const dim3 grid((unsigned)tiles(BMV, BNV));
+            switch (ldu) {
+                case -1: hipLaunchKernelGGL((gemm_i8dma_kernel<BMV, BNV, 128, 2, false>), grid, dim3(512), 0, st, p, p.w8); break;
+                case DT_BF16: hipLaunchKernelGGL((gemm_i8dma_kernel<BMV, BNV, 128, 2, false, DT_BF16>), grid, dim3(512), 0, st, p, p.w8); break;
+                case DT_F16: hipLaunchKernelGGL((gemm_i8dma_kernel<BMV, BNV, 128, 2, false, DT_F16>), grid, dim3(512), 0, st, p, p.w8); break;
+                case DT_F32: hipLaunchKernelGGL((gemm_i8dma_kernel<BMV, BNV, 128, 2, false, DT_F32>), grid, dim3(512), 0, st, p, p.w8); break;
+            }
+        };
+        if (ldu != -1 && ldu != DT_BF16 && ldu != DT_F16 && ldu != DT_F32) return hipErrorInvalidValue;
         if (tiles(256, 256) >= 192)
-            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2, false>), dim3((unsigned)tiles(256, 256)), dim3(512), 0, st, p,
-                               p.w8);
+            go.template operator()<256, 256>();
         // 128 x 256 also when it fits one round on the 256 CUs and 128 x 128 would not: one round of
         // the larger tile beats 1.25 rounds of the smaller (M1024 K13824 N5120: 150.6 vs 157.1 us)
         else if (tiles(128, 256) >= 192 || (tiles(128, 256) <= 256 && tiles(128, 128) > 256))
-            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2, false>), dim3((unsigned)tiles(128, 256)), dim3(512), 0, st, p,
-                               p.w8);
+            go.template operator()<128, 256>();
         else
-            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 128, 128, 2, false>), dim3((unsigned)tiles(128, 128)), dim3(512), 0, st, p,
-                               p.w8);
+            go.template operator()<128, 128>();
         return hipGetLastError();
     }
     // large tiles when the grid still fills the GPU and one scale covers each row's k-tile
@@ -993,6 +1054,18 @@ hipError_t launch_grid(const GemmI8Args& p, hipStream_t st) {
 }
 
 }  // namespace
+
+// The conditions under which launch_o takes the decode-once DMA GEMM, and the LoRA operands it reads
+// with 16-byte loads.
+bool gemm_i8_fuses_lora(const GemmI8Args& p) {
+    const bool dma = p.w8 && a8_decode_once(p.M, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
+                     (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0 && !a8_smallm_ok(p);
+    const LoraTile& L = p.lora;
+    const int es = L.up_dt == DT_F32 ? 4 : 2;
+    return dma && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= i8dma_lora_rank(L.up_dt) &&
+           (uintptr_t)L.t % 16 == 0 && (uintptr_t)L.up % 16 == 0 &&
+           (L.ld_up * es) % 16 == 0 && (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);
+}
 
 bool a8_grid_supported(const GemmI8Args& p) {
     return (p.bits == 4 || (p.bits == 6 && !p.codebook)) && p.K % 64 == 0 && p.group_size % 64 == 0 &&

@@ -18,121 +18,11 @@
 //     in LDS; the tile is staged through LDS, then each output is read, increased by scale * acc
 //     in fp32 and rounded once to y's dtype, 8 outputs per thread.  When the base linear left its
 //     output in an fp32 buffer (`base`), that is read instead of y, so a 16-bit y is rounded once.
-#include "qlin_internal.h"
+#include "lora_frag.h"
 
 namespace qlin {
 
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ __bf16 to_bf16(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16_bits(f)); }
-
-// hi = bf16(v), lo = bf16(v - hi) (v - hi is exact in fp32)
-__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint16_t hb = f32_to_bf16_bits(v[i]);
-        hi[i] = __builtin_bit_cast(__bf16, hb);
-        lo[i] = to_bf16(v[i] - bf16_bits_to_f32(hb));
-    }
-}
-
-// Raw storage of 8 consecutive values of one operand (16 bytes for f16/bf16, 32 for f32), loaded
-// ahead of use so that several steps of loads are in flight.
-template <int DT>
-struct Raw8 {
-    u32x4 v[DT == DT_F32 ? 2 : 1];
-};
-
-// VEC (16-byte loads) requires cols % 8 == 0 and cols >= 8, so with k a multiple of 8 a piece is
-// either wholly inside the row or wholly past its end: the load is issued unconditionally from a
-// clamped column, and the caller zeroes a past-the-end piece when it uses it (a load behind a
-// lane-dependent branch, or a select right after it, would be waited for on the spot).
-template <int DT, bool VEC>
-__device__ __forceinline__ Raw8<DT> raw_load(const void* base, int64_t ld, int64_t row, int64_t k, int64_t cols) {
-    Raw8<DT> r;
-    if constexpr (VEC) {
-        const int64_t kc = min(k, cols - 8);
-        if constexpr (DT == DT_F32) {
-            const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(base) + row * ld + kc);
-            r.v[0] = p[0];
-            r.v[1] = p[1];
-        } else {
-            r.v[0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + row * ld + kc);
-        }
-        return r;  // a piece past the end holds the row's last 8 values: the caller zeroes it at use
-    } else {
-    float f[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = k + i < cols ? load_rt(base, DT, row * ld + k + i) : 0.0f;
-    if constexpr (DT == DT_F32) {
-        r.v[0] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
-        r.v[1] = u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])};
-    } else {
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = DT == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)f[2 * i])
-                                             : (uint32_t)f32_to_bf16_bits(f[2 * i]);
-            const uint32_t hi = DT == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)f[2 * i + 1])
-                                             : (uint32_t)f32_to_bf16_bits(f[2 * i + 1]);
-            w[i] = lo | (hi << 16);  // the loaded values are exact in the storage type
-        }
-        r.v[0] = u32x4{w[0], w[1], w[2], w[3]};
-    }
-    return r;
-    }
-}
-
-template <int DT>
-__device__ __forceinline__ Raw8<DT> zero_unless(const Raw8<DT>& r, bool keep) {
-    Raw8<DT> z;
-#pragma unroll
-    for (int j = 0; j < (DT == DT_F32 ? 2 : 1); ++j) z.v[j] = keep ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
-    return z;
-}
-
-template <int DT>
-__device__ __forceinline__ void raw_to_f32(const Raw8<DT>& r, float* f) {
-    if constexpr (DT == DT_F32) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[i] = __uint_as_float(r.v[0][i]);
-            f[4 + i] = __uint_as_float(r.v[1][i]);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = bits_to_f32_rt(r.v[0][i] & 0xFFFFu, DT);
-            f[2 * i + 1] = bits_to_f32_rt(r.v[0][i] >> 16, DT);
-        }
-    }
-}
-
-// acc += A . B over one 16-value step from raw loads; bf16 operands are used as loaded.
-template <int DA, int DB>
-__device__ __forceinline__ void mfma_raw(const Raw8<DA>& ra, const Raw8<DB>& rb, f32x16& acc) {
-    constexpr bool SA = DA != DT_BF16, SB = DB != DT_BF16;
-    bf16x8 ah, al, bh, bl;
-    if constexpr (SA) {
-        float f[8];
-        raw_to_f32(ra, f);
-        split8(f, ah, al);
-    } else {
-        ah = __builtin_bit_cast(bf16x8, ra.v[0]);
-    }
-    if constexpr (SB) {
-        float f[8];
-        raw_to_f32(rb, f);
-        split8(f, bh, bl);
-    } else {
-        bh = __builtin_bit_cast(bf16x8, rb.v[0]);
-    }
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
-    if constexpr (SA) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
-    if constexpr (SB) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
-}
 
 // 16-value steps whose loads are in flight together: 8 x (1 + NH) 16-byte pieces for 16-bit
 // operands at NH = 1, fewer with two rank halves or an fp32 operand (8 registers per piece)
@@ -380,14 +270,13 @@ __global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
 
 }  // namespace
 
-hipError_t run_lora(const LoraArgs& a, hipStream_t st) {
-    if (a.M == 0 || a.N == 0) return hipSuccess;
+hipError_t run_lora_t(const LoraArgs& a, hipStream_t st, const float** t_final) {
     if (a.R < 1 || !a.t) return hipErrorInvalidValue;
     if (a.S < 1 || a.S > 8) return hipErrorInvalidValue;
     const int nh = a.R <= 32 ? 1 : 2;  // rank halves per workgroup
     const dim3 dgrid((unsigned)((a.R + 32 * nh - 1) / (32 * nh)), (unsigned)((a.M + 31) / 32), (unsigned)a.S);
     bool ok = false;
-    const bool vd = a.vec_x && a.vec_down, vu = a.vec_up;
+    const bool vd = a.vec_x && a.vec_down;
     auto down = [&]<int DX, int DD>() {
         if (a.x_dt == DX && a.down_dt == DD) {
             if (vd && nh == 1) hipLaunchKernelGGL((lora_down_kernel<DX, DD, true, 1>), dgrid, dim3(256), 0, st, a);
@@ -408,13 +297,25 @@ hipError_t run_lora(const LoraArgs& a, hipStream_t st) {
     if (!ok) return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    LoraArgs u = a;  // the up kernel reads one t: the partials' sum when K was split
+    *t_final = a.t;  // one t: the partials' sum when K was split
     if (a.S > 1) {
         const int64_t n = a.M * a.R;
-        u.t = a.t + (int64_t)a.S * n;
-        hipLaunchKernelGGL(lora_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.t, a.S, n, u.t);
+        float* sum = a.t + (int64_t)a.S * n;
+        hipLaunchKernelGGL(lora_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.t, a.S, n, sum);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        *t_final = sum;
     }
+    return hipSuccess;
+}
+
+hipError_t run_lora(const LoraArgs& a, hipStream_t st) {
+    if (a.M == 0 || a.N == 0) return hipSuccess;
+    LoraArgs u = a;  // the up kernel reads the final t
+    const float* tf = nullptr;
+    hipError_t e = run_lora_t(a, st, &tf);
+    if (e != hipSuccess) return e;
+    u.t = const_cast<float*>(tf);
+    const bool vu = a.vec_up;
     const dim3 ugrid((unsigned)((a.N + UP_T - 1) / UP_T), (unsigned)((a.M + UP_T - 1) / UP_T));
 #define QLIN_LORA_UP(DU)                                                                              \
     if (vu) hipLaunchKernelGGL((lora_up_kernel<DU, true>), ugrid, dim3(256), 0, st, u);               \

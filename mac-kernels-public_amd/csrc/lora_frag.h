@@ -1,0 +1,216 @@
+// LoRA operand fragments for v_mfma_f32_32x32x16_bf16: raw 8-value loads of f32 / f16 / bf16 rows and
+// the exact bf16 split of every operand that is not already bf16 (hi = bf16(v), lo = bf16(v - hi);
+// bf16 x bf16 products are exact in fp32, hi + lo carries 16 significand bits, the lo x lo term is
+// dropped).  Shared by the LoRA kernels (lora.hip) and the GEMM epilogues that add the LoRA term of
+// their own output tile (gemm_f16.hip, gemm_i8.hip).
+#pragma once
+#include <utility>
+
+#include "qlin_internal.h"
+
+namespace qlin {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ __bf16 to_bf16(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16_bits(f)); }
+
+// hi = bf16(v), lo = bf16(v - hi) (v - hi is exact in fp32)
+__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint16_t hb = f32_to_bf16_bits(v[i]);
+        hi[i] = __builtin_bit_cast(__bf16, hb);
+        lo[i] = to_bf16(v[i] - bf16_bits_to_f32(hb));
+    }
+}
+
+// Raw storage of 8 consecutive values of one operand (16 bytes for f16/bf16, 32 for f32), loaded
+// ahead of use so that several steps of loads are in flight.
+template <int DT>
+struct Raw8 {
+    u32x4 v[DT == DT_F32 ? 2 : 1];
+};
+
+// VEC (16-byte loads) requires cols % 8 == 0 and cols >= 8, so with k a multiple of 8 a piece is
+// either wholly inside the row or wholly past its end: the load is issued unconditionally from a
+// clamped column, and the caller zeroes a past-the-end piece when it uses it (a load behind a
+// lane-dependent branch, or a select right after it, would be waited for on the spot).
+template <int DT, bool VEC>
+__device__ __forceinline__ Raw8<DT> raw_load(const void* base, int64_t ld, int64_t row, int64_t k, int64_t cols) {
+    Raw8<DT> r;
+    if constexpr (VEC) {
+        const int64_t kc = min(k, cols - 8);
+        if constexpr (DT == DT_F32) {
+            const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(base) + row * ld + kc);
+            r.v[0] = p[0];
+            r.v[1] = p[1];
+        } else {
+            r.v[0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + row * ld + kc);
+        }
+        return r;  // a piece past the end holds the row's last 8 values: the caller zeroes it at use
+    } else {
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = k + i < cols ? load_rt(base, DT, row * ld + k + i) : 0.0f;
+    if constexpr (DT == DT_F32) {
+        r.v[0] = u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+        r.v[1] = u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])};
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = DT == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)f[2 * i])
+                                             : (uint32_t)f32_to_bf16_bits(f[2 * i]);
+            const uint32_t hi = DT == DT_F16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)f[2 * i + 1])
+                                             : (uint32_t)f32_to_bf16_bits(f[2 * i + 1]);
+            w[i] = lo | (hi << 16);  // the loaded values are exact in the storage type
+        }
+        r.v[0] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    return r;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> zero_unless(const Raw8<DT>& r, bool keep) {
+    Raw8<DT> z;
+#pragma unroll
+    for (int j = 0; j < (DT == DT_F32 ? 2 : 1); ++j) z.v[j] = keep ? r.v[j] : u32x4{0u, 0u, 0u, 0u};
+    return z;
+}
+
+template <int DT>
+__device__ __forceinline__ void raw_to_f32(const Raw8<DT>& r, float* f) {
+    if constexpr (DT == DT_F32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[i] = __uint_as_float(r.v[0][i]);
+            f[4 + i] = __uint_as_float(r.v[1][i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = bits_to_f32_rt(r.v[0][i] & 0xFFFFu, DT);
+            f[2 * i + 1] = bits_to_f32_rt(r.v[0][i] >> 16, DT);
+        }
+    }
+}
+
+// acc += A . B over one 16-value step from raw loads; bf16 operands are used as loaded.
+template <int DA, int DB>
+__device__ __forceinline__ void mfma_raw(const Raw8<DA>& ra, const Raw8<DB>& rb, f32x16& acc) {
+    constexpr bool SA = DA != DT_BF16, SB = DB != DT_BF16;
+    bf16x8 ah, al, bh, bl;
+    if constexpr (SA) {
+        float f[8];
+        raw_to_f32(ra, f);
+        split8(f, ah, al);
+    } else {
+        ah = __builtin_bit_cast(bf16x8, ra.v[0]);
+    }
+    if constexpr (SB) {
+        float f[8];
+        raw_to_f32(rb, f);
+        split8(f, bh, bl);
+    } else {
+        bh = __builtin_bit_cast(bf16x8, rb.v[0]);
+    }
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+    if constexpr (SA) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+    if constexpr (SB) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+}
+
+// LoRA term of a GEMM workgroup's BMT x BNT output tile, added by its waves to accumulators that
+// already hold their fp32 base values (after bias).  The whole rank (R <= RC) is staged at once: all
+// NT threads load the tile's t rows [BMT x RC] (fp32) and up rows [BNT x RC] into LDS together (every
+// load in flight at once, zeros past R; t is multiplied by L.scale on its way into LDS), then each
+// wave runs the bf16 MFMAs of (scale t) . up^T on split operands (mfma_raw) for its TI x TJ sub-tiles
+// of 32 x 32 straight into acc[i][j] (fp32 values, or their bits in int32 registers), so the base
+// value is the MFMAs' accumulator input.  A wave's sub-tile (i, j) covers tile rows
+// wr0 + 32 i .. + 31 and columns wc0 + 32 j .. + 31, in the MFMA C layout (lane l, register r: row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32).  Requires 8 <= R <= RC, R % 8 == 0 and
+// 16-byte aligned t and up rows (t row stride R); lds must hold lora_lds_bytes<DU, BMT, BNT, RC>().
+// No loop here has a run-time trip count, so the caller's accumulators stay in registers.  Starts
+// and ends with a workgroup barrier.
+template <int DU, int RC>
+constexpr int lora_t_stride() { return RC + 4; }  // floats; the 4-float pad spreads the rows over banks
+template <int DU, int RC>
+constexpr int lora_u_stride() { return DU == DT_F32 ? RC + 4 : RC + 8; }  // elements
+template <int DU, int BMT, int BNT, int RC>
+constexpr int lora_lds_bytes() {
+    return BMT * lora_t_stride<DU, RC>() * 4 + BNT * lora_u_stride<DU, RC>() * (DU == DT_F32 ? 4 : 2);
+}
+
+// Ranks a GEMM epilogue with `lds_bytes` of LDS (less what it keeps for itself) can stage at once.
+template <int DU, int BMT, int BNT>
+constexpr int lora_max_rank(int lds_bytes) {
+    return lora_lds_bytes<DU, BMT, BNT, 64>() <= lds_bytes ? 64 : lora_lds_bytes<DU, BMT, BNT, 32>() <= lds_bytes ? 32 : 0;
+}
+
+template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, typename AccT>
+__device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* lds, int64_t m0, int64_t n0, int64_t M,
+                                                   int64_t N, int wr0, int wc0, int tid, int lane, AccT (&acc)[TI][TJ]) {
+    static_assert(sizeof(AccT) == sizeof(f32x16), "32 x 32 accumulators: fp32 values or their int32 bits");
+    constexpr int TW = lora_t_stride<DU, RC>(), UW = lora_u_stride<DU, RC>();
+    constexpr int ES = DU == DT_F32 ? 4 : 2, UPP = 16 / ES;   // up element size, elements per 16 bytes
+    constexpr int TP = BMT * RC / 4 / NT, UP = BNT * RC / UPP / NT;  // 16-byte pieces per thread
+    static_assert(TP * 4 * NT == BMT * RC && UP * UPP * NT == BNT * RC, "chunk must split into whole rounds");
+    float* ts = reinterpret_cast<float*>(lds);
+    uint8_t* us = lds + BMT * TW * 4;
+    const int r32 = lane & 31, h = lane >> 5;
+    {
+        constexpr int64_t c0 = 0;
+        u32x4 tv[TP], uv[UP];
+#pragma unroll
+        for (int i = 0; i < TP; ++i) {
+            const int p = tid + NT * i, row = p / (RC / 4), c = 4 * (p % (RC / 4));
+            const int64_t m = min(m0 + row, M - 1), k = min<int64_t>(c0 + c, L.R - 4);
+            tv[i] = *reinterpret_cast<const u32x4*>(L.t + m * L.R + k);
+        }
+#pragma unroll
+        for (int i = 0; i < UP; ++i) {
+            const int p = tid + NT * i, row = p / (RC / UPP), c = UPP * (p % (RC / UPP));
+            const int64_t n = min(n0 + row, N - 1), k = min<int64_t>(c0 + c, L.R - UPP);
+            uv[i] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(L.up) + (n * L.ld_up + k) * ES);
+        }
+        __syncthreads();  // every wave is done with the LDS the chunk overwrites
+#pragma unroll
+        for (int i = 0; i < TP; ++i) {
+            const int p = tid + NT * i, row = p / (RC / 4), c = 4 * (p % (RC / 4));
+            f32x4 v = __builtin_bit_cast(f32x4, tv[i]) * L.scale;
+            if (c0 + c >= L.R) v = f32x4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<f32x4*>(ts + row * TW + c) = v;
+        }
+#pragma unroll
+        for (int i = 0; i < UP; ++i) {
+            const int p = tid + NT * i, row = p / (RC / UPP), c = UPP * (p % (RC / UPP));
+            *reinterpret_cast<u32x4*>(us + (row * UW + c) * ES) = c0 + c < L.R ? uv[i] : u32x4{0u, 0u, 0u, 0u};
+        }
+        __syncthreads();
+        // compile-time sub-tile indices, so that every access to the caller's accumulators is constant
+        auto subtile = [&]<int I, int J>() {
+            __builtin_amdgcn_sched_barrier(0);  // one sub-tile's fragments in registers at a time
+            f32x16 lo = __builtin_bit_cast(f32x16, acc[I][J]);
+            const float* ta = ts + (wr0 + 32 * I + r32) * TW + 8 * h;
+            const uint8_t* ub = us + ((wc0 + 32 * J + r32) * UW + 8 * h) * ES;
+#pragma unroll
+            for (int q = 0; q < RC / 16; ++q) {
+                Raw8<DT_F32> ra;
+                ra.v[0] = *reinterpret_cast<const u32x4*>(ta + 16 * q);
+                ra.v[1] = *reinterpret_cast<const u32x4*>(ta + 16 * q + 4);
+                Raw8<DU> rb;
+#pragma unroll
+                for (int v = 0; v < (DU == DT_F32 ? 2 : 1); ++v)
+                    rb.v[v] = *reinterpret_cast<const u32x4*>(ub + (16 * q) * ES + 16 * v);
+                mfma_raw<DT_F32, DU>(ra, rb, lo);
+            }
+            acc[I][J] = __builtin_bit_cast(AccT, lo);
+        };
+        [&]<int... IJ>(std::integer_sequence<int, IJ...>) {
+            (subtile.template operator()<IJ / TJ, IJ % TJ>(), ...);
+        }(std::make_integer_sequence<int, TI * TJ>{});
+    }
+    __syncthreads();  // LDS free for the caller's staging
+}
+
+}  // namespace qlin

@@ -126,6 +126,18 @@ hipError_t run_gguf_gemv(const GgufGemvArgs& a, hipStream_t st);
 
 // ---- weight-only fp16 MFMA tile GEMM (gemm_f16.hip) ----
 enum { WO_INT8 = 0, WO_GGUF = 1 };
+// LoRA term added by a GEMM epilogue to its own output tile: y = dtype(base + scale * t up^T), t the
+// fp32 low-rank activation [M, R] (row stride R), up [N, R] (f32 / f16 / bf16, row stride ld_up).
+// t == nullptr: no LoRA term.
+struct LoraTile {
+    const float* t = nullptr;
+    const void* up = nullptr;
+    int up_dt = DT_BF16;
+    int64_t ld_up = 0;
+    int64_t R = 0;
+    float scale = 1.0f;
+};
+
 struct GemmF16Args {
     int wkind = WO_INT8;
     int gguf_type = 0;
@@ -144,8 +156,11 @@ struct GemmF16Args {
     void* y = nullptr;
     int y_dtype = DT_F16;
     int64_t ldy = 0;
+    LoraTile lora;                   // INT8, 256 x 256 DMA tiles only (gemm_f16_fuses_lora)
 };
 hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st);
+// Whether run_gemm_f16 takes a kernel that adds a.lora in its epilogue for these operands.
+bool gemm_f16_fuses_lora(const GemmF16Args& a);
 
 // GGUF per-row weight exponent: e[n] = exponent bounding max |w[n, :]| (gemm_f16.hip).
 hipError_t run_gguf_row_exp(int type, const uint8_t* w, int64_t N, int64_t K, int32_t* e, hipStream_t st);
@@ -171,7 +186,10 @@ struct GemmI8Args {
     int y_dtype = DT_F16;
     int64_t ldy = 0;
     int8_t* w8 = nullptr;            // workspace for the decoded int8 grid [N, K] (decode-once path)
+    LoraTile lora;                   // decode-once DMA GEMM only (gemm_i8_fuses_lora)
 };
+// Whether run_gemm_i8 takes a kernel that adds p.lora in its epilogue for these operands.
+bool gemm_i8_fuses_lora(const GemmI8Args& p);
 // Activation rows from which the A8 linear decodes the weight grid once into the workspace
 // (N * K bytes) instead of once per 256-row tile inside the GEMM.
 inline bool a8_decode_once(int64_t M, int64_t K) { return M >= 1024 && K % 128 == 0; }
@@ -203,6 +221,8 @@ struct LoraArgs {
     int64_t ldb = 0;
 };
 hipError_t run_lora(const LoraArgs& a, hipStream_t st);
+// t = x down^T alone (the K-split partials and their sum); *t_final receives the [M, R] result.
+hipError_t run_lora_t(const LoraArgs& a, hipStream_t st, const float** t_final);
 
 // Residual epilogue (epilogue.hip): y = dtype(res + rscale[n] * base), base fp32 [M, N].
 struct ResidualArgs {

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(_HERE, "libqlin.so")
 QLIN_OK, QLIN_EUNSUPPORTED, QLIN_EINVAL, QLIN_EHIP, QLIN_EWORKSPACE = 0, 1, 2, 3, 4
 DT_F32, DT_F16, DT_BF16, DT_I8, DT_U8, DT_I32, DT_E4M3 = 0, 1, 2, 3, 4, 5, 6
 OP_INT8_LINEAR, OP_W4A8_LINEAR, OP_GGUF_LINEAR, OP_LORA, OP_INT8_GRAD_INPUT, OP_W4A8_GRAD_INPUT = 0, 1, 2, 3, 4, 5
+OP_INT8_LINEAR_LORA, OP_W4A8_LINEAR_LORA = 6, 7
 
 _TORCH_DT = {
     torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.int8: DT_I8,
@@ -31,7 +32,7 @@ EXPORTS = (
     "qlin_version", "qlin_status_string", "qlin_last_error", "qlin_workspace_size", "qlin_query",
     "qlin_int8_linear", "qlin_w4a8_linear", "qlin_gguf_linear", "qlin_gguf_linear_noalloc", "qlin_dequantize_gguf",
     "qlin_dequantize_int8", "qlin_dequantize_w4a8", "qlin_quantize_act_int8", "qlin_lora_apply", "qlin_lora_apply_base",
-    "qlin_residual_epilogue",
+    "qlin_residual_epilogue", "qlin_int8_linear_lora", "qlin_w4a8_linear_lora",
     "qlin_int8_linear_grad_input", "qlin_w4a8_linear_grad_input",
 )
 
@@ -68,6 +69,8 @@ def load():
         "qlin_query": (I, [I, I64, I64, I64, I, I, I]),
         "qlin_int8_linear": (I, [T, T, T, T, T, I, P, SZ, P]),
         "qlin_w4a8_linear": (I, [T, T, T, T, T, T, T, I, I, I, P, SZ, P]),
+        "qlin_int8_linear_lora": (I, [T, T, T, T, T, I, T, T, ctypes.c_float, P, SZ, P]),
+        "qlin_w4a8_linear_lora": (I, [T, T, T, T, T, T, T, I, I, I, T, T, ctypes.c_float, P, SZ, P]),
         "qlin_gguf_linear": (I, [T, P, I, I64, I64, T, T, P, SZ, P]),
         "qlin_gguf_linear_noalloc": (I, [T, P, I, I64, I64, T, T, P]),
         "qlin_dequantize_gguf": (I, [P, I, I64, I64, T, P]),

@@ -96,17 +96,36 @@ def _finish(op, lora, res, x2, y, yb):
     _lib.check(st, op)
 
 
-def _apply_lora(op, lora, x2, y, base=None):
-    """y = dtype(base + scale * (x2 @ down^T) @ up^T) on the GPU after the base linear; `base` is the
-    fp32 buffer from _base_out, or y itself (updated in place)."""
-    if lora is None or y.numel() == 0:
-        return
+def _lora_operands(op, lora):
     down, up, scale = lora
     _check_device(op, down, up)
     if down.stride(-1) != 1:
         down = down.contiguous()
     if up.stride(-1) != 1:
         up = up.contiguous()
+    return down, up, scale
+
+
+def _fused_lora(op, lora, res, x2, run):
+    """Runs the linear with the LoRA term in its GEMM epilogue when no residual follows: `run(down, up,
+    scale)` returns the entry point's status.  True when it ran; False when the entry point declined
+    (QLIN_EUNSUPPORTED: the rows take a kernel without the fused term), and the caller runs the
+    plain linear and the separate LoRA kernels."""
+    if lora is None or res is not None:
+        return False
+    st = run(*_lora_operands(op, lora))
+    if st == _lib.QLIN_EUNSUPPORTED:
+        return False
+    _lib.check(st, op)
+    return True
+
+
+def _apply_lora(op, lora, x2, y, base=None):
+    """y = dtype(base + scale * (x2 @ down^T) @ up^T) on the GPU after the base linear; `base` is the
+    fp32 buffer from _base_out, or y itself (updated in place)."""
+    if lora is None or y.numel() == 0:
+        return
+    down, up, scale = _lora_operands(op, lora)
     r = down.shape[0]
     ws = _workspace(_lib.OP_LORA, x2.shape[0], up.shape[0], x2.shape[1], r, x2)
     L = _lib.load()
@@ -194,8 +213,17 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     g = int(convrot_groupsize) if convrot else 0
     s = scale.reshape(-1) if scale.numel() in (1, n) else scale
     b = _bias(bias, n)
-    ws = _workspace(_lib.OP_INT8_LINEAR, x2.shape[0], n, k, g, x2)
     L = _lib.load()
+    m = x2.shape[0]
+    if m > 16:
+        def run(down, up, lscale):
+            wsl = _workspace(_lib.OP_INT8_LINEAR_LORA, m, n, k, down.shape[0], x2)
+            return L.qlin_int8_linear_lora(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(y), g,
+                                           _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(),
+                                           _lib.stream_of(x.device))
+        if _fused_lora(op, lora, res, x2, run):
+            return y.reshape(shape)
+    ws = _workspace(_lib.OP_INT8_LINEAR, x2.shape[0], n, k, g, x2)
     yb = _base_out(lora, y, res)
     st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(yb), g,
                             ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
@@ -267,8 +295,18 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     cb = None if codebook is None else codebook.to(torch.float32).contiguous()
     sch = s_channel.reshape(-1).to(torch.float32).contiguous()
     b = _bias(bias, n)
-    ws = _workspace(_lib.OP_W4A8_LINEAR, x2.shape[0], n, k, bits, x2)
     L = _lib.load()
+    m = x2.shape[0]
+    if m >= 1024:
+        def run(down, up, lscale):
+            wsl = _workspace(_lib.OP_W4A8_LINEAR_LORA, m, n, k, down.shape[0], x2)
+            return L.qlin_w4a8_linear_lora(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
+                                           _lib.desc(b), _lib.desc(y), bits, int(group_size), int(convrot_groupsize or 0),
+                                           _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(),
+                                           _lib.stream_of(x.device))
+        if _fused_lora(op, lora, res, x2, run):
+            return y.reshape(shape)
+    ws = _workspace(_lib.OP_W4A8_LINEAR, x2.shape[0], n, k, bits, x2)
     yb = _base_out(lora, y, res)
     st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
                             _lib.desc(b), _lib.desc(yb), bits, int(group_size), int(convrot_groupsize or 0),

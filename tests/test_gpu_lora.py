@@ -205,3 +205,116 @@ def test_lora_cancelling_the_weight_is_exactly_zero(odt, m):
     want = (xb.double() @ d.double().T).to(odt)
     assert torch.isfinite(yb.float()).all()
     assert torch.equal(yb.cpu(), want)
+
+
+# ------------------------------------------------------------------------------------------------
+# LoRA fused into the large-M GEMMs (qlin_int8_linear_lora / qlin_w4a8_linear_lora): the GEMM adds
+# scale * t up^T to its own output tile after the bias and rounds once.  A zero residual keeps the
+# same single rounding through the separate kernels (fp32 base, LoRA, residual epilogue), so the
+# two paths are compared output for output, besides the reference's bars.
+# ------------------------------------------------------------------------------------------------
+
+def _close_or_equal(fused, plain, what):
+    """The fused GEMM adds (scale t) up^T into the base inside its MFMAs, the separate kernels form
+    base + scale (t up^T): the same terms with fp32 roundings in another order (a few fp32 ulps
+    apart), rounded once to the output dtype.  So the outputs agree to the rounding step of the
+    output dtype (two steps at a power of two) plus 1e-5 of the output's scale for results that
+    cancel towards 0."""
+    f, p = fused.float(), plain.float()
+    eps = torch.finfo(fused.dtype).eps
+    diff = (f - p).abs()
+    lim = 2 * eps * torch.maximum(f.abs(), p.abs()) + 1e-5 * p.abs().max()
+    worst = (diff - lim).max().item()
+    assert worst <= 0, f"{what}: fused and separate LoRA differ beyond the output rounding (excess {worst:.3e})"
+
+
+@pytest.mark.parametrize("r,fdt,xdt", [(64, torch.bfloat16, torch.bfloat16), (16, torch.float16, torch.float16),
+                                       (200, torch.float32, torch.bfloat16), (8, torch.bfloat16, torch.float32)])
+def test_int8_lora_fused_into_gemm(r, fdt, xdt):
+    """M2048 N5120: 160 tiles of 256 x 256, the GEMM that carries the LoRA term."""
+    Q = qlin()
+    m, n, k, g = 2048, 5120, 1024, 128
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(20)) * 0.02).numpy()
+    qn, sn = qz().quantize_int8_convrot_weight(w, g)
+    q, s = torch.from_numpy(qn).to(DEV), torch.from_numpy(sn).reshape(-1).to(DEV)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(21)) * 0.5).to(xdt).to(DEV)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(22)) * 0.1).half().to(DEV)
+    down, up = factors(n, k, r, fdt, fdt, seed=23)
+    kw = dict(convrot=True, convrot_groupsize=g, lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.8)
+    base = Q.int8_linear(x, q, s, b, convrot=True, convrot_groupsize=g)
+    y = Q.int8_linear(x, q, s, b, **kw)
+    plain = Q.int8_linear(x, q, s, b, residual=torch.zeros(m, n, dtype=y.dtype, device=DEV), **kw)
+    torch.cuda.synchronize()
+    _close_or_equal(y, plain, f"int8 r={r} {fdt}")
+    ref = side_ref(x.cpu(), down, up, 0.8)
+    check_side(y, base, ref, f"int8 fused r={r} {fdt}")
+    rows = torch.tensor([0, 1000, m - 1])
+    wdq = O.dequantize_int8_convrot(qn, sn, g)
+    want = O.linear_ref(x.cpu()[rows].float().numpy(), wdq) + b.double().cpu().numpy()[None, :] + ref[rows.numpy()]
+    if xdt != torch.bfloat16:
+        check_full(y[rows.to(DEV)], want, f"int8 fused full r={r}")
+
+
+@pytest.mark.parametrize("bits,m,r,fdt", [(4, 1024, 64, torch.bfloat16), (6, 2048, 32, torch.float16),
+                                          (6, 1100, 64, torch.float32)])
+def test_w4a8_lora_fused_into_gemm(bits, m, r, fdt):
+    """A8 rows from 1024 on: the weight grid decoded once, then the DMA GEMM that carries the LoRA term
+    (256 x 256 tiles at M2048 N4096, 128 x 256 at M1024, 128 x 128 at M1100 N1024)."""
+    Q = qlin()
+    n = 4096 if m == 2048 else (1024 if m == 1100 else 2048)
+    k, g, gs = 1024, 256, 64
+    gen = torch.Generator().manual_seed(30 + bits)
+    hi = 15 if bits == 4 else 63
+    codes = torch.randint(1, hi + 1, (n, k), generator=gen, dtype=torch.int32)
+    q = qz().pack_codes(codes, bits).to(DEV)
+    lo, top = (8.0, 18.0) if bits == 4 else (2.0, 4.1)
+    s_rel = (lo + (top - lo) * torch.rand(n, k // gs, generator=gen)).half().to(DEV)
+    s_ch = (torch.rand(n, generator=gen) * 2e-4 + 1e-4).float().to(DEV)
+    x = torch.randn(m, k, generator=gen).half().to(DEV)
+    down, up = factors(n, k, r, fdt, fdt, seed=31)
+    args = (x, q, s_rel, s_ch, None, None, None, gs, g)
+    kw = dict(lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=1.5)
+    base = Q.w4a8_int8_linear(*args)
+    y = Q.w4a8_int8_linear(*args, **kw)
+    plain = Q.w4a8_int8_linear(*args, residual=torch.zeros(m, n, dtype=torch.float16, device=DEV), **kw)
+    torch.cuda.synchronize()
+    _close_or_equal(y, plain, f"w{bits}a8 m={m} r={r}")
+    check_side(y, base, side_ref(x.cpu(), down, up, 1.5), f"w{bits}a8 fused m={m} r={r}")
+
+
+def test_lora_fused_declines_to_the_separate_kernels():
+    """A rank that is not a multiple of 8 at a fused shape: the fused entry point declines before
+    launching and the separate LoRA kernels give the result."""
+    Q = qlin()
+    m, n, k = 2048, 5120, 512
+    q = torch.randint(-100, 101, (n, k), generator=torch.Generator().manual_seed(40)).to(torch.int8).to(DEV)
+    s = torch.full((n,), 1e-3, device=DEV)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(41)).half()
+    down, up = factors(n, k, 12, torch.bfloat16, torch.bfloat16, seed=42)
+    base = Q.int8_linear(x.to(DEV), q, s)
+    y = Q.int8_linear(x.to(DEV), q, s, lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.5)
+    check_side(y, base, side_ref(x, down, up, 0.5), "r=12 at a fused shape")
+    from qlin import _lib
+    L = _lib.load()
+    y2 = torch.empty_like(y)
+    nb = L.qlin_workspace_size(_lib.OP_INT8_LINEAR_LORA, m, n, k, 12, _lib.DT_F16)
+    ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+    st = L.qlin_int8_linear_lora(_lib.desc(x.to(DEV)), _lib.desc(q), _lib.desc(s), None, _lib.desc(y2), 0,
+                                 _lib.desc(down.to(DEV)), _lib.desc(up.to(DEV)), 0.5, ws.data_ptr(), ws.numel(),
+                                 _lib.stream_of(ws.device))
+    assert st == _lib.QLIN_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16])
+def test_lora_fused_cancelling_the_weight_is_exactly_zero(odt):
+    """The cancellation case at a shape the fused GEMM takes (M2048 N5120): base and LoRA terms meet
+    in fp32 in the GEMM epilogue and round once, so a LoRA equal to minus the weight gives 0."""
+    m, n, k = 2048, 5120, 64
+    g = torch.Generator().manual_seed(50)
+    x = torch.randint(-7, 8, (m, k), generator=g).half()
+    q = torch.randint(-100, 101, (n, k), generator=g).to(torch.int8)
+    Q = qlin()
+    y = Q.int8_linear(x.to(DEV), q.to(DEV), torch.ones(n, device=DEV), None, odt,
+                      lora_down=torch.eye(k).to(torch.bfloat16).to(DEV),
+                      lora_up=(-q.float()).to(torch.bfloat16).to(DEV), lora_scale=1.0)
+    assert y.dtype == odt and torch.count_nonzero(y).item() == 0
