@@ -214,6 +214,24 @@ def test_lora_cancelling_the_weight_is_exactly_zero(odt, m):
 # two paths are compared output for output, besides the reference's bars.
 # ------------------------------------------------------------------------------------------------
 
+@pytest.fixture
+def fused_calls(monkeypatch):
+    """The outcomes of the wrapper's fused attempts for calls with a LoRA, in order: True where the
+    GEMM carried the LoRA term, False where the call took the separate kernels."""
+    from qlin import ops
+    seen = []
+    real = ops._fused_lora
+
+    def spy(op, lora, *a):
+        ran = real(op, lora, *a)
+        if lora is not None:
+            seen.append(ran)
+        return ran
+
+    monkeypatch.setattr(ops, "_fused_lora", spy)
+    return seen
+
+
 def _close_or_equal(fused, plain, what):
     """The fused GEMM adds (scale t) up^T into the base inside its MFMAs, the separate kernels form
     base + scale (t up^T): the same terms with fp32 roundings in another order (a few fp32 ulps
@@ -229,8 +247,8 @@ def _close_or_equal(fused, plain, what):
 
 
 @pytest.mark.parametrize("r,fdt,xdt", [(64, torch.bfloat16, torch.bfloat16), (16, torch.float16, torch.float16),
-                                       (200, torch.float32, torch.bfloat16), (8, torch.bfloat16, torch.float32)])
-def test_int8_lora_fused_into_gemm(r, fdt, xdt):
+                                       (48, torch.float32, torch.bfloat16), (8, torch.bfloat16, torch.float32)])
+def test_int8_lora_fused_into_gemm(r, fdt, xdt, fused_calls):
     """M2048 N5120: 160 tiles of 256 x 256, the GEMM that carries the LoRA term."""
     Q = qlin()
     m, n, k, g = 2048, 5120, 1024, 128
@@ -245,6 +263,7 @@ def test_int8_lora_fused_into_gemm(r, fdt, xdt):
     y = Q.int8_linear(x, q, s, b, **kw)
     plain = Q.int8_linear(x, q, s, b, residual=torch.zeros(m, n, dtype=y.dtype, device=DEV), **kw)
     torch.cuda.synchronize()
+    assert fused_calls == [True, False]
     _close_or_equal(y, plain, f"int8 r={r} {fdt}")
     ref = side_ref(x.cpu(), down, up, 0.8)
     check_side(y, base, ref, f"int8 fused r={r} {fdt}")
@@ -256,8 +275,8 @@ def test_int8_lora_fused_into_gemm(r, fdt, xdt):
 
 
 @pytest.mark.parametrize("bits,m,r,fdt", [(4, 1024, 64, torch.bfloat16), (6, 2048, 32, torch.float16),
-                                          (6, 1100, 64, torch.float32)])
-def test_w4a8_lora_fused_into_gemm(bits, m, r, fdt):
+                                          (6, 1100, 32, torch.float32)])
+def test_w4a8_lora_fused_into_gemm(bits, m, r, fdt, fused_calls):
     """A8 rows from 1024 on: the weight grid decoded once, then the DMA GEMM that carries the LoRA term
     (256 x 256 tiles at M2048 N4096, 128 x 256 at M1024, 128 x 128 at M1100 N1024)."""
     Q = qlin()
@@ -278,35 +297,54 @@ def test_w4a8_lora_fused_into_gemm(bits, m, r, fdt):
     y = Q.w4a8_int8_linear(*args, **kw)
     plain = Q.w4a8_int8_linear(*args, residual=torch.zeros(m, n, dtype=torch.float16, device=DEV), **kw)
     torch.cuda.synchronize()
+    assert fused_calls == [True, False]
     _close_or_equal(y, plain, f"w{bits}a8 m={m} r={r}")
     check_side(y, base, side_ref(x.cpu(), down, up, 1.5), f"w{bits}a8 fused m={m} r={r}")
 
 
-def test_lora_fused_declines_to_the_separate_kernels():
-    """A rank that is not a multiple of 8 at a fused shape: the fused entry point declines before
-    launching and the separate LoRA kernels give the result."""
+@pytest.mark.parametrize("r,fdt", [(12, torch.bfloat16), (72, torch.bfloat16), (40, torch.float32)])
+def test_lora_fused_declines_to_the_separate_kernels(r, fdt, fused_calls):
+    """Ranks the GEMM epilogue does not take at a fused shape (not a multiple of 8; above 64; fp32 up
+    factors above 32 in the A8 GEMM): the fused entry point declines before launching and the
+    separate LoRA kernels give the result."""
     Q = qlin()
     m, n, k = 2048, 5120, 512
-    q = torch.randint(-100, 101, (n, k), generator=torch.Generator().manual_seed(40)).to(torch.int8).to(DEV)
-    s = torch.full((n,), 1e-3, device=DEV)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(41)).half()
-    down, up = factors(n, k, 12, torch.bfloat16, torch.bfloat16, seed=42)
-    base = Q.int8_linear(x.to(DEV), q, s)
-    y = Q.int8_linear(x.to(DEV), q, s, lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.5)
-    check_side(y, base, side_ref(x, down, up, 0.5), "r=12 at a fused shape")
+    down, up = factors(n, k, r, fdt, fdt, seed=42)
+    dd, ud = down.to(DEV), up.to(DEV)
     from qlin import _lib
     L = _lib.load()
-    y2 = torch.empty_like(y)
-    nb = L.qlin_workspace_size(_lib.OP_INT8_LINEAR_LORA, m, n, k, 12, _lib.DT_F16)
-    ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
-    st = L.qlin_int8_linear_lora(_lib.desc(x.to(DEV)), _lib.desc(q), _lib.desc(s), None, _lib.desc(y2), 0,
-                                 _lib.desc(down.to(DEV)), _lib.desc(up.to(DEV)), 0.5, ws.data_ptr(), ws.numel(),
-                                 _lib.stream_of(ws.device))
+    if fdt == torch.float32:
+        # the INT8 GEMM takes fp32 up factors to rank 64; the A8 GEMM's LDS holds 32
+        codes = torch.randint(1, 16, (n, k), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
+        qp = qz().pack_codes(codes, 4).to(DEV)
+        s_rel = torch.full((n, k // 64), 10.0, dtype=torch.float16, device=DEV)
+        s_ch = torch.full((n,), 1e-4, device=DEV)
+        args = (x.to(DEV), qp, s_rel, s_ch, None, None, None, 64, 0)
+        base = Q.w4a8_int8_linear(*args)
+        y = Q.w4a8_int8_linear(*args, lora_down=dd, lora_up=ud, lora_scale=0.5)
+        nb = L.qlin_workspace_size(_lib.OP_W4A8_LINEAR_LORA, m, n, k, r, _lib.DT_F16)
+        ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+        st = L.qlin_w4a8_linear_lora(_lib.desc(x.to(DEV)), _lib.desc(qp), _lib.desc(s_rel), _lib.desc(s_ch), None,
+                                     None, _lib.desc(torch.empty_like(y)), 4, 64, 0, _lib.desc(dd), _lib.desc(ud),
+                                     0.5, ws.data_ptr(), ws.numel(), _lib.stream_of(ws.device))
+    else:
+        q = torch.randint(-100, 101, (n, k), generator=torch.Generator().manual_seed(40)).to(torch.int8).to(DEV)
+        s = torch.full((n,), 1e-3, device=DEV)
+        base = Q.int8_linear(x.to(DEV), q, s)
+        y = Q.int8_linear(x.to(DEV), q, s, lora_down=dd, lora_up=ud, lora_scale=0.5)
+        nb = L.qlin_workspace_size(_lib.OP_INT8_LINEAR_LORA, m, n, k, r, _lib.DT_F16)
+        ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+        st = L.qlin_int8_linear_lora(_lib.desc(x.to(DEV)), _lib.desc(q), _lib.desc(s), None,
+                                     _lib.desc(torch.empty_like(y)), 0, _lib.desc(dd), _lib.desc(ud),
+                                     0.5, ws.data_ptr(), ws.numel(), _lib.stream_of(ws.device))
+    assert fused_calls == [False]
+    check_side(y, base, side_ref(x, down, up, 0.5), f"r={r} {fdt} at a fused shape")
     assert st == _lib.QLIN_EUNSUPPORTED
 
 
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16])
-def test_lora_fused_cancelling_the_weight_is_exactly_zero(odt):
+def test_lora_fused_cancelling_the_weight_is_exactly_zero(odt, fused_calls):
     """The cancellation case at a shape the fused GEMM takes (M2048 N5120): base and LoRA terms meet
     in fp32 in the GEMM epilogue and round once, so a LoRA equal to minus the weight gives 0."""
     m, n, k = 2048, 5120, 64
@@ -317,4 +355,5 @@ def test_lora_fused_cancelling_the_weight_is_exactly_zero(odt):
     y = Q.int8_linear(x.to(DEV), q.to(DEV), torch.ones(n, device=DEV), None, odt,
                       lora_down=torch.eye(k).to(torch.bfloat16).to(DEV),
                       lora_up=(-q.float()).to(torch.bfloat16).to(DEV), lora_scale=1.0)
+    assert fused_calls == [True]
     assert y.dtype == odt and torch.count_nonzero(y).item() == 0
