@@ -122,23 +122,22 @@ __device__ __forceinline__ void mfma_raw(const Raw8<DA>& ra, const Raw8<DB>& rb,
 
 // LoRA term of a GEMM workgroup's BMT x BNT output tile, added by its waves to accumulators that
 // already hold their fp32 base values (after bias).  The whole rank (R <= RC) is staged at once: all
-// NT threads load the tile's t rows [BMT x RC] (fp32) and up rows [BNT x RC] into LDS together (every
-// load in flight at once, zeros past R; t is multiplied by L.scale on its way into LDS), then each
-// wave runs the bf16 MFMAs of (scale t) . up^T on split operands (mfma_raw) for its TI x TJ sub-tiles
-// of 32 x 32 straight into acc[i][j] (fp32 values, or their bits in int32 registers), so the base
-// value is the MFMAs' accumulator input.  A wave's sub-tile (i, j) covers tile rows
-// wr0 + 32 i .. + 31 and columns wc0 + 32 j .. + 31, in the MFMA C layout (lane l, register r: row
-// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32).  Requires 8 <= R <= RC, R % 8 == 0 and
-// 16-byte aligned t and up rows (t row stride R); lds must hold lora_lds_bytes<DU, BMT, BNT, RC>().
-// No loop here has a run-time trip count, so the caller's accumulators stay in registers.  Starts
-// and ends with a workgroup barrier.
-template <int DU, int RC>
-constexpr int lora_t_stride() { return RC + 4; }  // floats; the 4-float pad spreads the rows over banks
-template <int DU, int RC>
-constexpr int lora_u_stride() { return DU == DT_F32 ? RC + 4 : RC + 8; }  // elements
+// NT threads load the tile's t rows [BMT x RC] (fp32) and up rows [BNT x RC] together (every load in
+// flight at once, zeros past R).  t is multiplied by L.scale and split into bf16 hi and lo on its
+// way into LDS, once per workgroup; up goes in as loaded.  Each wave then takes its TJ column blocks
+// in turn: it reads (and, for f16 / f32, splits) the up fragments of the block once, and runs the
+// bf16 MFMAs hi.hi, lo.hi (and hi.lo) of (scale t) . up^T for each of its TI row blocks straight into
+// acc[i][j] (fp32 values, or their bits in int32 registers), so the base value is the MFMAs'
+// accumulator input.  A wave's sub-tile (i, j) covers tile rows wr0 + 32 i .. + 31 and columns
+// wc0 + 32 j .. + 31, in the MFMA C layout (lane l, register r: row 8 (r / 4) + 4 (l / 32) + r % 4,
+// column l % 32).  LDS rows are unpadded; their 16-byte chunks are XOR-swizzled (lora_chunk) so the
+// 32 rows of a fragment read spread over the banks.  Requires 8 <= R <= RC, R % 8 == 0 and 16-byte
+// aligned t and up rows (t row stride R); lds must hold lora_lds_bytes<DU, BMT, BNT, RC>().  No loop
+// here has a run-time trip count, so the caller's accumulators stay in registers.  Starts and ends
+// with a workgroup barrier.
 template <int DU, int BMT, int BNT, int RC>
 constexpr int lora_lds_bytes() {
-    return BMT * lora_t_stride<DU, RC>() * 4 + BNT * lora_u_stride<DU, RC>() * (DU == DT_F32 ? 4 : 2);
+    return BMT * RC * 4 + BNT * RC * (DU == DT_F32 ? 4 : 2);  // t as bf16 hi + lo, up as stored
 }
 
 // Ranks a GEMM epilogue with `lds_bytes` of LDS (less what it keeps for itself) can stage at once.
@@ -147,69 +146,108 @@ constexpr int lora_max_rank(int lds_bytes) {
     return lora_lds_bytes<DU, BMT, BNT, 64>() <= lds_bytes ? 64 : lora_lds_bytes<DU, BMT, BNT, 32>() <= lds_bytes ? 32 : 0;
 }
 
+// Byte offset of 16-byte chunk c of row `row` in an unpadded LDS array of BPR-byte rows: the chunk
+// index is XOR-ed with the row's position among the rows that share a 128-byte bank line, so the
+// same chunk of 8 consecutive rows lands on 8 different 16-byte bank groups.
+template <int BPR>
+__device__ __forceinline__ int lora_chunk(int row, int c) {
+    constexpr int CPR = BPR / 16, RPL = CPR >= 8 ? 1 : 8 / CPR, SW = CPR >= 8 ? 8 : CPR;
+    static_assert(BPR % 16 == 0 && CPR >= 2, "rows of whole 16-byte chunks");
+    return row * BPR + 16 * (c ^ ((row / RPL) % SW));
+}
+
 template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, typename AccT>
 __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* lds, int64_t m0, int64_t n0, int64_t M,
                                                    int64_t N, int wr0, int wc0, int tid, int lane, AccT (&acc)[TI][TJ]) {
     static_assert(sizeof(AccT) == sizeof(f32x16), "32 x 32 accumulators: fp32 values or their int32 bits");
-    constexpr int TW = lora_t_stride<DU, RC>(), UW = lora_u_stride<DU, RC>();
+    static_assert(RC % 16 == 0, "whole MFMA steps");
     constexpr int ES = DU == DT_F32 ? 4 : 2, UPP = 16 / ES;   // up element size, elements per 16 bytes
-    constexpr int TP = BMT * RC / 4 / NT, UP = BNT * RC / UPP / NT;  // 16-byte pieces per thread
-    static_assert(TP * 4 * NT == BMT * RC && UP * UPP * NT == BNT * RC, "chunk must split into whole rounds");
-    float* ts = reinterpret_cast<float*>(lds);
-    uint8_t* us = lds + BMT * TW * 4;
+    constexpr int TBPR = RC * 2, UBPR = RC * ES;             // bytes per LDS row: t hi (or lo), up
+    constexpr int TP = BMT * RC / 8 / NT, UP = BNT * RC / UPP / NT;  // pieces per thread: 8 t, 16 B of up
+    static_assert(TP * 8 * NT == BMT * RC && UP * UPP * NT == BNT * RC, "rank must split into whole rounds");
+    constexpr bool SU = DU != DT_BF16;  // up is split into hi and lo too
+    uint8_t* th = lds;
+    uint8_t* tl = lds + BMT * TBPR;
+    uint8_t* us = lds + 2 * BMT * TBPR;
     const int r32 = lane & 31, h = lane >> 5;
-    {
-        constexpr int64_t c0 = 0;
-        u32x4 tv[TP], uv[UP];
+    u32x4 tv[TP][2], uv[UP];
 #pragma unroll
-        for (int i = 0; i < TP; ++i) {
-            const int p = tid + NT * i, row = p / (RC / 4), c = 4 * (p % (RC / 4));
-            const int64_t m = min(m0 + row, M - 1), k = min<int64_t>(c0 + c, L.R - 4);
-            tv[i] = *reinterpret_cast<const u32x4*>(L.t + m * L.R + k);
-        }
+    for (int i = 0; i < TP; ++i) {
+        const int p = tid + NT * i, row = p / (RC / 8), c = 8 * (p % (RC / 8));
+        const int64_t m = min(m0 + row, M - 1), k = min<int64_t>(c, L.R - 8);
+        tv[i][0] = *reinterpret_cast<const u32x4*>(L.t + m * L.R + k);
+        tv[i][1] = *reinterpret_cast<const u32x4*>(L.t + m * L.R + k + 4);
+    }
 #pragma unroll
-        for (int i = 0; i < UP; ++i) {
-            const int p = tid + NT * i, row = p / (RC / UPP), c = UPP * (p % (RC / UPP));
-            const int64_t n = min(n0 + row, N - 1), k = min<int64_t>(c0 + c, L.R - UPP);
-            uv[i] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(L.up) + (n * L.ld_up + k) * ES);
-        }
-        __syncthreads();  // every wave is done with the LDS the chunk overwrites
+    for (int i = 0; i < UP; ++i) {
+        const int p = tid + NT * i, row = p / (RC / UPP), c = UPP * (p % (RC / UPP));
+        const int64_t n = min(n0 + row, N - 1), k = min<int64_t>(c, L.R - UPP);
+        uv[i] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(L.up) + (n * L.ld_up + k) * ES);
+    }
+    __syncthreads();  // every wave is done with the LDS the staging overwrites
 #pragma unroll
-        for (int i = 0; i < TP; ++i) {
-            const int p = tid + NT * i, row = p / (RC / 4), c = 4 * (p % (RC / 4));
-            f32x4 v = __builtin_bit_cast(f32x4, tv[i]) * L.scale;
-            if (c0 + c >= L.R) v = f32x4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<f32x4*>(ts + row * TW + c) = v;
-        }
+    for (int i = 0; i < TP; ++i) {
+        const int p = tid + NT * i, row = p / (RC / 8), c = 8 * (p % (RC / 8));
+        float v[8];
 #pragma unroll
-        for (int i = 0; i < UP; ++i) {
-            const int p = tid + NT * i, row = p / (RC / UPP), c = UPP * (p % (RC / UPP));
-            *reinterpret_cast<u32x4*>(us + (row * UW + c) * ES) = c0 + c < L.R ? uv[i] : u32x4{0u, 0u, 0u, 0u};
+        for (int e = 0; e < 4; ++e) {
+            v[e] = c < L.R ? __uint_as_float(tv[i][0][e]) * L.scale : 0.f;
+            v[4 + e] = c < L.R ? __uint_as_float(tv[i][1][e]) * L.scale : 0.f;
         }
-        __syncthreads();
-        // compile-time sub-tile indices, so that every access to the caller's accumulators is constant
-        auto subtile = [&]<int I, int J>() {
-            __builtin_amdgcn_sched_barrier(0);  // one sub-tile's fragments in registers at a time
-            f32x16 lo = __builtin_bit_cast(f32x16, acc[I][J]);
-            const float* ta = ts + (wr0 + 32 * I + r32) * TW + 8 * h;
-            const uint8_t* ub = us + ((wc0 + 32 * J + r32) * UW + 8 * h) * ES;
+        bf16x8 hi, lo;
+        split8(v, hi, lo);
+        *reinterpret_cast<bf16x8*>(th + lora_chunk<TBPR>(row, c / 8)) = hi;
+        *reinterpret_cast<bf16x8*>(tl + lora_chunk<TBPR>(row, c / 8)) = lo;
+    }
+#pragma unroll
+    for (int i = 0; i < UP; ++i) {
+        const int p = tid + NT * i, row = p / (RC / UPP), c = UPP * (p % (RC / UPP));
+        *reinterpret_cast<u32x4*>(us + lora_chunk<UBPR>(row, c / UPP)) = c < L.R ? uv[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    // compile-time block indices, so that every access to the caller's accumulators is constant
+    auto col = [&]<int J>() {
+        __builtin_amdgcn_sched_barrier(0);
+        const int un = wc0 + 32 * J + r32;
+        bf16x8 bh[RC / 16], bl[RC / 16];
+#pragma unroll
+        for (int q = 0; q < RC / 16; ++q) {
+            Raw8<DU> rb;
+            if constexpr (DU == DT_F32) {
+                rb.v[0] = *reinterpret_cast<const u32x4*>(us + lora_chunk<UBPR>(un, 4 * q + 2 * h));
+                rb.v[1] = *reinterpret_cast<const u32x4*>(us + lora_chunk<UBPR>(un, 4 * q + 2 * h + 1));
+            } else {
+                rb.v[0] = *reinterpret_cast<const u32x4*>(us + lora_chunk<UBPR>(un, 2 * q + h));
+            }
+            if constexpr (SU) {
+                float f[8];
+                raw_to_f32(rb, f);
+                split8(f, bh[q], bl[q]);
+            } else {
+                bh[q] = __builtin_bit_cast(bf16x8, rb.v[0]);
+            }
+        }
+        auto row = [&]<int I>() {
+            __builtin_amdgcn_sched_barrier(0);
+            const int tm = wr0 + 32 * I + r32;
+            f32x16 c = __builtin_bit_cast(f32x16, acc[I][J]);
 #pragma unroll
             for (int q = 0; q < RC / 16; ++q) {
-                Raw8<DT_F32> ra;
-                ra.v[0] = *reinterpret_cast<const u32x4*>(ta + 16 * q);
-                ra.v[1] = *reinterpret_cast<const u32x4*>(ta + 16 * q + 4);
-                Raw8<DU> rb;
-#pragma unroll
-                for (int v = 0; v < (DU == DT_F32 ? 2 : 1); ++v)
-                    rb.v[v] = *reinterpret_cast<const u32x4*>(ub + (16 * q) * ES + 16 * v);
-                mfma_raw<DT_F32, DU>(ra, rb, lo);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(th + lora_chunk<TBPR>(tm, 2 * q + h));
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(tl + lora_chunk<TBPR>(tm, 2 * q + h));
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[q], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[q], c, 0, 0, 0);
+                if constexpr (SU) c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[q], c, 0, 0, 0);
             }
-            acc[I][J] = __builtin_bit_cast(AccT, lo);
+            acc[I][J] = __builtin_bit_cast(AccT, c);
         };
-        [&]<int... IJ>(std::integer_sequence<int, IJ...>) {
-            (subtile.template operator()<IJ / TJ, IJ % TJ>(), ...);
-        }(std::make_integer_sequence<int, TI * TJ>{});
-    }
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+            (row.template operator()<I>(), ...);
+        }(std::make_integer_sequence<int, TI>{});
+    };
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+        (col.template operator()<J>(), ...);
+    }(std::make_integer_sequence<int, TJ>{});
     __syncthreads();  // LDS free for the caller's staging
 }
 

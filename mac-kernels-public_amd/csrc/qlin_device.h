@@ -27,11 +27,13 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// f32 -> bf16 bits, round to nearest even; a NaN keeps its top payload bits and becomes quiet.
+// Both results are computed and one is selected, so the conversion is branch-free.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t qnan = (u >> 16) | 0x40u;
+    return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : rne);
 }
 
 // f32 -> IEEE fp16 bits, round to nearest even, overflow to inf, subnormals kept; computed with
