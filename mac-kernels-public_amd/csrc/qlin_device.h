@@ -28,12 +28,14 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 // f32 -> bf16 bits, round to nearest even; a NaN keeps its top payload bits and becomes quiet.
-// Both results are computed and one is selected, so the conversion is branch-free.
+// gfx950's v_cvt_pk_bf16_f32 rounds to nearest even with denormals kept; it gives the integer
+// rounding (u + 0x7FFF + ((u >> 16) & 1)) >> 16 for every non-NaN fp32 input (all 2^32 bit
+// patterns compared on the device).  The NaN case is a select, so the conversion is branch-free.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     const uint32_t u = __float_as_uint(f);
-    const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t hw = __builtin_bit_cast(uint16_t, (__bf16)f);
     const uint32_t qnan = (u >> 16) | 0x40u;
-    return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : rne);
+    return (uint16_t)((u & 0x7FFFFFFFu) > 0x7F800000u ? qnan : hw);
 }
 
 // f32 -> IEEE fp16 bits, round to nearest even, overflow to inf, subnormals kept; computed with
@@ -91,6 +93,9 @@ template <> struct dtype_traits<bf16_t> {
 // Round a float to the storage type T and back (the value an x.dtype tensor would hold).
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return dtype_traits<T>::to_f32(dtype_traits<T>::from_f32(v)); }
+// bf16: the hardware conversion and a shift (a NaN stays a NaN; only its payload is not kept).
+template <>
+__device__ __forceinline__ float round_to<bf16_t>(float v) { return (float)(__bf16)v; }
 
 // ---------------------------------------------------------------------------------------------
 // Cross-lane helpers.
