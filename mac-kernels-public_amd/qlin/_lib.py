@@ -95,6 +95,7 @@ def load():
 _DESC = struct.Struct("=Qii8q")
 assert _DESC.size == ctypes.sizeof(QlinTensor)
 _DESC_SLOTS = 32
+_PACK = _DESC.pack_into
 _tls = threading.local()
 
 
@@ -104,32 +105,38 @@ def desc(t: torch.Tensor | None, dtype_override: int | None = None):
     same thread: build them right before the call that reads them."""
     if t is None:
         return None
-    nd = t.dim()
-    if nd > 4:
-        raise ValueError("at most 4 dims")
-    ring = _tls.__dict__.get("ring")
-    if ring is None:
+    try:
+        ring = _tls.ring
+    except AttributeError:
         buf = ctypes.create_string_buffer(_DESC.size * _DESC_SLOTS)
         ring = _tls.ring = [buf, ctypes.addressof(buf), 0]
     i = ring[2]
     ring[2] = (i + 1) % _DESC_SLOTS
-    dt = dtype_override if dtype_override is not None else _TORCH_DT[t.dtype]
-    sh, st = t.shape, t.stride()
+    dt = _TORCH_DT[t.dtype] if dtype_override is None else dtype_override
+    sh = t.shape
+    nd = len(sh)
+    off = _DESC.size * i
     if nd == 2:
-        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, 2, sh[0], sh[1], 0, 0, st[0], st[1], 0, 0)
+        st = t.stride()
+        _PACK(ring[0], off, t.data_ptr(), dt, 2, sh[0], sh[1], 0, 0, st[0], st[1], 0, 0)
     elif nd == 1:
-        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, 1, sh[0], 0, 0, 0, st[0], 0, 0, 0)
+        _PACK(ring[0], off, t.data_ptr(), dt, 1, sh[0], 0, 0, 0, t.stride(0), 0, 0, 0)
     elif nd == 0:
-        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, 1, 1, 0, 0, 0, 1, 0, 0, 0)
-    else:
+        _PACK(ring[0], off, t.data_ptr(), dt, 1, 1, 0, 0, 0, 1, 0, 0, 0)
+    elif nd <= 4:
+        st = t.stride()
         pad = (0,) * (4 - nd)
-        _DESC.pack_into(ring[0], _DESC.size * i, t.data_ptr(), dt, nd, *sh, *pad, *st, *pad)
-    return ring[1] + _DESC.size * i
+        _PACK(ring[0], off, t.data_ptr(), dt, nd, *sh, *pad, *st, *pad)
+    else:
+        raise ValueError("at most 4 dims")
+    return ring[1] + off
 
 
 def stream_of(device: torch.device) -> int:
     """The raw handle of the current stream of `device`."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
+    idx = device.index
+    if idx is None:
+        idx = torch.cuda.current_device()
     return torch._C._cuda_getCurrentRawStream(idx)
 
 

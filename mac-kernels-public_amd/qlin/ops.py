@@ -24,9 +24,21 @@ from .gguf import GGUF_TYPES, gguf_type_id
 
 _FLOAT = (torch.float16, torch.bfloat16, torch.float32)
 
+# os.environ keeps its encoded copy in a dict on POSIX; reading that is ~8x cheaper than
+# os.environ.get and still sees every change made through os.environ.
+_ENV_DATA = getattr(os.environ, "_data", None) if os.name == "posix" else None
+
+
+def env_disabled() -> bool:
+    """QLIN_DISABLE set to anything but "" or "0" (read at every call)."""
+    if _ENV_DATA is not None:
+        v = _ENV_DATA.get(b"QLIN_DISABLE")
+        return v is not None and v not in (b"", b"0")
+    return os.environ.get("QLIN_DISABLE", "0") not in ("", "0")
+
 
 def _disabled(op):
-    if os.environ.get("QLIN_DISABLE", "0") not in ("", "0"):
+    if env_disabled():
         raise NoCapableBackendError(op, {"hip": "disabled by QLIN_DISABLE"})
 
 
@@ -139,24 +151,25 @@ def _apply_lora(op, lora, x2, y, base=None):
 
 
 def _check_device(op, *tensors):
-    dev = None
+    dev = -1
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise NoCapableBackendError(op, {"hip": f"tensor on {t.device}, the kernels need a ROCm device"})
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"{op}: tensors on different devices ({dev}, {t.device})")
-    return dev
+        d = t.get_device()
+        if dev < 0:
+            dev = d
+        elif d != dev:
+            raise ValueError(f"{op}: tensors on different devices (cuda:{dev}, cuda:{d})")
 
 
 def _as_2d(x: torch.Tensor, k: int):
-    if x.shape[-1] != k:
-        raise ValueError(f"x has {x.shape[-1]} input features, the weight has {k}")
-    lead = tuple(x.shape[:-1])
-    x2 = x.reshape(-1, k)
+    sh = x.shape
+    if sh[-1] != k:
+        raise ValueError(f"x has {sh[-1]} input features, the weight has {k}")
+    lead = tuple(sh[:-1])
+    x2 = x if len(sh) == 2 else x.reshape(-1, k)
     if x2.shape[0] > 1 and x2.stride(1) != 1:
         x2 = x2.contiguous()
     if x2.shape[0] > 1 and x2.stride(0) < k:
@@ -174,9 +187,29 @@ def _out(x2, lead, n, out_dtype, x):
     return y, lead + (n,)
 
 
-def _workspace(op, m, n, k, param, x2):
-    nbytes = _lib.load().qlin_workspace_size(op, m, n, k, param, _lib._TORCH_DT[x2.dtype])
-    return _lib.workspace(nbytes, x2.device, _lib.stream_of(x2.device))
+_WS_SIZES: dict = {}
+
+
+def _workspace(op, m, n, k, param, x2, stream=None):
+    """The per-stream workspace for one call (sizes cached per shape; the C ABI computes them)."""
+    key = (op, m, n, k, param, x2.dtype)
+    nbytes = _WS_SIZES.get(key)
+    if nbytes is None:
+        if len(_WS_SIZES) > 4096:
+            _WS_SIZES.clear()
+        nbytes = _WS_SIZES[key] = _lib.load().qlin_workspace_size(op, m, n, k, param, _lib._TORCH_DT[x2.dtype])
+    return _lib.workspace(nbytes, x2.device, _lib.stream_of(x2.device) if stream is None else stream)
+
+
+def _shaped(y, shape):
+    return y if len(shape) == 2 else y.reshape(shape)
+
+
+def _f32_1d(t):
+    """t flattened to a contiguous fp32 vector (t itself when it already is one)."""
+    if t.dim() == 1 and t.dtype == torch.float32 and t.is_contiguous():
+        return t
+    return t.reshape(-1).to(torch.float32).contiguous()
 
 
 def _bias(bias, n):
@@ -184,7 +217,7 @@ def _bias(bias, n):
         return None
     if bias.numel() != n:
         raise ValueError(f"bias has {bias.numel()} elements, expected {n}")
-    return bias.reshape(n).contiguous()
+    return bias if bias.dim() == 1 and bias.is_contiguous() else bias.reshape(n).contiguous()
 
 
 # ------------------------------------------------------------------------------------------------
@@ -211,25 +244,25 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     if x2.shape[0] == 0 or n == 0:
         return y.reshape(shape)
     g = int(convrot_groupsize) if convrot else 0
-    s = scale.reshape(-1) if scale.numel() in (1, n) else scale
+    s = scale if scale.dim() == 1 or scale.numel() not in (1, n) else scale.reshape(-1)
     b = _bias(bias, n)
     L = _lib.load()
     m = x2.shape[0]
-    if m > 16:
+    stream = _lib.stream_of(x.device)
+    if m > 16 and lora is not None:
         def run(down, up, lscale):
-            wsl = _workspace(_lib.OP_INT8_LINEAR_LORA, m, n, k, down.shape[0], x2)
+            wsl = _workspace(_lib.OP_INT8_LINEAR_LORA, m, n, k, down.shape[0], x2, stream)
             return L.qlin_int8_linear_lora(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(y), g,
-                                           _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(),
-                                           _lib.stream_of(x.device))
+                                           _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(), stream)
         if _fused_lora(op, lora, res, x2, run):
-            return y.reshape(shape)
-    ws = _workspace(_lib.OP_INT8_LINEAR, x2.shape[0], n, k, g, x2)
+            return _shaped(y, shape)
+    ws = _workspace(_lib.OP_INT8_LINEAR, m, n, k, g, x2, stream)
     yb = _base_out(lora, y, res)
     st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(yb), g,
-                            ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+                            ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, op)
     _finish(op, lora, res, x2, y, yb)
-    return y.reshape(shape)
+    return _shaped(y, shape)
 
 
 def dequantize_int8(qdata, scale):
@@ -290,30 +323,30 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     y, shape = _out(x2, lead, n, out_dtype, x)
     res = _residual_args(op, residual, residual_scale, shape, n)
     if x2.shape[0] == 0 or n == 0:
-        return y.reshape(shape)
+        return _shaped(y, shape)
     q = qdata if qdata.dtype in (torch.int8, torch.uint8) else qdata.view(torch.int8)
-    cb = None if codebook is None else codebook.to(torch.float32).contiguous()
-    sch = s_channel.reshape(-1).to(torch.float32).contiguous()
+    cb = None if codebook is None else _f32_1d(codebook)
+    sch = _f32_1d(s_channel)
     b = _bias(bias, n)
     L = _lib.load()
     m = x2.shape[0]
-    if m >= 1024:
+    stream = _lib.stream_of(x.device)
+    if m >= 1024 and lora is not None:
         def run(down, up, lscale):
-            wsl = _workspace(_lib.OP_W4A8_LINEAR_LORA, m, n, k, down.shape[0], x2)
+            wsl = _workspace(_lib.OP_W4A8_LINEAR_LORA, m, n, k, down.shape[0], x2, stream)
             return L.qlin_w4a8_linear_lora(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
                                            _lib.desc(b), _lib.desc(y), bits, int(group_size), int(convrot_groupsize or 0),
-                                           _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(),
-                                           _lib.stream_of(x.device))
+                                           _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(), stream)
         if _fused_lora(op, lora, res, x2, run):
-            return y.reshape(shape)
-    ws = _workspace(_lib.OP_W4A8_LINEAR, x2.shape[0], n, k, bits, x2)
+            return _shaped(y, shape)
+    ws = _workspace(_lib.OP_W4A8_LINEAR, m, n, k, bits, x2, stream)
     yb = _base_out(lora, y, res)
     st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
                             _lib.desc(b), _lib.desc(yb), bits, int(group_size), int(convrot_groupsize or 0),
-                            ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+                            ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, op)
     _finish(op, lora, res, x2, y, yb)
-    return y.reshape(shape)
+    return _shaped(y, shape)
 
 
 def dequantize_w4a8_int8_weight(qdata, s_rel, s_channel, codebook=None, correction=None, group_size=16,
@@ -400,15 +433,16 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
     y, oshape = _out(x2, lead, n, out_dtype, x)
     res = _residual_args(op, residual, residual_scale, oshape, n)
     if x2.shape[0] == 0 or n == 0:
-        return y.reshape(oshape)
+        return _shaped(y, oshape)
     b = _bias(bias, n)
-    ws = _workspace(_lib.OP_GGUF_LINEAR, x2.shape[0], n, k, tid, x2)
+    stream = _lib.stream_of(x.device)
+    ws = _workspace(_lib.OP_GGUF_LINEAR, x2.shape[0], n, k, tid, x2, stream)
     yb = _base_out(lora, y, res)
     st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(yb),
-                                      ws.data_ptr(), ws.numel(), _lib.stream_of(x.device))
+                                      ws.data_ptr(), ws.numel(), stream)
     _lib.check(st, op)
     _finish(op, lora, res, x2, y, yb)
-    return y.reshape(oshape)
+    return _shaped(y, oshape)
 
 
 def dequantize_gguf(weight, qtype, shape, out_dtype=torch.float32):
