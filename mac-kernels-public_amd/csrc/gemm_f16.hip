@@ -395,26 +395,40 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     // passes of RP rows (row stride BNT + 8 words), then every thread writes 8 consecutive outputs of
     // a row with 16-byte stores.  32 x 32 sub-tiles: lane l, register r holds row 8 (r / 4) +
     // 4 (l / 32) + r % 4, column l % 32; 16 x 16: row 4 (l / 16) + r, column l % 16.
-    constexpr int ORW = BNT + 8;
-    constexpr int RP = (BMT * ORW * 4 <= (int)sizeof(smem)) ? BMT : BMT / 2;
-    static_assert(RP * ORW * 4 <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
+    // Every operand of the epilogue is requested before the first store (the tile's row exponents
+    // go to LDS): a global load between the stores would wait for the stores before it.  Each pass
+    // computes all of a thread's outputs before its stores; the passes synchronize LDS only.
+    constexpr int ORW = BNT + 8, ERB = BMT * 4;
     constexpr int CPR = BNT / 8;                 // 8-column chunks per row
+    constexpr int RP = (BMT * CPR / NT <= 4 && BMT * ORW * 4 + ERB <= (int)sizeof(smem)) ? BMT
+                       : (BMT / 2 * CPR / NT <= 4 && BMT / 2 * ORW * 4 + ERB <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
+    static_assert(RP * ORW * 4 + ERB <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
     static_assert(NT % CPR == 0 && (RP * CPR) % NT == 0, "chunks must split evenly");
+    constexpr int Q = RP * CPR / NT;             // chunks per thread and pass
     float* ot = reinterpret_cast<float*>(smem);
+    int* erow = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(smem) + sizeof(smem) - ERB);
     const int cc = tid % CPR;                    // this thread's chunk (the same in every pass)
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, a.N - nc));
-    float cs[8], bv[8];
+    const int xer = a.xexp ? a.xexp[min(m0 + min(tid, BMT - 1), (int64_t)a.M - 1)] : 0;
+    uint32_t csb[8], bvb[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int64_t n = min(nc + e, a.N - 1);
-        cs[e] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-        bv[e] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+        csb[e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+        bvb[e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
+    }
+    float cs[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        cs[e] = bits_to_f32_rt(csb[e], a.scale_dtype);
+        bv[e] = a.bias ? bits_to_f32_rt(bvb[e], a.bias_dtype) : 0.0f;
     }
     const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
-        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
+        lds_barrier();  // the operand buffers (or the previous pass) are no longer read
+        if (pass == 0 && tid < BMT) erow[tid] = xer;
         if ((wm * WM) / RP == pass) {
             const int rw = wm * WM - pass * RP;  // this wave's first row in the staging block
 #pragma unroll
@@ -428,19 +442,21 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
                         ot[row * ORW + col] = acc[i][j][r];
                     }
         }
-        __syncthreads();
+        lds_barrier();
+        float v[Q][8];
 #pragma unroll
-        for (int q = 0; q < RP * CPR / NT; ++q) {
+        for (int q = 0; q < Q; ++q) {
             const int row = tid / CPR + (NT / CPR) * q;
-            const int64_t m = m0 + pass * RP + row;
-            if (m >= a.M || ncount == 0) continue;
             const f32x4 v0 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc);
             const f32x4 v1 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc + 4);
-            const int e2 = a.xexp ? a.xexp[m] : 0;
-            float v[8];
+            const int e2 = erow[pass * RP + row];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
-            store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
+            for (int e = 0; e < 8; ++e) v[q][e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int64_t m = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+            if (m < a.M && ncount > 0) store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v[q], ncount, vec);
         }
     }
 }
@@ -565,41 +581,52 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
     // Epilogue: y = ldexp(acc, xexp[m]) * scale[n] + bias[n], staged through LDS in passes of RP
     // rows (row stride BNT + 8 words); every thread writes 8 consecutive outputs with 16-byte stores.
     // Lane l, register r of a 32 x 32 sub-tile holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-    constexpr int ORW = BNT + 8;
-    constexpr int RP = (BMT * ORW * 4 <= (int)sizeof(smem)) ? BMT
-                       : (BMT / 2 * ORW * 4 <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
-    static_assert(RP * ORW * 4 <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
-    constexpr int CPR = BNT / 8;
+    // Every operand of the epilogue is requested before the first store (the tile's row exponents
+    // go to LDS): a global load between the stores would wait for the stores before it (one counter
+    // counts both), a memory round trip per stored row.  Each pass computes all of a thread's
+    // outputs before its stores, the passes synchronize LDS only.
+    constexpr int ORW = BNT + 8, ERB = BMT * 4, CPR = BNT / 8;
+    constexpr int RP = (BMT * CPR / NT <= 4 && BMT * ORW * 4 + ERB <= (int)sizeof(smem)) ? BMT
+                       : (BMT / 2 * CPR / NT <= 4 && BMT / 2 * ORW * 4 + ERB <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
+    static_assert(RP * ORW * 4 + ERB <= (int)sizeof(smem) && RP % 32 == 0, "output staging must fit");
     static_assert(NT % CPR == 0 && (RP * CPR) % NT == 0, "chunks must split evenly");
+    constexpr int Q = RP * CPR / NT;  // chunks per thread and pass
     float* ot = reinterpret_cast<float*>(smem);
+    int* erow = reinterpret_cast<int*>(smem + sizeof(smem) - ERB);
     const int cc = tid % CPR;
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, a.N - nc));
-    // the store loop's scales and bias (with a LoRA term the staged values are final)
+    // row exponent of thread tid (threads past the tile re-read its last row; tid < BMT stores it)
+    const int xer = a.xexp ? a.xexp[min(m0 + min(tid, BMT - 1), (int64_t)a.M - 1)] : 0;
+    // the store loop's scales and bias as raw bits (with a LoRA term the staged values are final)
     constexpr int CB8 = LDU >= 0 ? 1 : 8;
-    float cs[CB8], bv[CB8];
+    uint32_t csb[CB8], bvb[CB8];
     if constexpr (LDU < 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t n = min(nc + e, a.N - 1);
-            cs[e] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-            bv[e] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+            csb[e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            bvb[e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
         }
     }
     const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
     if constexpr (LDU >= 0) {
-        // the tile's row exponents at the end of LDS, past the LoRA chunks
         constexpr int RC = lora_max_rank<LDU, BMT, BNT>((int)sizeof(smem) - BMT * 4);
         static_assert(RC == wo_dma_lora_rank(LDU), "the host's rank limit must match");
-        int* erow = reinterpret_cast<int*>(smem + sizeof(smem) - BMT * 4);
-        __syncthreads();  // every wave is past the main loop: the operand buffers are free
-        if (tid < BMT) erow[tid] = a.xexp ? a.xexp[min(m0 + tid, a.M - 1)] : 0;
-        __syncthreads();
+        uint32_t csj[TJ], bvj[TJ];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const int64_t n = min(n0 + wn * WN + 32 * j + r32, a.N - 1);
-            const float csn = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-            const float bvn = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+            csj[j] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            bvj[j] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
+        }
+        lds_barrier();  // every wave is past the main loop: the operand buffers are free
+        if (tid < BMT) erow[tid] = xer;
+        lds_barrier();
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const float csn = bits_to_f32_rt(csj[j], a.scale_dtype);
+            const float bvn = a.bias ? bits_to_f32_rt(bvj[j], a.bias_dtype) : 0.0f;
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -608,37 +635,50 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
         }
         lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(a.lora, smem, m0, n0, a.M, a.N, wm * WM, wn * WN, tid, lane, acc);
     }
+    float cs[CB8], bv[CB8];
+    if constexpr (LDU < 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            cs[e] = bits_to_f32_rt(csb[e], a.scale_dtype);
+            bv[e] = a.bias ? bits_to_f32_rt(bvb[e], a.bias_dtype) : 0.0f;
+        }
+    }
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
-        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
-        if ((wm * WM) / RP == pass) {
-            const int rw = wm * WM - pass * RP;
+        lds_barrier();  // the operand buffers (or the previous pass) are no longer read
+        if constexpr (LDU < 0)
+            if (pass == 0 && tid < BMT) erow[tid] = xer;
+        // the wave's 32-row sub-tiles that fall in this pass
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+        for (int i = 0; i < TI; ++i)
+            if ((wm * WM + 32 * i) / RP == pass) {
+                const int rw = wm * WM + 32 * i - pass * RP;
 #pragma unroll
                 for (int j = 0; j < TJ; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        ot[(rw + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] = acc[i][j][r];
-        }
-        __syncthreads();
+                        ot[(rw + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] = acc[i][j][r];
+            }
+        lds_barrier();
+        float v[Q][8];
 #pragma unroll
-        for (int q = 0; q < RP * CPR / NT; ++q) {
+        for (int q = 0; q < Q; ++q) {
             const int row = tid / CPR + (NT / CPR) * q;
-            const int64_t m = m0 + pass * RP + row;
-            if (m >= a.M || ncount == 0) continue;
             const f32x4 v0 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc);
             const f32x4 v1 = *reinterpret_cast<const f32x4*>(ot + row * ORW + 8 * cc + 4);
-            float v[8];
             if constexpr (LDU >= 0) {  // staged final values
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = e < 4 ? v0[e] : v1[e - 4];
+                for (int e = 0; e < 8; ++e) v[q][e] = e < 4 ? v0[e] : v1[e - 4];
             } else {
-                const int e2 = a.xexp ? a.xexp[m] : 0;
+                const int e2 = erow[pass * RP + row];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
+                for (int e = 0; e < 8; ++e) v[q][e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
             }
-            store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int64_t m = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+            if (m < a.M && ncount > 0) store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v[q], ncount, vec);
         }
     }
 }
@@ -805,11 +845,27 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
     // Epilogue: the sub-tiles go to LDS as fp32 (row stride BNT + 4 words), k part 0 first, then
     // parts 1 .. KH - 1 added in order.  Lane l, register r of a 32 x 32 sub-tile holds row
     // 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.  Then y = ldexp(acc, xexp[m]) * scale[n] +
-    // bias[n], 8 consecutive outputs per thread with 16-byte stores.
+    // bias[n], 8 consecutive outputs per thread with 16-byte stores.  The scales, bias and row
+    // exponents are requested before the parts are added (their round trip overlaps the LDS passes,
+    // and no global load sits between the stores); the passes synchronize LDS only.
     constexpr int ORW = BNT + 4;
     static_assert(BMT * ORW * 4 <= (int)sizeof(smem), "output staging must fit");
+    constexpr int NT = 64 * NW, CPR = BNT / 8, Q = (BMT * CPR + NT - 1) / NT;
     float* ot = reinterpret_cast<float*>(smem);
     float* op = ot + 4 * h * ORW + 32 * tn + r32;
+    int xeq[Q];
+    uint32_t csb[Q][8], bvb[Q][8];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int c = min(tid + NT * q, BMT * CPR - 1), row = c / CPR, cq = c % CPR;
+        xeq[q] = a.xexp ? a.xexp[min(m0 + row, (int64_t)a.M - 1)] : 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t n = min(n0 + 8 * cq + e, a.N - 1);
+            csb[q][e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            bvb[q][e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
+        }
+    }
 #pragma unroll
     for (int part = 0; part < KH; ++part) {
         if (kh == part) {
@@ -821,25 +877,26 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
                     *d = part == 0 ? acc[i][r] : *d + acc[i][r];
                 }
         }
-        __syncthreads();
+        lds_barrier();
     }
-    constexpr int NT = 64 * NW, CPR = BNT / 8;
     const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
-    for (int c = tid; c < BMT * CPR; c += NT) {
-        const int row = c / CPR, cc = c % CPR;
-        const int64_t m = m0 + row, nc = n0 + 8 * cc;
-        if (m >= a.M || nc >= a.N) continue;
-        const int ncount = (int)min<int64_t>(8, a.N - nc);
-        const int e2 = a.xexp ? a.xexp[m] : 0;
-        float v[8];
+    float v[Q][8];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int c = min(tid + NT * q, BMT * CPR - 1), row = c / CPR, cq = c % CPR;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int64_t n = min(nc + e, a.N - 1);
-            const float cs = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-            const float bv = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
-            v[e] = __builtin_ldexpf(ot[row * ORW + 8 * cc + e], e2) * cs + bv;
+            const float cs = bits_to_f32_rt(csb[q][e], a.scale_dtype);
+            const float bv = a.bias ? bits_to_f32_rt(bvb[q][e], a.bias_dtype) : 0.0f;
+            v[q][e] = __builtin_ldexpf(ot[row * ORW + 8 * cq + e], xeq[q]) * cs + bv;
         }
-        store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v, ncount, vec);
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int c = tid + NT * q, row = c / CPR, cq = c % CPR;
+        const int64_t m = m0 + row, nc = n0 + 8 * cq;
+        if (c < BMT * CPR && m < a.M && nc < a.N)
+            store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v[q], (int)min<int64_t>(8, a.N - nc), vec);
     }
 }
 

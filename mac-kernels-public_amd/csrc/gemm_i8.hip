@@ -767,25 +767,32 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     // Epilogue: y = fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]), each operation rounded on its
     // own, staged through LDS in passes of RP rows and written as 16-byte row pieces.  Lane l,
     // register r of a 32 x 32 sub-tile holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
-    constexpr int ORW = BNT + 8;
-    constexpr int RP = (BMT * ORW * 4 <= (int)sizeof(smem)) ? BMT
-                       : (BMT / 2 * ORW * 4 <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
-    static_assert(RP * ORW * 4 <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
+    // Every operand of the epilogue is requested before the first store, the tile's activation
+    // scales go to LDS: a global load between the stores would wait for the stores before it (one
+    // counter counts both), a memory round trip per stored row.  The passes synchronize LDS only.
+    constexpr int ORW = BNT + 8, SRB = BMT * 4;
+    constexpr int RP = (BMT * ORW * 4 + SRB <= (int)sizeof(smem)) ? BMT
+                       : (BMT / 2 * ORW * 4 + SRB <= (int)sizeof(smem)) ? BMT / 2 : BMT / 4;
+    static_assert(RP * ORW * 4 + SRB <= (int)sizeof(smem) && RP % WM == 0, "output staging must fit");
     constexpr int CPR = BNT / 8;
     static_assert(NT % CPR == 0 && (RP * CPR) % NT == 0, "chunks must split evenly");
     int32_t* ot = reinterpret_cast<int32_t*>(smem);
+    float* srow = reinterpret_cast<float*>(smem + sizeof(smem) - SRB);
     const int cc = tid % CPR;
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, p.N - nc));
+    // row scale of thread tid (threads past the tile re-read its last row; only tid < BMT stores it)
+    const float sxr = p.sx[min(m0 + min(tid, BMT - 1), (int64_t)p.M - 1)];
     // the store loop's scales and bias (with a LoRA term the staged values are final)
     constexpr int CB8 = LDU >= 0 ? 1 : 8;
-    float sc[CB8], bv[CB8];
+    float sc[CB8];
+    uint32_t bvb[CB8];
     if constexpr (LDU < 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t n = min(nc + e, p.N - 1);
             sc[e] = p.s_ch[n];
-            bv[e] = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+            bvb[e] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, n) : 0u;
         }
     }
     const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
@@ -793,31 +800,43 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
         // the tile's activation scales at the end of LDS, past the LoRA chunks
         constexpr int RC = lora_max_rank<LDU, BMT, BNT>((int)sizeof(smem) - BMT * 4);
         static_assert(RC >= i8dma_lora_rank(LDU), "the host's rank limit must fit every tile shape");
-        float* srow = reinterpret_cast<float*>(smem + sizeof(smem) - BMT * 4);
-        __syncthreads();  // every wave is past the main loop: the operand buffers are free
-        if (tid < BMT) srow[tid] = p.sx[min(m0 + tid, p.M - 1)];
-        __syncthreads();
+        float scn[TJ];
+        uint32_t bvj[TJ];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const int64_t n = min(n0 + wn * WN + 32 * j + r32, p.N - 1);
-            const float scn = p.s_ch[n];
-            const float bvn = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+            scn[j] = p.s_ch[n];
+            bvj[j] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, n) : 0u;
+        }
+        lds_barrier();  // every wave is past the main loop: the operand buffers are free
+        if (tid < BMT) srow[tid] = sxr;
+        lds_barrier();
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const float bvn = p.bias ? bits_to_f32_rt(bvj[j], p.bias_dtype) : 0.0f;
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
 #pragma clang fp contract(off)
                     float base = (float)acc[i][j][r] * srow[wm * WM + 32 * i + 8 * (r / 4) + 4 * h + r % 4];
-                    base = base * scn;
+                    base = base * scn[j];
                     if (p.bias) base = base + bvn;
                     acc[i][j][r] = __float_as_int(base);
                 }
         }
         lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(p.lora, smem, m0, n0, p.M, p.N, wm * WM, wn * WN, tid, lane, acc);
     }
+    float bv[CB8];
+    if constexpr (LDU < 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bv[e] = p.bias ? bits_to_f32_rt(bvb[e], p.bias_dtype) : 0.0f;
+    }
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
-        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
+        lds_barrier();  // the operand buffers (or the previous pass) are no longer read
+        if constexpr (LDU < 0)
+            if (pass == 0 && tid < BMT) srow[tid] = sxr;
         if ((wm * WM) / RP == pass) {
             const int rw = wm * WM - pass * RP;
 #pragma unroll
@@ -828,30 +847,35 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
                     for (int r = 0; r < 16; ++r)
                         ot[(rw + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] = acc[i][j][r];
         }
-        __syncthreads();
+        lds_barrier();
+        // all of the pass's outputs of this thread first, then all of its stores: a register that
+        // feeds a store in flight is not rewritten until the next pass
+        constexpr int Q = RP * CPR / NT;
+        float v[Q][8];
 #pragma unroll
-        for (int q = 0; q < RP * CPR / NT; ++q) {
+        for (int q = 0; q < Q; ++q) {
             const int row = tid / CPR + (NT / CPR) * q;
-            const int64_t m = m0 + pass * RP + row;
-            if (m >= p.M || ncount == 0) continue;
             const i32x4 a0 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc);
             const i32x4 a1 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc + 4);
-            float v[8];
             if constexpr (LDU >= 0) {  // staged final values
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = __int_as_float(e < 4 ? a0[e] : a1[e - 4]);
+                for (int e = 0; e < 8; ++e) v[q][e] = __int_as_float(e < 4 ? a0[e] : a1[e - 4]);
             } else {
 #pragma clang fp contract(off)
-                const float sxm = p.sx[m];
+                const float sxm = srow[pass * RP + row];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     float val = (float)(e < 4 ? a0[e] : a1[e - 4]) * sxm;
                     val = val * sc[e];
                     if (p.bias) val = val + bv[e];
-                    v[e] = val;
+                    v[q][e] = val;
                 }
             }
-            store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v, ncount, vec);
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int64_t m = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+            if (m < p.M && ncount > 0) store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v[q], ncount, vec);
         }
     }
 }
