@@ -483,47 +483,55 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
     }
 
     // Epilogue: y = fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]), each operation rounded on its
-    // own.  The int32 tile goes through LDS in two passes of 128 rows (row stride 264 words: rows
-    // 4 apart fall 32 banks apart), then every thread writes 8 consecutive outputs of a row with
-    // 16-byte stores.  Lane l, register r of a 32 x 32 sub-tile holds row 8 (r / 4) + 4 (l / 32) +
-    // r % 4, column l % 32.
-    constexpr int ORW = BNT + 8;  // output staging row stride (words)
-    static_assert(128 * ORW * 4 <= (int)sizeof(smem), "output staging must fit in the operand buffers");
+    // own.  The int32 tile goes through LDS in four passes of 64 rows, one wave row each (row stride
+    // 264 words: rows 4 apart fall 32 banks apart), then every thread writes 8 consecutive outputs
+    // of a row with 16-byte stores.  Lane l, register r of a 32 x 32 sub-tile holds row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32.  Every operand of the epilogue is requested before the
+    // first store (the tile's activation scales go to LDS): a global load between the stores would
+    // wait for the stores before it.  Each pass computes all of a thread's outputs before its
+    // stores; the passes synchronize LDS only.
+    constexpr int ORW = BNT + 8, CPR = BNT / 8, RP = WM, Q = RP * CPR / NT;
+    static_assert(RP * ORW * 4 + BMT * 4 <= (int)sizeof(smem), "output staging must fit in the operand buffers");
+    static_assert((RP * CPR) % NT == 0, "chunks must split evenly");
     int32_t* ot = reinterpret_cast<int32_t*>(smem);
-    const int cc = tid % (BNT / 8);              // this thread's 8-column chunk (the same in every pass)
+    float* sxs = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(smem) + sizeof(smem) - BMT * 4);
+    const int cc = tid % CPR;                    // this thread's 8-column chunk (the same in every pass)
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, p.N - nc));
-    float sc[8], bv[8];
+    const float sxr = p.sx[min(m0 + min(tid, BMT - 1), (int64_t)p.M - 1)];
+    float sc[8];
+    uint32_t bvb[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int64_t n = min(nc + e, p.N - 1);
         sc[e] = p.s_ch[n];
-        bv[e] = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+        bvb[e] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, n) : 0u;
     }
+    float bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bv[e] = p.bias ? bits_to_f32_rt(bvb[e], p.bias_dtype) : 0.0f;
     const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-        __syncthreads();  // the operand buffers (or the previous pass) are no longer read
-        if ((wm >> 1) == pass) {
+    for (int pass = 0; pass < BMT / RP; ++pass) {
+        lds_barrier();  // the operand buffers (or the previous pass) are no longer read
+        if (pass == 0 && tid < BMT) sxs[tid] = sxr;
+        if (wm == pass) {
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int j = 0; j < TJ; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        ot[((wm & 1) * WM + 32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] =
-                            acc[i][j][r];
+                        ot[(32 * i + 8 * (r / 4) + 4 * h + r % 4) * ORW + wn * WN + 32 * j + r32] = acc[i][j][r];
         }
-        __syncthreads();
+        lds_barrier();
+        float v[Q][8];
 #pragma unroll
-        for (int q = 0; q < 128 * (BNT / 8) / NT; ++q) {
-            const int row = tid / (BNT / 8) + (NT / (BNT / 8)) * q;
-            const int64_t m = m0 + 128 * pass + row;
-            if (m >= p.M || ncount == 0) continue;
+        for (int q = 0; q < Q; ++q) {
+            const int row = tid / CPR + (NT / CPR) * q;
             const i32x4 a0 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc);
             const i32x4 a1 = *reinterpret_cast<const i32x4*>(ot + row * ORW + 8 * cc + 4);
-            const float sxm = p.sx[m];
-            float v[8];
+            const float sxm = sxs[RP * pass + row];
             {
 #pragma clang fp contract(off)
 #pragma unroll
@@ -531,10 +539,14 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
                     float val = (float)(e < 4 ? a0[e] : a1[e - 4]) * sxm;
                     val = val * sc[e];
                     if (p.bias) val = val + bv[e];
-                    v[e] = val;
+                    v[q][e] = val;
                 }
             }
-            store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v, ncount, vec);
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int64_t m = m0 + RP * pass + tid / CPR + (NT / CPR) * q;
+            if (m < p.M && ncount > 0) store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v[q], ncount, vec);
         }
     }
 }
@@ -909,6 +921,19 @@ __global__ __launch_bounds__(512) void a8_smallm_kernel(GemmI8Args p) {
     const int8_t* xrow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xrow[mt] = p.xq + (int64_t)min(16 * mt + nl, (int)p.M - 1) * p.ldx;
+    // the epilogue's operands for this thread's outputs e = tid + 512 j, requested now so that the
+    // epilogue needs no memory round trip
+    constexpr int EPT = (MT * 256 + 511) / 512;
+    float esx[EPT], esc[EPT];
+    uint32_t ebv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = min(tid + 512 * j, MT * 256 - 1), em = 16 * (e >> 8) + 4 * ((e & 63) >> 4) + ((e & 255) >> 6);
+        const int64_t enn = min(n0 + (e & 15), p.N - 1);
+        esx[j] = p.sx[min(em, (int)p.M - 1)];
+        esc[j] = p.s_ch[enn];
+        ebv[j] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, enn) : 0u;
+    }
 
     struct Stage {
         u32x4 nib[2];
@@ -975,16 +1000,18 @@ __global__ __launch_bounds__(512) void a8_smallm_kernel(GemmI8Args p) {
     // 16 x 16 outputs per m-tile: lane l, register i of a wave holds row 4 (l / 16) + i, column l % 16
     {
 #pragma clang fp contract(off)
-    for (int e = tid; e < MT * 256; e += 512) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + 512 * j;
         const int mt = e >> 8, rem = e & 255, i = rem >> 6, sl = rem & 63;
         const int64_t m = 16 * mt + 4 * (sl >> 4) + i, nn = n0 + (sl & 15);
-        if (m >= p.M || nn >= p.N) continue;
+        if (e >= MT * 256 || m >= p.M || nn >= p.N) continue;
         int sum = 0;
 #pragma unroll
         for (int w = 0; w < 8; ++w) sum += red[w][mt][i][sl];
-        float val = (float)sum * p.sx[m];
-        val = val * p.s_ch[nn];
-        if (p.bias) val = val + load_rt(p.bias, p.bias_dtype, nn);
+        float val = (float)sum * esx[j];
+        val = val * esc[j];
+        if (p.bias) val = val + bits_to_f32_rt(ebv[j], p.bias_dtype);
         store_rt(p.y, p.y_dtype, m * p.ldy + nn, val);
     }
     }

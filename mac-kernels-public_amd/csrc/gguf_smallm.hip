@@ -90,6 +90,22 @@ __global__ __launch_bounds__(64 * W) void gguf_smallm_kernel(
     uint8_t* my = smem + wave * 16 * RS;
     // rows of the 4 outputs this lane holds per m-tile: 4*g + i; skip FMAs for rows past M when M <= 4
     const int ilim = (MT == 1 && M < 4) ? M : 4;
+    // the epilogue's operands for this thread's outputs e = tid + 64 W j (row exponent, weight scale
+    // and bias as raw bits), requested now so that the epilogue needs no memory round trip; the
+    // 16-wave variant (128 registers) loads them at the end instead
+    constexpr int EPT = (MT * 256 + 64 * W - 1) / (64 * W);
+    constexpr bool EPRE = W != SM_WAVES_WIDE;
+    int exe[EPT];
+    uint32_t ews[EPT], ebv[EPT];
+#pragma unroll
+    for (int j = 0; j < (EPRE ? EPT : 0); ++j) {
+        const int e = min(tid + 64 * W * j, MT * 256 - 1);
+        const int em = min((e >> 8) * 16 + 4 * ((e & 63) >> 4) + ((e & 255) >> 6), M - 1);
+        const int en = min(n0 + (e & 15), N - 1);
+        exe[j] = xexp ? xexp[em] : 0;
+        ews[j] = wscale ? load_bits_rt(wscale, wscale_dt, en * wscale_stride) : 0u;
+        ebv[j] = bias ? load_bits_rt(bias, bias_dt, en) : 0u;
+    }
 
     // No load below branches on the lane: activation rows past M re-read row M - 1 and weight rows
     // past N re-read row N - 1 (their results are never stored).  With 8 waves, stages past this
@@ -239,17 +255,24 @@ __global__ __launch_bounds__(64 * W) void gguf_smallm_kernel(
         for (int i = 0; i < 4; ++i) red[wave][mt][i][lane] = acc[mt][i];
     __syncthreads();
     // 16 x 16 outputs per m-tile; thread e handles element (i = e/64, source lane = e%64).
-    for (int e = tid; e < MT * 256; e += 64 * W) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = tid + 64 * W * j;
         const int mt = e >> 8, rem = e & 255, i = rem >> 6, sl = rem & 63;
         const int m = mt * 16 + 4 * (sl >> 4) + i;
         const int n = n0 + (sl & 15);
-        if (m < M && n < N) {
+        if (e < MT * 256 && m < M && n < N) {
             float sum = 0.0f;
 #pragma unroll
             for (int wv = 0; wv < W; ++wv) sum += red[wv][mt][i][sl];
-            float v = xexp ? __builtin_ldexpf(sum, xexp[m]) : sum;
-            if (wscale) v *= load_rt(wscale, wscale_dt, n * wscale_stride);
-            if (bias) v += load_rt(bias, bias_dt, n);
+            if constexpr (!EPRE) {
+                exe[j] = xexp ? xexp[m] : 0;
+                ews[j] = wscale ? load_bits_rt(wscale, wscale_dt, (int64_t)n * wscale_stride) : 0u;
+                ebv[j] = bias ? load_bits_rt(bias, bias_dt, n) : 0u;
+            }
+            float v = xexp ? __builtin_ldexpf(sum, exe[j]) : sum;
+            if (wscale) v *= bits_to_f32_rt(ews[j], wscale_dt);
+            if (bias) v += bits_to_f32_rt(ebv[j], bias_dt);
             store_rt(y, y_dt, (int64_t)m * ldy + n, v);
         }
     }

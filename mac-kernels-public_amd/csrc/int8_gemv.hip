@@ -101,6 +101,15 @@ __global__ __launch_bounds__(IG_THREADS) void int8_gemv_kernel(Int8GemvArgs a, i
             wr[r][i] = *reinterpret_cast<const u32x4*>(row + 16 * (int64_t)u);
         }
     }
+    // epilogue operands as raw bits, requested with the weights: a value conversion at the load
+    // would wait for every load in flight, a memory round trip after the weights have arrived
+    uint32_t csb[RW], bvb[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int64_t n = min(n0 + r, a.N - 1);
+        csb[r] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+        bvb[r] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
+    }
     // 2. the activation units, as two registers of 8 values each (zero past the range or past M)
     u32x4 xr[MR][UPL], xh[MR][UPL];
     if constexpr (FUSED) {
@@ -186,14 +195,6 @@ __global__ __launch_bounds__(IG_THREADS) void int8_gemv_kernel(Int8GemvArgs a, i
             }
         }
     }
-    // epilogue operands, fetched before the arithmetic
-    float cs[RW], bv[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const int64_t n = min(n0 + r, a.N - 1);
-        cs[r] = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-        bv[r] = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
-    }
 
     // 3. code x activation dot products, fp32
     float acc[MR][RW];
@@ -260,7 +261,9 @@ __global__ __launch_bounds__(IG_THREADS) void int8_gemv_kernel(Int8GemvArgs a, i
             const int64_t n = n0 + r;
             if (lane == m * RW + r && m < a.M && n < a.N) {
                 const int e = FUSED ? xe[m] : a.xexp ? a.xexp[m] : 0;
-                store_rt(a.y, a.y_dtype, m * a.ldy + n, __builtin_ldexpf(acc[m][r], e) * cs[r] + bv[r]);
+                const float bv = a.bias ? bits_to_f32_rt(bvb[r], a.bias_dtype) : 0.0f;
+                store_rt(a.y, a.y_dtype, m * a.ldy + n,
+                         __builtin_ldexpf(acc[m][r], e) * bits_to_f32_rt(csb[r], a.scale_dtype) + bv);
             }
         }
 }
