@@ -116,7 +116,10 @@ __device__ __forceinline__ void a8_scale(float amax, float& scale, float& st) {
 template <typename TIn, bool FAST>
 __device__ __forceinline__ void emit_a8(const float* v, float st, float y, int64_t e0, int K, bool vec_ok,
                                         int8_t* dst, TIn* xd) {
-    int8_t qq[16];
+    // q = clamp(t, -128, 127) with t = rne(dtype(x / st)) integer-valued: t + 128 (exact) goes to an
+    // unsigned byte through v_cvt_pk_u8_f32, which saturates to [0, 255] (and gives 0 for a NaN,
+    // the -128 the float clamp gives), packed four to a word; XOR 0x80 restores the signed byte.
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         float qt;
@@ -129,20 +132,16 @@ __device__ __forceinline__ void emit_a8(const float* v, float st, float y, int64
                 qt = v[i] / st;
             }
         }
-        float t = __builtin_rintf(round_to<TIn>(qt));
-        t = fminf(fmaxf(t, -128.0f), 127.0f);
-        qq[i] = (int8_t)(int)t;
+        const float t = __builtin_rintf(round_to<TIn>(qt));
+        w[i / 4] = __builtin_amdgcn_cvt_pk_u8_f32(t + 128.0f, (uint32_t)(i % 4), w[i / 4]);
     }
-    if (e0 + 16 <= K && vec_ok) {
-        uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = (uint32_t)(uint8_t)qq[4 * i] | ((uint32_t)(uint8_t)qq[4 * i + 1] << 8) |
-                   ((uint32_t)(uint8_t)qq[4 * i + 2] << 16) | ((uint32_t)(uint8_t)qq[4 * i + 3] << 24);
+    for (int i = 0; i < 4; ++i) w[i] ^= 0x80808080u;
+    if (e0 + 16 <= K && vec_ok) {
         *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
     } else {
         for (int i = 0; i < 16; ++i)
-            if (e0 + i < K) dst[i] = qq[i];
+            if (e0 + i < K) dst[i] = (int8_t)(w[i / 4] >> (8 * (i % 4)));
     }
     if (xd) {
         for (int i = 0; i < 16; ++i)
