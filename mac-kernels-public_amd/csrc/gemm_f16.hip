@@ -188,28 +188,80 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
         __syncthreads();
     }
 
-    // Epilogue.  acc[i][j][v] = D[m = wm*64 + 16i + 4g + v][n = wn*64 + 16j + r16].
+    // Epilogue.  acc[i][j][v] = D[m = wm*64 + 16i + 4g + v][n = wn*64 + 16j + r16].  Its operands
+    // (row and weight exponents, scales, bias) are loaded before the first store: a load between
+    // stores would wait for the stores before it.
+    int xev[4][4], cev[4];
+    uint32_t csb[4], bvb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xev[i][v] = a.xexp ? a.xexp[min(m0 + wm * 64 + 16 * i + 4 * g + v, a.M - 1)] : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t n = n0 + wn * 64 + 16 * j + r16;
-        if (n >= a.N) continue;
-        float cs;
-        int ce = 0;
-        if constexpr (WK == WO_INT8) cs = load_rt(a.scale, a.scale_dtype, n * a.scale_stride);
-        else { cs = 1.0f; ce = a.wexp[n]; }
-        const float bv = a.bias ? load_rt(a.bias, a.bias_dtype, n) : 0.0f;
+        const int64_t n = min(n0 + wn * 64 + 16 * j + r16, a.N - 1);
+        if constexpr (WK == WO_INT8) {
+            csb[j] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            cev[j] = 0;
+        } else {
+            csb[j] = 0u;
+            cev[j] = a.wexp[n];
+        }
+        bvb[j] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
+    }
+    // every output in place first, then (per output dtype) its stored bits in a register of its
+    // own and the stores: rewriting the data register of a store in flight would wait for it
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float cs = 1.0f;
+        if constexpr (WK == WO_INT8) cs = bits_to_f32_rt(csb[j], a.scale_dtype);
+        const float bv = a.bias ? bits_to_f32_rt(bvb[j], a.bias_dtype) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int64_t m = m0 + wm * 64 + 16 * i + 4 * g + v;
-                if (m >= a.M) continue;
-                const int e = (a.xexp ? a.xexp[m] : 0) + ce;
-                float val = __builtin_ldexpf(acc[i][j][v], e);
+                float val = __builtin_ldexpf(acc[i][j][v], xev[i][v] + cev[j]);
                 if constexpr (WK == WO_INT8) val *= cs;
                 val += bv;
-                store_rt(a.y, a.y_dtype, m * a.ldy + n, val);
+                acc[i][j][v] = val;
             }
+    }
+    auto at = [&](int i, int j, int v, int64_t& idx) {
+        const int64_t m = m0 + wm * 64 + 16 * i + 4 * g + v, n = n0 + wn * 64 + 16 * j + r16;
+        idx = m * a.ldy + n;
+        return m < a.M && n < a.N;
+    };
+    if (a.y_dtype == DT_F32) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int64_t idx;
+                    if (at(i, j, v, idx)) reinterpret_cast<float*>(a.y)[idx] = acc[i][j][v];
+                }
+    } else {
+        uint32_t hb[4][4][4];
+        const bool h16 = a.y_dtype == DT_F16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    hb[i][j][v] = h16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)acc[i][j][v])
+                                      : (uint32_t)f32_to_bf16_bits(acc[i][j][v]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int64_t idx;
+                    if (at(i, j, v, idx)) reinterpret_cast<uint16_t*>(a.y)[idx] = (uint16_t)hb[i][j][v];
+                }
     }
 }
 

@@ -199,27 +199,75 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args p) {
     }
 
     // Epilogue rounds each operation separately (no fused multiply-add), so the output is exactly
-    // fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]).
+    // fp(((f32(acc) * sx[m]) * s_channel[n]) + bias[n]).  Its operands are loaded before the first
+    // store: a load between stores would wait for the stores before it.
+    float sxv[4][4], scv[4];
+    uint32_t bvb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sxv[i][v] = p.sx[min(m0 + wm * 64 + 16 * i + 4 * g + v, p.M - 1)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t n = min(n0 + wn * 64 + 16 * j + r16, p.N - 1);
+        scv[j] = p.s_ch[n];
+        bvb[j] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, n) : 0u;
+    }
+    // every output first, then (per output dtype) its stored bits in a register of its own and the
+    // stores: rewriting the data register of a store in flight would wait for it
+    float out[4][4][4];
     {
 #pragma clang fp contract(off)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t n = n0 + wn * 64 + 16 * j + r16;
-        if (n >= p.N) continue;
-        const float sc = p.s_ch[n];
-        const float bv = p.bias ? load_rt(p.bias, p.bias_dtype, n) : 0.0f;
+        const float bv = p.bias ? bits_to_f32_rt(bvb[j], p.bias_dtype) : 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int64_t m = m0 + wm * 64 + 16 * i + 4 * g + v;
-                if (m >= p.M) continue;
-                float val = (float)acc[i][j][v] * p.sx[m];
-                val = val * sc;
+                float val = (float)acc[i][j][v] * sxv[i][v];
+                val = val * scv[j];
                 if (p.bias) val = val + bv;
-                store_rt(p.y, p.y_dtype, m * p.ldy + n, val);
+                out[i][j][v] = val;
             }
     }
+    }
+    auto at = [&](int i, int j, int v, int64_t& idx) {
+        const int64_t m = m0 + wm * 64 + 16 * i + 4 * g + v, n = n0 + wn * 64 + 16 * j + r16;
+        idx = m * p.ldy + n;
+        return m < p.M && n < p.N;
+    };
+    if (p.y_dtype == DT_F32) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int64_t idx;
+                    if (at(i, j, v, idx)) reinterpret_cast<float*>(p.y)[idx] = out[i][j][v];
+                }
+    } else {
+        uint32_t hb[4][4][4];
+        const bool h16 = p.y_dtype == DT_F16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    hb[i][j][v] = h16 ? (uint32_t)__builtin_bit_cast(uint16_t, (f16)out[i][j][v])
+                                      : (uint32_t)f32_to_bf16_bits(out[i][j][v]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int64_t idx;
+                    if (at(i, j, v, idx)) reinterpret_cast<uint16_t*>(p.y)[idx] = (uint16_t)hb[i][j][v];
+                }
     }
 }
 
