@@ -215,9 +215,45 @@ __global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
         }
     }
     // C layout: lane l, register e holds row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.  Two
-    // passes: the waves of row half `pass` stage their 64 rows, then every thread updates y.
+    // passes: the waves of row half `pass` stage their 64 rows, then every thread updates y.  A
+    // pass requests all of its base (or y) values before its first store -- a load between stores
+    // would wait for the stores before it -- and its barriers order LDS only.
+    constexpr int CPT = 64 * UP_T / 8 / 256;  // 8-output chunks per thread and pass
     for (int pass = 0; pass < 2; ++pass) {
-    __syncthreads();  // t (or the previous half) is no longer read
+    float v[CPT][8];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 256 * j, row = c / (UP_T / 8), col = 8 * (c % (UP_T / 8));
+        const int64_t m = min(mt + 64 * pass + row, a.M - 1), n = nt + col;  // rows past M re-read M - 1
+        const int cnt = (int)max<int64_t>(0, min<int64_t>(8, a.N - n));
+        if (a.base) {  // the base output in fp32: one rounding of base + side into y
+            if (bvec && cnt == 8) {
+                raw_to_f32(raw_load<DT_F32, true>(a.base, a.ldb, m, n, a.N), v[j]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[j][e] = e < cnt ? a.base[m * a.ldb + n + e] : 0.0f;
+            }
+        } else if (ypre) {
+            const u32x4 q = yv[pass * (YC / 2) + j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[j][2 * e] = bits_to_f32_rt(q[e] & 0xFFFFu, a.y_dt);
+                v[j][2 * e + 1] = bits_to_f32_rt(q[e] >> 16, a.y_dt);
+            }
+        } else if (vec && cnt == 8) {
+            if (a.y_dt == DT_F32) {
+                raw_to_f32(raw_load<DT_F32, true>(a.y, a.ldy, m, n, a.N), v[j]);
+            } else if (a.y_dt == DT_F16) {
+                raw_to_f32(raw_load<DT_F16, true>(a.y, a.ldy, m, n, a.N), v[j]);
+            } else {
+                raw_to_f32(raw_load<DT_BF16, true>(a.y, a.ldy, m, n, a.N), v[j]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[j][e] = e < cnt ? load_rt(a.y, a.y_dt, m * a.ldy + n + e) : 0.0f;
+        }
+    }
+    lds_barrier();  // t (or the previous half) is no longer read
     if (wm == pass) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -227,43 +263,19 @@ __global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
                 for (int e = 0; e < 16; ++e)
                     ot[(32 * i + 8 * (e / 4) + 4 * h + e % 4) * OTW + 64 * wn + 32 * j + r32] = acc[i][j][e];
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
-    for (int j = 0; j < 64 * UP_T / 8 / 256; ++j) {
+    for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 256 * j, row = c / (UP_T / 8), col = 8 * (c % (UP_T / 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = v[j][e] + a.scale * ot[row * OTW + col + e];
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
         const int c = tid + 256 * j, row = c / (UP_T / 8), col = 8 * (c % (UP_T / 8));
         const int64_t m = mt + 64 * pass + row, n = nt + col;
         if (m >= a.M || n >= a.N) continue;
-        const int cnt = (int)min<int64_t>(8, a.N - n);
-        float v[8];
-        if (a.base) {  // the base output in fp32: one rounding of base + side into y
-            if (bvec && cnt == 8) {
-                raw_to_f32(raw_load<DT_F32, true>(a.base, a.ldb, m, n, a.N), v);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = e < cnt ? a.base[m * a.ldb + n + e] : 0.0f;
-            }
-        } else if (ypre) {
-            const u32x4 q = yv[pass * (YC / 2) + j];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[2 * e] = bits_to_f32_rt(q[e] & 0xFFFFu, a.y_dt);
-                v[2 * e + 1] = bits_to_f32_rt(q[e] >> 16, a.y_dt);
-            }
-        } else if (vec && cnt == 8) {
-            if (a.y_dt == DT_F32) {
-                raw_to_f32(raw_load<DT_F32, true>(a.y, a.ldy, m, n, a.N), v);
-            } else if (a.y_dt == DT_F16) {
-                raw_to_f32(raw_load<DT_F16, true>(a.y, a.ldy, m, n, a.N), v);
-            } else {
-                raw_to_f32(raw_load<DT_BF16, true>(a.y, a.ldy, m, n, a.N), v);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = e < cnt ? load_rt(a.y, a.y_dt, m * a.ldy + n + e) : 0.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = v[e] + a.scale * ot[row * OTW + col + e];
-        store8_rt(a.y, a.y_dt, m * a.ldy + n, v, cnt, vec);
+        store8_rt(a.y, a.y_dt, m * a.ldy + n, v[j], (int)min<int64_t>(8, a.N - n), vec);
     }
     }
 }
