@@ -112,7 +112,11 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
 /* y[M,N] = x[M,K] @ W^T + bias, W decoded from GGUF blocks of `ggml_type` laid out as
  * consecutive blocks over the row-major [N,K] elements (the GGUF tensor bytes, N*K/qk*ts long).
  * Replaces comfy_kitchen.gguf_linear(x, weight, qtype, shape, bias, out_dtype)
- * (docs/research/2026-10-03-gguf-on-metal.md:85; bench/bench_gguf_linear.py:120). */
+ * (docs/research/2026-10-03-gguf-on-metal.md:85; bench/bench_gguf_linear.py:120).
+ * Above 64 rows the size qlin_workspace_size reports includes an fp16 copy of the decoded weight
+ * (N*K*2 bytes): the call decodes W once into it and runs the GEMM on the copy.  A workspace
+ * without that room still works (the GEMM then decodes every weight tile it loads, much slower);
+ * both meet the same accuracy bar, with different fp32 summation orders. */
 qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                              const qlin_tensor* bias, qlin_tensor* y,
                              void* workspace, size_t workspace_bytes, void* stream);
@@ -149,10 +153,13 @@ qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata
  * QLIN_NOALLOC_SCRATCH_BYTES array per GPU, held until the process ends.  For callers that cannot
  * call hipMalloc or take a caller-sized buffer: code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation.  A call whose workspace (qlin_workspace_size(QLIN_OP_GGUF_LINEAR,
- * ...)) exceeds the scratch returns QLIN_EWORKSPACE before launching anything (every M <= 64 at
- * N, K <= 8192 fits).  Nothing in the scratch needs to start at zero.  All calls on one GPU share
+ * ...), less the decoded weight copy above 64 rows) exceeds the scratch returns QLIN_EWORKSPACE
+ * before launching anything (every M <= 64 at N, K <= 8192 fits); the decoded copy is used when
+ * the rest of the scratch holds it.  Nothing in the scratch needs to start at zero.  All calls on one GPU share
  * its scratch: calls that overlap in time on that GPU (concurrent streams, or threads) race.
- * No counterpart in the reference; otherwise identical to qlin_gguf_linear (results bit-identical). */
+ * No counterpart in the reference; otherwise identical to qlin_gguf_linear (results bit-identical
+ * whenever the scratch left over holds the decoded weight copy that qlin_gguf_linear's workspace
+ * holds: always up to 64 rows; above, when N*K*2 bytes fit beside the rest). */
 qlin_status qlin_gguf_linear_noalloc(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N,
                                      int64_t K, const qlin_tensor* bias, qlin_tensor* y, void* stream);
 

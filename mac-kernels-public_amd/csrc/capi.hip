@@ -159,6 +159,13 @@ size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
     return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
            (S > 1 ? align_up((size_t)S * M * N * 4) : 0);
 }
+// Above GGUF_SMALLM_MAX_M rows the GEMM reads the weight once per 128-row tile: decoding it once
+// into the workspace (fp16, N x K) and loading it as stored beats decoding every tile (Q4_K,
+// K = N = 4096, M = 512: 200 us decoding in the GEMM).  The call takes that path when the
+// workspace holds the decoded copy beyond ws_gguf; the size query asks for it.
+size_t ws_gguf_decoded(int64_t M, int64_t N, int64_t K) {
+    return M > GGUF_SMALLM_MAX_M ? align_up((size_t)(N * K * 2)) : 0;
+}
 // input gradient: normalized dy rows (N rounded up to 128) + row exponents (+ the W4A8 int8 grid)
 size_t ws_grad(int64_t M, int64_t N, int64_t K, bool grid) {
     const int64_t lda = (N + 127) / 128 * 128;
@@ -292,7 +299,7 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
     switch (op) {
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
         case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K);
-        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param);
+        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K);
         case QLIN_OP_INT8_GRAD_INPUT: return ws_grad(M, N, K, false);
         case QLIN_OP_W4A8_GRAD_INPUT: return ws_grad(M, N, K, true);
         case QLIN_OP_INT8_LINEAR_LORA: return ws_int8(M, K) + ws_lora(M, K, param);
@@ -688,13 +695,22 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
     GemmF16Args a;
     if ((s = wo_activations(X, 0, ws, st, a.x, a.ldx, a.xexp))) return s;
     int32_t* wexp = (int32_t*)ws.take((size_t)N * 4);
-    if ((s = hip_status(run_gguf_row_exp(ggml_type, (const uint8_t*)weight, N, K, wexp, st), "gguf row exponents")))
-        return s;
-    a.wkind = WO_GGUF;
     a.gguf_type = ggml_type;
     a.M = M; a.N = N; a.K = K;
-    a.w = weight; a.ldw = row_bytes;
     a.wexp = wexp;
+    if (const size_t dec = ws_gguf_decoded(M, N, K); dec && workspace_bytes - ws.used >= dec) {
+        f16* w16 = (f16*)ws.take((size_t)(N * K * 2));
+        if ((s = hip_status(run_gguf_decode_f16(ggml_type, (const uint8_t*)weight, row_bytes, N, K, wexp, w16, st),
+                            "gguf decode")))
+            return s;
+        a.wkind = WO_F16;
+        a.w = w16; a.ldw = K;
+    } else {
+        if ((s = hip_status(run_gguf_row_exp(ggml_type, (const uint8_t*)weight, N, K, wexp, st), "gguf row exponents")))
+            return s;
+        a.wkind = WO_GGUF;
+        a.w = weight; a.ldw = row_bytes;
+    }
     a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
     a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
     return hip_status(run_gemm_f16(a, st), "gguf gemm");

@@ -90,6 +90,20 @@ __device__ __forceinline__ void load_b_int8(const int8_t* __restrict__ w, int64_
     }
 }
 
+// Decoded fp16 weight tile (WO_F16): row n = tid/2, 32 halves from column 32*(tid%2), loaded as
+// stored (K % 32 == 0, 16-byte aligned rows).  Rows past N re-read row N - 1 (their outputs are
+// never stored); the half past K (K % 64 == 32) is zero, as in the decoding load.
+__device__ __forceinline__ void load_b_f16(const f16* __restrict__ w, int64_t ldw, int64_t N, int64_t K, int64_t n0,
+                                           int64_t k0, int tid, TileRegs& R) {
+    const int r = tid >> 1, h = tid & 1;
+    const int64_t n = min(n0 + r, N - 1), k = k0 + 32 * h;
+    const bool in = k < K;
+    const u32x4* p = reinterpret_cast<const u32x4*>(w + n * ldw + (in ? k : 0));
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) R.b[i] = in ? p[i] : z;
+}
+
 // GGUF weight tile: row n = tid/2, 32 values from column 32*(tid%2): exact fp32 decode, scaled by
 // 2^-e[n], rounded once to fp16.  Requires K % 32 == 0 and rows made of whole blocks.
 template <int T>
@@ -154,6 +168,7 @@ __global__ __launch_bounds__(256) void gemm_f16_kernel(GemmF16Args a) {
         const int64_t k0 = (int64_t)kt * BK;
         load_a(x, a.ldx, a.M, a.K, m0, k0, tid, a_vec, R);
         if constexpr (WK == WO_INT8) load_b_int8((const int8_t*)a.w, a.ldw, a.N, a.K, n0, k0, tid, b_vec, R);
+        else if constexpr (WK == WO_F16) load_b_f16((const f16*)a.w, a.ldw, a.N, a.K, n0, k0, tid, R);
         else load_b_gguf<GT>((const uint8_t*)a.w, a.N, a.K, a.wexp, n0, k0, tid, R);
     };
 
@@ -764,7 +779,8 @@ __device__ __forceinline__ void wait_stages(int nd) {
 // reads at one logical chunk land in 16 distinct 16-byte bank groups.  k order: 32-value step s of
 // a k-tile, MFMA e of lane half h takes k = 32 s + 16 h + 8 e .. + 7 in both operands, so one
 // 16-byte weight read (logical chunk 2 s + h) feeds both MFMAs of the step; the activation chunk
-// is 4 s + 2 h + e.
+// is 4 s + 2 h + e.  W16: the weights are fp16 (a decoded GGUF tensor, y = ldexp(acc, xexp[m] +
+// wexp[n]) + bias[n]), laid out in LDS like the activations, chunk 4 s + 2 h + e.
 template <int BMT, int BNT, int KT>
 constexpr int wo_dmas_kparts() {
     return (8 / (BNT / 32)) < (KT / 32) ? (8 / (BNT / 32)) : (KT / 32);
@@ -780,14 +796,15 @@ __device__ __forceinline__ int lds_swz(int r) {
     else return r % 16;
 }
 
-template <int BMT, int BNT, int KT, int STAGES>
+template <int BMT, int BNT, int KT, int STAGES, bool W16 = false>
 __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_dmas_kernel(GemmF16Args a) {
     constexpr int TM = BMT / 32, TN = BNT / 32;
     constexpr int KH = wo_dmas_kparts<BMT, BNT, KT>();
     constexpr int NW = TN * KH;
     constexpr int SPW = KT / 32 / KH;                          // 32-value k steps per wave per k-tile
-    constexpr int CA = KT / 8, CB = KT / 16;                  // 16-byte chunks per LDS row
-    constexpr int ASZ = BMT * KT * 2, BSZ = BNT * KT;          // bytes per stage
+    constexpr int ES = W16 ? 2 : 1;                           // bytes per weight
+    constexpr int CA = KT / 8, CB = KT * ES / 16;             // 16-byte chunks per LDS row
+    constexpr int ASZ = BMT * KT * 2, BSZ = BNT * KT * ES;     // bytes per stage
     constexpr int WA = BMT * CA / 64, WB = BNT * CB / 64;     // wave-wide DMA instructions per stage
     constexpr int NA = (WA + NW - 1) / NW, NB = (WB + NW - 1) / NW;
     static_assert(BMT % 32 == 0 && BNT % 32 == 0 && NW <= 8 && STAGES >= 3, "tile shape");
@@ -808,7 +825,7 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
     // u % CH, holding logical chunk (u % CH) ^ sw(row).  Rows past M or N re-read the last row
     // (never stored).
     const f16* asrc[NA];
-    const int8_t* bsrc[NB];
+    const uint8_t* bsrc[NB];
     int na = 0, nb = 0;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
@@ -819,7 +836,7 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const int j = wave + NW * i, u = 64 * j + lane, row = u / CB;
-        bsrc[i] = (const int8_t*)a.w + min(n0 + row, a.N - 1) * a.ldw + 16 * ((u % CB) ^ lds_swz<CB>(row));
+        bsrc[i] = (const uint8_t*)a.w + min(n0 + row, a.N - 1) * a.ldw * ES + 16 * ((u % CB) ^ lds_swz<CB>(row));
         nb += j < WB;
     }
     const int nd = na + nb;
@@ -831,7 +848,7 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
             if (i < na) lds_dma16(asrc[i] + k0, st + 16 * 64 * (wave + NW * i));
 #pragma unroll
         for (int i = 0; i < NB; ++i)
-            if (i < nb) lds_dma16(bsrc[i] + k0, st + ASZ + 16 * 64 * (wave + NW * i));
+            if (i < nb) lds_dma16(bsrc[i] + k0 * ES, st + ASZ + 16 * 64 * (wave + NW * i));
     };
 
     f32x16 acc[TM];
@@ -845,14 +862,21 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
     for (int i = 0; i < TM; ++i) swa[i] = lds_swz<CA>(32 * i + r32);
     auto mfmas = [&](int buf) {
         const uint8_t* as = smem + buf * (ASZ + BSZ) + r32 * (KT * 2);
-        const uint8_t* bs = smem + buf * (ASZ + BSZ) + ASZ + rb * KT;
+        const uint8_t* bs = smem + buf * (ASZ + BSZ) + ASZ + rb * (KT * ES);
         // every fragment of the k-tile is read before the first MFMA
         u32x4 q[SPW];
+        f16x8 bw[W16 ? SPW : 1][2];
         f16x8 av[SPW][TM][2];
 #pragma unroll
         for (int j = 0; j < SPW; ++j) {
             const int s = kh * SPW + j;
-            q[j] = *reinterpret_cast<const u32x4*>(bs + 16 * ((2 * s + h) ^ swb));
+            if constexpr (W16) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    bw[j][e] = *reinterpret_cast<const f16x8*>(bs + 16 * ((4 * s + 2 * h + e) ^ swb));
+            } else {
+                q[j] = *reinterpret_cast<const u32x4*>(bs + 16 * ((2 * s + h) ^ swb));
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -862,13 +886,19 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
         }
 #pragma unroll
         for (int j = 0; j < SPW; ++j) {
-            uint32_t o[8];
-            i8x4_to_f16(q[j].x, o[0], o[1]);
-            i8x4_to_f16(q[j].y, o[2], o[3]);
-            i8x4_to_f16(q[j].z, o[4], o[5]);
-            i8x4_to_f16(q[j].w, o[6], o[7]);
-            const f16x8 b0 = __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
-            const f16x8 b1 = __builtin_bit_cast(f16x8, u32x4{o[4], o[5], o[6], o[7]});
+            f16x8 b0, b1;
+            if constexpr (W16) {
+                b0 = bw[j][0];
+                b1 = bw[j][1];
+            } else {
+                uint32_t o[8];
+                i8x4_to_f16(q[j].x, o[0], o[1]);
+                i8x4_to_f16(q[j].y, o[2], o[3]);
+                i8x4_to_f16(q[j].z, o[4], o[5]);
+                i8x4_to_f16(q[j].w, o[6], o[7]);
+                b0 = __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+                b1 = __builtin_bit_cast(f16x8, u32x4{o[4], o[5], o[6], o[7]});
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[j][i][0], b0, acc[i], 0, 0, 0);
 #pragma unroll
@@ -914,7 +944,8 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t n = min(n0 + 8 * cq + e, a.N - 1);
-            csb[q][e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
+            if constexpr (W16) csb[q][e] = (uint32_t)a.wexp[n];  // the weight row's exponent
+            else csb[q][e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
             bvb[q][e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
         }
     }
@@ -938,9 +969,13 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
         const int c = min(tid + NT * q, BMT * CPR - 1), row = c / CPR, cq = c % CPR;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float cs = bits_to_f32_rt(csb[q][e], a.scale_dtype);
             const float bv = a.bias ? bits_to_f32_rt(bvb[q][e], a.bias_dtype) : 0.0f;
-            v[q][e] = __builtin_ldexpf(ot[row * ORW + 8 * cq + e], xeq[q]) * cs + bv;
+            if constexpr (W16) {
+                v[q][e] = __builtin_ldexpf(ot[row * ORW + 8 * cq + e], xeq[q] + (int)csb[q][e]) + bv;
+            } else {
+                const float cs = bits_to_f32_rt(csb[q][e], a.scale_dtype);
+                v[q][e] = __builtin_ldexpf(ot[row * ORW + 8 * cq + e], xeq[q]) * cs + bv;
+            }
         }
     }
 #pragma unroll
@@ -1014,6 +1049,37 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
 #undef QLIN_WO
         }
     }
+    if constexpr (WK == WO_F16) {
+        // decoded fp16 weights: the DMA-ring kernel with the largest tile whose grid still fills the
+        // GPU in one round (256 workgroups), or 128 x 128 past that
+        const bool vec = a.K % 64 == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 8 == 0 &&
+                         (uintptr_t)a.w % 16 == 0;
+        if (vec) {
+            auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
+            int bm = 128, bn = 128;
+            if (tiles(128, 128) < 256) {
+                int64_t best = 0;
+                for (auto [m_, n_] : {std::pair{64, 128}, {64, 64}, {32, 128}, {32, 64}}) {
+                    const int64_t t = tiles(m_, n_);
+                    if (t <= 256 && t > best) { best = t; bm = m_; bn = n_; }
+                }
+            }
+            const int kt = a.K % 128 == 0 && bm < 128 ? 128 : 64;
+            const dim3 grid((unsigned)tiles(bm, bn));
+#define QLIN_WOS16(BMV, BNV, KTV, STV)                                                                          \
+    if (bm == BMV && bn == BNV && kt == KTV) {                                                                  \
+        hipLaunchKernelGGL((gemm_wo_dmas_kernel<BMV, BNV, KTV, STV, true>), grid,                               \
+                           dim3(64 * wo_dmas_waves<BMV, BNV, KTV>()), 0, st, a);                                \
+        return hipGetLastError();                                                                               \
+    }
+            QLIN_WOS16(128, 128, 64, 4)
+            QLIN_WOS16(64, 128, 128, 3) QLIN_WOS16(64, 128, 64, 6)
+            QLIN_WOS16(64, 64, 128, 4) QLIN_WOS16(64, 64, 64, 8)
+            QLIN_WOS16(32, 128, 128, 3) QLIN_WOS16(32, 128, 64, 6)
+            QLIN_WOS16(32, 64, 128, 6) QLIN_WOS16(32, 64, 64, 8)
+#undef QLIN_WOS16
+        }
+    }
     dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);
     hipLaunchKernelGGL((gemm_f16_kernel<WK, GT>), grid, block, 0, st, a);
     return hipGetLastError();
@@ -1061,8 +1127,106 @@ bool gemm_f16_fuses_lora(const GemmF16Args& a) {
 hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st) {
     if (a.M == 0 || a.N == 0) return hipSuccess;
     if (a.wkind == WO_INT8) return launch1<WO_INT8, 0>(a, st);
+    if (a.wkind == WO_F16) {
+        if (a.K % 32 || a.ldw % 8 || (uintptr_t)a.w % 16) return hipErrorInvalidValue;
+        return launch1<WO_F16, 0>(a, st);
+    }
     hipError_t err = hipErrorInvalidValue;
     bool ok = gguf::dispatch_type(a.gguf_type, [&]<int T>() { err = launch1<WO_GGUF, T>(a, st); });
+    return ok ? err : hipErrorInvalidValue;
+}
+
+// One workgroup per weight row n: the row's exponent e[n] (of its largest |w|, as
+// gguf_row_exp_kernel computes it) and the row stored as fp16(w 2^-e[n]), 8 values per 16-byte
+// store.  CPT > 0: the packed row is first copied to LDS in dwords (the decode's byte reads then
+// hit LDS, not the texture path), and each thread decodes its CPT chunks of 8 values (chunk c at
+// 8 (tid + 256 c)) once and keeps them in registers (K <= 2048 CPT); CPT = 0: any K, the row
+// decoded twice from global memory (the second time from cache).
+template <int T, int CPT>
+__global__ __launch_bounds__(256) void gguf_decode_f16_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
+                                                              int64_t K, int32_t* __restrict__ wexp,
+                                                              f16* __restrict__ out) {
+    constexpr int QK = gguf::Info<T>::QK, TS = gguf::Info<T>::TS;
+    constexpr int RW = CPT > 0 ? (CPT * 2048 / QK * TS + 3) / 4 : 1;  // dwords of the longest row
+    __shared__ float red[4];
+    __shared__ uint32_t rs[RW];
+    const int64_t n = blockIdx.x;
+    const uint8_t* row = w + n * row_bytes;
+    if constexpr (CPT > 0) {
+        if ((((uintptr_t)w | (uintptr_t)row_bytes) & 3) == 0) {
+            const uint32_t* r4 = reinterpret_cast<const uint32_t*>(row);
+            for (int i = threadIdx.x; i < row_bytes / 4; i += 256) rs[i] = r4[i];
+        } else {
+            for (int i = threadIdx.x; i < row_bytes; i += 256) reinterpret_cast<uint8_t*>(rs)[i] = row[i];
+        }
+        __syncthreads();
+        row = reinterpret_cast<const uint8_t*>(rs);
+    }
+    f16* orow = out + n * K;
+    auto decode = [&](int64_t j, float* v) {
+        const int64_t blk = j / QK;
+        gguf::decode8<T>(row + blk * TS, (int)(j - blk * QK), v);
+    };
+    auto store = [&](int64_t j, const float* v, int e) {
+        uint32_t p[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            p[t] = pack2((f16)__builtin_ldexpf(v[2 * t], -e), (f16)__builtin_ldexpf(v[2 * t + 1], -e));
+        *reinterpret_cast<u32x4*>(orow + j) = u32x4{p[0], p[1], p[2], p[3]};
+    };
+    float amax = 0.0f;
+    float v[CPT > 0 ? CPT : 1][8];
+    if constexpr (CPT > 0) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int64_t j = ((int64_t)threadIdx.x + 256 * c) * 8;
+            if (j < K) decode(j, v[c]);
+            else
+#pragma unroll
+                for (int t = 0; t < 8; ++t) v[c][t] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(v[c][t]));
+        }
+    } else {
+        for (int64_t j = (int64_t)threadIdx.x * 8; j < K; j += 256 * 8) {
+            decode(j, v[0]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) amax = fmaxf(amax, fabsf(v[0][t]));
+        }
+    }
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    const int e = frexp_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    if (threadIdx.x == 0) wexp[n] = e;
+    if constexpr (CPT > 0) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int64_t j = ((int64_t)threadIdx.x + 256 * c) * 8;
+            if (j < K) store(j, v[c], e);
+        }
+    } else {
+        for (int64_t j = (int64_t)threadIdx.x * 8; j < K; j += 256 * 8) {
+            decode(j, v[0]);
+            store(j, v[0], e);
+        }
+    }
+}
+
+hipError_t run_gguf_decode_f16(int type, const uint8_t* w, int64_t row_bytes, int64_t N, int64_t K, int32_t* e,
+                               f16* out, hipStream_t st) {
+    if (N == 0 || K == 0) return hipSuccess;
+    if (K % 32 || (uintptr_t)out % 16) return hipErrorInvalidValue;
+    hipError_t err = hipErrorInvalidValue;
+    const int64_t cpt = (K + 2047) / 2048;
+    bool ok = gguf::dispatch_type(type, [&]<int T>() {
+        const dim3 grid((unsigned)N), block(256);
+        if (cpt <= 1) hipLaunchKernelGGL((gguf_decode_f16_kernel<T, 1>), grid, block, 0, st, w, row_bytes, K, e, out);
+        else if (cpt <= 2) hipLaunchKernelGGL((gguf_decode_f16_kernel<T, 2>), grid, block, 0, st, w, row_bytes, K, e, out);
+        else if (cpt <= 4) hipLaunchKernelGGL((gguf_decode_f16_kernel<T, 4>), grid, block, 0, st, w, row_bytes, K, e, out);
+        else hipLaunchKernelGGL((gguf_decode_f16_kernel<T, 0>), grid, block, 0, st, w, row_bytes, K, e, out);
+        err = hipGetLastError();
+    });
     return ok ? err : hipErrorInvalidValue;
 }
 

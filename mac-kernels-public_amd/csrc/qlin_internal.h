@@ -125,7 +125,7 @@ bool gguf_gemv_supported(int type, int64_t M, int64_t K, int64_t row_bytes, cons
 hipError_t run_gguf_gemv(const GgufGemvArgs& a, hipStream_t st);
 
 // ---- weight-only fp16 MFMA tile GEMM (gemm_f16.hip) ----
-enum { WO_INT8 = 0, WO_GGUF = 1 };
+enum { WO_INT8 = 0, WO_GGUF = 1, WO_F16 = 2 };  // WO_F16: fp16 weights w[n] 2^-e[n] (a decoded GGUF tensor)
 // LoRA term added by a GEMM epilogue to its own output tile: y = dtype(base + scale * t up^T), t the
 // fp32 low-rank activation [M, R] (row stride R), up [N, R] (f32 / f16 / bf16, row stride ld_up).
 // t == nullptr: no LoRA term.
@@ -159,6 +159,11 @@ struct GemmF16Args {
     LoraTile lora;                   // INT8, 256 x 256 DMA tiles only (gemm_f16_fuses_lora)
 };
 hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st);
+// The GGUF weight's row exponents e[n] (as run_gguf_row_exp) and the weight decoded once as
+// fp16(w[n][k] 2^-e[n]) into out [N][K] (row stride K), with the GEMM load stage's arithmetic:
+// exact fp32 decode, scaling by 2^-e[n], one rounding.
+hipError_t run_gguf_decode_f16(int type, const uint8_t* w, int64_t row_bytes, int64_t N, int64_t K, int32_t* e,
+                               f16* out, hipStream_t st);
 // Whether run_gemm_f16 takes a kernel that adds a.lora in its epilogue for these operands.
 bool gemm_f16_fuses_lora(const GemmF16Args& a);
 

@@ -226,6 +226,54 @@ def test_gguf_linear_split_k_graph_replays():
         assert torch.equal(got, want), f"replay {i} differs from the eager call"
 
 
+@pytest.mark.parametrize("name,m,n,k", [
+    ("Q4_0", 65, 131, 1056),    # K % 64 == 32: the last k-tile's upper half is past K; ragged N
+    ("Q8_0", 200, 300, 96),     # two k-tiles, the second half empty
+    ("IQ4_NL", 129, 257, 2080),
+    ("Q4_K", 300, 520, 2048),
+    ("Q6_K", 96, 1000, 768),
+    ("Q2_K", 77, 64, 512),      # one column tile, half of it past N
+    ("Q5_K", 130, 256, 6144),   # the decode keeps 3 chunks of 8 per thread (4 slots)
+    ("Q8_0", 70, 96, 8448),     # K > 8192: the decode reads each row twice
+    ("Q4_K", 1024, 512, 1024),  # 128 x 128 tiles
+])
+def test_gguf_linear_decode_once(name, m, n, k):
+    """Above 64 rows, with the workspace qlin_workspace_size reports, the weight is decoded once into
+    it as fp16 and a DMA-ring GEMM loads that copy (K % 64 == 32: the tiled GEMM loads it); with the
+    minimum workspace (no room for the copy) the tiled GEMM decodes every tile it loads.  Both meet
+    the oracle's bar.  The workspaces start as all-ones bytes (fp16 NaN), so any element of the
+    copy left unwritten shows."""
+    from qlin import _lib
+    L = _lib.load()
+    raw = qz().random_gguf_blocks(name, n, k, seed=71)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = x_fp16(m, k, seed=m + 7)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(9)) * 0.1).half()
+    want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
+    rawd, xd, bd = torch.from_numpy(raw).to(DEV), x.to(DEV), b.to(DEV)
+    tid = qlin().GGUF_TYPES[name][0]
+    full = L.qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, k, tid, _lib._TORCH_DT[torch.float16])
+    copy = (n * k * 2 + 255) // 256 * 256
+    outs = []
+    for nbytes in (full, full - copy):
+        ws = torch.full((nbytes,), 255, dtype=torch.uint8, device=DEV)
+        y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        st = L.qlin_gguf_linear(_lib.desc(xd), rawd.data_ptr(), tid, n, k, _lib.desc(bd), _lib.desc(y),
+                                ws.data_ptr(), nbytes, _lib.stream_of(xd.device))
+        _lib.check(st, "gguf_linear")
+        outs.append(y)
+    torch.cuda.synchronize()
+    check_linear(outs[0], want, f"{name} M={m} N={n} K={k} decoded once")
+    check_linear(outs[1], want, f"{name} M={m} N={n} K={k} decoded per tile")
+    if k % 64:  # the same tiled GEMM over the same fp16 values: the same bits
+        assert torch.equal(outs[0], outs[1]), "decoded copy and per-tile decode differ"
+    # below the minimum: refused before anything runs (the pointer is never dereferenced)
+    ws = torch.empty(full - copy - 256, dtype=torch.uint8, device=DEV)
+    st = L.qlin_gguf_linear(_lib.desc(xd), rawd.data_ptr(), tid, n, k, _lib.desc(bd), _lib.desc(y),
+                            ws.data_ptr(), ws.numel(), _lib.stream_of(xd.device))
+    assert st == _lib.QLIN_EWORKSPACE
+
+
 # Long rows.  One activation row with K / (values per lane chunk) in {16, 32, 64} takes the GEMV
 # kernel for every format it covers (at K = 1024 most formats take the small-M kernel instead);
 # K = 4096 is the decode shape.  M = 8 and 16 take the small-M kernel (Q6_K: the K split).
