@@ -343,6 +343,8 @@ CONFIGS = {
     "w6a8_m9504_k13824_n5120": dict(kind="a8", bits=6, gs=64, g=256, m=9504, k=13824, n=5120),
     "dit_layer_int8_convrot_m4608": dict(kind="dit", m=4608, g=128,
                                          linears=((9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288))),
+    # a GGUF prefill: 512 activation rows (the weight decoded once into the workspace, then the GEMM)
+    "gguf_q4_k_m512_k4096_n4096": dict(kind="gguf", type="Q4_K", m=512, k=4096, n=4096),
 }
 
 # The launches a call makes at these shapes (the C ABI's dispatch), named as in the kernel traces.
@@ -355,6 +357,7 @@ CONFIG_KERNELS = {
     "w6a8_m9504_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m9504_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "dit_layer_int8_convrot_m4608": "4x (prologue_kernel+gemm_wo_dma_kernel<256,3>)",
+    "gguf_q4_k_m512_k4096_n4096": "prologue_kernel+gguf_decode_f16_kernel+gemm_wo_dmas_kernel<64,128,128,3,true>",
 }
 
 
@@ -499,6 +502,33 @@ def run_configs(names, steps, warmup, pool):
                                 "kernel": CONFIG_KERNELS[name], "ops_per_call": flops, "bytes_per_call": nbytes,
                                 "traffic": config_traffic(name)},
                    "cpu_baseline": cpu}
+        elif cfg["kind"] == "gguf":
+            t, m, k, n = cfg["type"], cfg["m"], cfg["k"], cfg["n"]
+            raw = quantized_base(t, n, k, seed=14)
+            copies = max(1, -(-POOL_BYTES // raw.numel()))
+            ws = make_gguf_weights(t, n, k, copies, seed=14, raw=raw)
+            x = gpu_activations(m, k, seed=15)
+            tid = qlin.GGUF_TYPES[t][0]
+
+            def step():
+                for wd in ws:
+                    qlin.gguf_linear(x, wd, tid, (n, k))
+
+            msr, _ = time_graph(step, steps, warmup)
+            us = msr / copies * 1e3
+            flops, nbytes = 2 * m * n * k, raw.numel() + m * k * 2 + m * n * 2
+            tfl = flops / (us * 1e-6) / 1e12
+            rn = raw.numpy()
+            cpu = pool and cpu_linear_baseline(pool, name, m, k, n,
+                                               lambda r0, r1: O.gguf_dequantize(rn[r0:r1], t, (r1 - r0, k)), 1024)
+            rec = {"us_per_call": round(us, 2), "TFLOPs": round(tfl, 2),
+                   "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "pool_copies": copies,
+                   "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS,
+                                "unit": "TFLOP/s", "frac": round(tfl / FP16_PEAK_TFLOPS, 4),
+                                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                "kernel": CONFIG_KERNELS[name], "flops_per_call": flops, "bytes_per_call": nbytes,
+                                "traffic": config_traffic(name)},
+                   "cpu_baseline": cpu}
         else:  # one DiT block layer: QKV, O, MLP up, MLP down
             m, g = cfg["m"], cfg["g"]
             layer_bytes = sum(n * k for n, k in cfg["linears"])
@@ -595,7 +625,12 @@ def profile_pass(which, reps=3, n=4096, k=4096, ms=(1, 8, 64)):
                     qlin.gguf_linear(xs[m], weights[t][r * len(ms) + j], tid, (n, k))
     else:
         cfg = CONFIGS[which]
-        if cfg["kind"] == "a8":
+        if cfg["kind"] == "gguf":
+            tid = qlin.GGUF_TYPES[cfg["type"]][0]
+            x = gpu_activations(cfg["m"], cfg["k"], 15)
+            for wd in make_gguf_weights(cfg["type"], cfg["n"], cfg["k"], reps, seed=14):
+                qlin.gguf_linear(x, wd, tid, (cfg["n"], cfg["k"]))
+        elif cfg["kind"] == "a8":
             q, sr, sc = a8_weight(cfg["n"], cfg["k"], cfg["bits"], cfg["gs"], seed=11)
             ws = permuted_copies((q, sr, sc), cfg["n"], reps, seed=12)
             x = gpu_activations(cfg["m"], cfg["k"], 13, cfg.get("outliers", False))
