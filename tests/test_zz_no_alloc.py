@@ -1,7 +1,8 @@
 """qlin_gguf_linear_noalloc: the GGUF linear with its workspace in the library's fixed per-GPU
 scratch instead of a caller buffer.  Every call goes through the C ABI and must equal
 qlin_gguf_linear (same kernels, caller workspace) bit for bit, on consecutive calls of different
-sizes (the scratch keeps the previous call's contents), and match the oracle's linear."""
+sizes (the scratch keeps the previous call's contents), and match the oracle's linear.  Above 64
+rows both decode the weight once at these sizes (the scratch holds the fp16 copy)."""
 import numpy as np
 import pytest
 import torch
