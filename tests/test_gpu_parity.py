@@ -267,6 +267,20 @@ def test_gguf_linear_decode_once(name, m, n, k):
     check_linear(outs[1], want, f"{name} M={m} N={n} K={k} decoded per tile")
     if k % 64:  # the same tiled GEMM over the same fp16 values: the same bits
         assert torch.equal(outs[0], outs[1]), "decoded copy and per-tile decode differ"
+    # a weight at an odd address (the C ABI takes any byte pointer): the decode copies its rows
+    # bytewise, and up to 64 rows the tiled GEMM decodes each tile
+    if name in ("Q4_0", "Q4_K", "Q6_K"):
+        buf = torch.empty(rawd.numel() + 1, dtype=torch.uint8, device=DEV)
+        buf[1:].copy_(rawd.reshape(-1))
+        for mm in (m, 8):
+            ws = torch.full((L.qlin_workspace_size(_lib.OP_GGUF_LINEAR, mm, n, k, tid, _lib._TORCH_DT[torch.float16]),),
+                            255, dtype=torch.uint8, device=DEV)
+            yo = torch.empty(mm, n, dtype=torch.float16, device=DEV)
+            st = L.qlin_gguf_linear(_lib.desc(xd[:mm]), buf.data_ptr() + 1, tid, n, k, _lib.desc(bd), _lib.desc(yo),
+                                    ws.data_ptr(), ws.numel(), _lib.stream_of(xd.device))
+            _lib.check(st, "gguf_linear (odd weight address)")
+            torch.cuda.synchronize()
+            check_linear(yo, want[:mm], f"{name} M={mm} N={n} K={k} weight at an odd address")
     # below the minimum: refused before anything runs (the pointer is never dereferenced)
     ws = torch.empty(full - copy - 256, dtype=torch.uint8, device=DEV)
     st = L.qlin_gguf_linear(_lib.desc(xd), rawd.data_ptr(), tid, n, k, _lib.desc(bd), _lib.desc(y),
