@@ -173,7 +173,7 @@ size_t ws_grad(int64_t M, int64_t N, int64_t K, bool grid) {
 }
 
 size_t ws_w4a8(int64_t M, int64_t N, int64_t K) {
-    return align_up((size_t)(M * K)) + align_up((size_t)M * 4) + (a8_decode_once(M, K) ? align_up((size_t)(N * K)) : 0);
+    return align_up((size_t)(M * K)) + align_up((size_t)M * 4) + (a8_decode_once(M, N, K) ? align_up((size_t)(N * K)) : 0);
 }
 
 // LoRA's low-rank activation t = x down^T: S fp32 K-split partials and their sum, or one [M, R].
@@ -800,7 +800,7 @@ static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     g.s_ch = (const float*)s_channel->data; g.codebook = cb;
     g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
     g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
-    if (a8_decode_once(M, K)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
+    if (a8_decode_once(M, N, K)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
     float* t = nullptr;
     if (L) {
         t = (float*)ws.take(ws_lora(M, K, D.rows));

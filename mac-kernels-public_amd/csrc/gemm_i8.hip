@@ -1080,7 +1080,7 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         else hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 2>), grid, block, 0, st, p);
         return hipGetLastError();
     }
-    if (p.w8 && a8_decode_once(p.M, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
+    if (p.w8 && a8_decode_once(p.M, p.N, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
         (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0) {
         const int64_t segs = p.N * (p.K / 64);
         if (4 * segs + 256 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // the grid kernel's 32-bit indices
@@ -1157,7 +1157,7 @@ hipError_t launch_grid(const GemmI8Args& p, hipStream_t st) {
 // The conditions under which launch_o takes the decode-once DMA GEMM, and the LoRA operands it reads
 // with 16-byte loads.
 bool gemm_i8_fuses_lora(const GemmI8Args& p) {
-    const bool dma = p.w8 && a8_decode_once(p.M, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
+    const bool dma = p.w8 && a8_decode_once(p.M, p.N, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
                      (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0 && !a8_smallm_ok(p);
     const LoraTile& L = p.lora;
     const int es = L.up_dt == DT_F32 ? 4 : 2;
