@@ -196,12 +196,15 @@ struct GemmI8Args {
 // Whether run_gemm_i8 takes a kernel that adds p.lora in its epilogue for these operands.
 bool gemm_i8_fuses_lora(const GemmI8Args& p);
 // A8 calls that decode the weight grid once into the workspace (N * K bytes) and run the int8 DMA
-// GEMM on it: from 1024 activation rows, and above the small-M kernel's 32 rows wherever the grid
-// has too few 256 x 256 tiles for the fused-decode kernel (the 128 x 128 kernel that decodes every
-// tile it loads then leaves most CUs idle: 103 us at M256 K = N = 4096).
+// GEMM on it: from 512 activation rows (two or more 256-row tiles would each decode the weight in
+// the fused-decode kernel: W6A8 K5120 M512 N27648 138 vs 167 us, M960 N13824 110 vs 160 us), and
+// above the small-M kernel's 32 rows wherever the grid has too few 256 x 256 tiles for the
+// fused-decode kernel (the 128 x 128 kernel that decodes every tile it loads then leaves most CUs
+// idle: W4A8 M256 K = N = 4096 42.5 vs 103.7 us).  One 256-row tile over a wide grid stays fused
+// (W4A8 M256 K4096 N49152: 86 vs 151 us).
 inline bool a8_decode_once(int64_t M, int64_t N, int64_t K) {
     if (K % 128) return false;
-    return M >= 1024 || (M > 32 && ((M + 255) / 256) * ((N + 255) / 256) < 192);
+    return M >= 512 || (M > 32 && ((M + 255) / 256) * ((N + 255) / 256) < 192);
 }
 // The int8 weight grid alone into p.w8 ([N][K], row stride K), one thread per 64-code segment:
 // group_size a multiple of 64, 16-byte aligned code rows.

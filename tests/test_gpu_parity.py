@@ -562,8 +562,11 @@ A8_TILE_CASES = [
     (6, "auto", torch.float16, 64, 128, 1300, 5000),
     (6, None, torch.float16, 64, 256, 1024, 4200),  # 136 tiles of 128 x 256 (one round), not 264 of 128 x 128
     (4, None, torch.float8_e4m3fn, 128, 256, 1024, 2000),
-    # M < 1024 with >= 192 tiles of 256 x 256: the fused-decode kernel, one scale table per thread
+    # M < 512 with >= 192 tiles of 256 x 256: the fused-decode kernel, one scale table per thread
     # pair (group 128) and per thread (group 64)
+    (4, None, torch.float16, 128, 128, 300, 24600),
+    (6, "auto", torch.float8_e4m3fn, 64, 256, 257, 25000),
+    # 512 <= M < 1024: the grid decoded once, then the int8 DMA GEMM
     (4, None, torch.float16, 128, 128, 1000, 12300),
     (6, "auto", torch.float8_e4m3fn, 64, 256, 777, 12500),
 ]
@@ -593,7 +596,12 @@ def test_w4a8_linear_large_tiles(bits, cb, srdt, gs, k, m, n):
     bad = got.view(np.uint16) != replay.astype(np.float16).view(np.uint16)
     assert not bad.any(), f"{int(bad.sum())} mismatches, first at {np.argwhere(bad)[:3].tolist()}"
     want = O.linear_ref(xq.astype(np.float32) * sx[:, None], w8.astype(np.float32) * s_ch.numpy()[:, None])
-    check_linear(y, want, f"bits={bits} large tiles")
+    # against float64: the fp16 output's own rounding (half an ulp, |y| 2^-11) bounds the large
+    # outputs of the outlier rows, above the absolute bar once |y| > 32
+    got64 = y.float().cpu().numpy().astype(np.float64)
+    assert O.rel_fro(got64, want) < REL_TOL
+    err, lim = np.abs(got64 - want), np.maximum(ABS_TOL, np.abs(want) * 2.0 ** -10)
+    assert (err <= lim).all(), f"bits={bits} large tiles: max error / bound {float((err / lim).max()):.3f}"
 
 
 @pytest.mark.parametrize("case", ["gauss_96x1024", "heavy_96x1024"])
