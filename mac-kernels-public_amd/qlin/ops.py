@@ -331,7 +331,9 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     L = _lib.load()
     m = x2.shape[0]
     stream = _lib.stream_of(x.device)
-    if m >= 1024 and lora is not None:
+    # above the small-M kernel's 32 rows the C ABI fuses the term where it decodes the weight grid
+    # once, and declines elsewhere
+    if m > 32 and lora is not None:
         def run(down, up, lscale):
             wsl = _workspace(_lib.OP_W4A8_LINEAR_LORA, m, n, k, down.shape[0], x2, stream)
             return L.qlin_w4a8_linear_lora(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),

@@ -275,10 +275,11 @@ def test_int8_lora_fused_into_gemm(r, fdt, xdt, fused_calls):
 
 
 @pytest.mark.parametrize("bits,m,r,fdt", [(4, 1024, 64, torch.bfloat16), (6, 2048, 32, torch.float16),
-                                          (6, 1100, 32, torch.float32)])
+                                          (6, 1100, 32, torch.float32), (4, 200, 16, torch.bfloat16)])
 def test_w4a8_lora_fused_into_gemm(bits, m, r, fdt, fused_calls):
-    """A8 rows from 1024 on: the weight grid decoded once, then the DMA GEMM that carries the LoRA term
-    (256 x 256 tiles at M2048 N4096, 128 x 256 at M1024, 128 x 128 at M1100 N1024)."""
+    """A8 calls whose weight grid is decoded once (from 512 rows, and above 32 rows on grids of fewer
+    than 192 tiles of 256 x 256), then the DMA GEMM that carries the LoRA term (256 x 256 tiles at
+    M2048 N4096, 128 x 256 at M1024, 128 x 128 at M1100 N1024 and M200 N2048)."""
     Q = qlin()
     n = 4096 if m == 2048 else (1024 if m == 1100 else 2048)
     k, g, gs = 1024, 256, 64
