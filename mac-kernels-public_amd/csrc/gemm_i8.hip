@@ -1107,8 +1107,10 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         // the larger tile beats 1.25 rounds of the smaller (M1024 K13824 N5120: 150.6 vs 157.1 us)
         else if (tiles(128, 256) >= 192 || (tiles(128, 256) <= 256 && tiles(128, 128) > 256))
             go.template operator()<128, 256>();
-        else
+        else if (tiles(128, 128) >= 128)
             go.template operator()<128, 128>();
+        else  // grids of fewer than 128 tiles of 128 x 128 (a few hundred rows): twice the workgroups
+            go.template operator()<128, 64>();
         return hipGetLastError();
     }
     // large tiles when the grid still fills the GPU and one scale covers each row's k-tile
