@@ -14,10 +14,12 @@ register sets) runs 24..216 times.  Checks, per call:
      selected channels of large shapes the same way);
   2. the whole output against a float64 GEMM on the GPU over the oracle's operands (the weights
      dequantized by the oracle, the activations rotated by the oracle's Hadamard matrix);
-  3. for A8, an exact replay of the int8 GEMM and epilogue over the whole output: int8 x int8
-     products summed in float64 are exact (|acc| < 2^53), then (f32(acc) * sx) * s_channel in fp32
-     and one rounding, compared bit for bit; the float64 accumulators of the sampled rows are
-     checked against the oracle's int64 GEMM first.
+  3. for A8, the activation leg against the oracle on the sampled rows (the rotated row within one
+     ulp of the oracle's exact rotation, its int8 codes and fp32 scale bit-exact against the
+     oracle's quantize_int8_rowwise), then an exact replay of the int8 GEMM and epilogue over the
+     whole output: int8 x int8 products summed in float64 are exact (|acc| < 2^53), then
+     (f32(acc) * sx) * s_channel in fp32 and one rounding, compared bit for bit; the float64
+     accumulators of the sampled rows are checked against the oracle's int64 GEMM first.
 Bar: relative Frobenius error < 1e-3 and max-abs error < 2e-2 against float64.
 
 Mid-size cases run each large-tile kernel variant with at least 8 k-tiles per pipeline stage.
@@ -29,6 +31,7 @@ import pytest
 import torch
 
 import oracle as O
+from a8_check import check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -176,12 +179,12 @@ def a8_case(m, n, k, bits, gs, g, seed, srel_dtype=torch.float16, outliers=True)
         sr32 = s_rel.float().numpy()
     w8 = O.w4a8_int8_grid(q.numpy(), sr32, None, k, bits, gs)
     assert torch.equal(Q.w4a8_int8_grid(qd, srd, None, gs).cpu(), torch.from_numpy(w8)), what + ": weight grid"
-    xq, sx = Q.quantize_int8_rowwise(xd, g)
-    sx = sx.reshape(-1)
-    w8d = torch.from_numpy(w8).to(DEV)
-    acc = xq.double() @ w8d.double().T                      # exact integer sums
     rows = sample_rows(m, seed)
     rows_d = torch.from_numpy(rows).to(DEV)
+    # the activation leg: rotation within one ulp of the oracle's, codes and scales bit-exact
+    xq, sx = check_a8_activation_rows(Q, xd, g, rows, what + ": activation quantization")
+    w8d = torch.from_numpy(w8).to(DEV)
+    acc = xq.double() @ w8d.double().T                      # exact integer sums
     acc_o = O.int8_gemm_i64(xq[rows_d].cpu().numpy(), w8)
     assert np.array_equal(acc[rows_d].cpu().numpy().astype(np.int64), acc_o), what + ": float64 replay != int64 oracle"
     replay = ((acc.float() * sx[:, None]) * scd[None, :]).half()

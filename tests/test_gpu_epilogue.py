@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle as O
+from a8_check import check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -92,7 +93,7 @@ def test_w4a8_linear_residual_single_rounding():
     s_ch = torch.ones(n)
     x = torch.randint(-100, 101, (m, k), generator=g).half()
     Q = qlin()
-    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), 0)
+    xq, sx = check_a8_activation_rows(Q, x.to(DEV), 0, np.arange(m), "A8 residual case: activations")
     w8 = Q.w4a8_int8_grid(q.to(DEV), s_rel.to(DEV), None, 128)
     acc = (xq.double() @ w8.double().T).cpu()
     lin = ((acc.float() * sx.cpu().reshape(-1, 1)) * s_ch[None, :])  # the A8 epilogue in fp32

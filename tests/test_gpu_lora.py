@@ -274,14 +274,19 @@ def test_int8_lora_fused_into_gemm(r, fdt, xdt, fused_calls):
         check_full(y[rows.to(DEV)], want, f"int8 fused full r={r}")
 
 
-@pytest.mark.parametrize("bits,m,r,fdt", [(4, 1024, 64, torch.bfloat16), (6, 2048, 32, torch.float16),
-                                          (6, 1100, 32, torch.float32), (4, 200, 16, torch.bfloat16)])
-def test_w4a8_lora_fused_into_gemm(bits, m, r, fdt, fused_calls):
+@pytest.mark.parametrize("bits,m,n,r,fdt", [
+    (4, 2048, 6144, 64, torch.bfloat16),   # 8 x 24 = 192 tiles of 256 x 256
+    (6, 2304, 6144, 32, torch.float32),    # 9 x 24 = 216 tiles of 256 x 256, fp32 up factors
+    (6, 2048, 4096, 32, torch.float16),    # 128 x 256 tiles (128 of 256 x 256 would not fill the GPU)
+    (4, 1024, 2048, 64, torch.bfloat16),   # 128 x 128 tiles
+    (6, 1100, 1024, 32, torch.float32),    # 128 x 64 tiles (fewer than 128 tiles of 128 x 128)
+    (4, 200, 2048, 16, torch.bfloat16),    # 128 x 64 tiles, a few hundred rows
+])
+def test_w4a8_lora_fused_into_gemm(bits, m, n, r, fdt, fused_calls):
     """A8 calls whose weight grid is decoded once (from 512 rows, and above 32 rows on grids of fewer
-    than 192 tiles of 256 x 256), then the DMA GEMM that carries the LoRA term (256 x 256 tiles at
-    M2048 N4096, 128 x 256 at M1024, 128 x 128 at M1100 N1024 and M200 N2048)."""
+    than 192 tiles of 256 x 256), then the DMA GEMM that carries the LoRA term, at each of its tile
+    shapes: 256 x 256 from 192 such tiles, else 128 x 256, 128 x 128 or 128 x 64."""
     Q = qlin()
-    n = 4096 if m == 2048 else (1024 if m == 1100 else 2048)
     k, g, gs = 1024, 256, 64
     gen = torch.Generator().manual_seed(30 + bits)
     hi = 15 if bits == 4 else 63

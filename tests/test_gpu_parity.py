@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle as O
+from a8_check import assert_quantized_like_oracle, assert_rotation_close, check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -512,6 +513,31 @@ def test_quantize_act_rotated(g):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), ws.view(np.uint32))
 
 
+
+# Row widths of the A8 calls the benchmark runs and the prologue variant each takes: K = 3072 with
+# G = 128 (W4A8 MLP-up; one slot of 16 values per thread), K = 5120 with G = 256 (W6A8 FFN up; one
+# slot), K = 13824 with G = 256 (W6A8 FFN down; two slots), K = 24576 (two slots, 768 threads), and
+# the two-pass wide kernel (four slots per chunk) at K = 65536 and 73728.
+A8_WIDTHS = [(3072, 128, 40), (5120, 256, 40), (13824, 256, 24), (24576, 128, 12), (65536, 128, 6),
+             (73728, 256, 5)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("k,g,m", A8_WIDTHS)
+def test_quantize_act_rotated_widths(k, g, m, dt):
+    """quantize_int8_rowwise(rot(x)) at every A8 width, fp16 and bf16 rows with 1% outliers at 20
+    sigma, a zero row and a tiny row: the rotated rows within one ulp of the oracle's exact rotation,
+    the codes and scales of those rows bit-exact against the oracle's quantize_int8_rowwise."""
+    x = x_fp16(m, k, seed=k + g, outliers=True).float()
+    x[1] = 0.0
+    x[2] = x[2] * 1e-6
+    x = x.to(dt)
+    q, s, xr = qlin().quantize_int8_rowwise(x.to(DEV), g, return_rotated=True)
+    what = f"K={k} G={g} {dt}"
+    assert_rotation_close(x, xr.cpu(), g, what)
+    assert_quantized_like_oracle(xr.cpu(), q.cpu(), s.cpu(), what)
+
+
 W4A8_CASES = [
     (4, 16, "auto", torch.float8_e4m3fn),
     (4, 128, None, torch.float16),
@@ -538,7 +564,7 @@ def test_w4a8_linear(bits, gs, cb, srdt, m):
     w8 = O.w4a8_int8_grid(q.numpy(), sr32, None if book is None else book.numpy(), k, bits, gs)
     assert np.array_equal(Q.w4a8_int8_grid(dev(q), dev(s_rel), dev(book), gs).cpu().numpy(), w8)
     # (2) exact replay of the int8 GEMM + epilogue on the activations the GPU quantized
-    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), g)
+    xq, sx = check_a8_activation_rows(Q, x.to(DEV), g, np.arange(m), f"bits={bits} gs={gs} M={m}: activations")
     xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
     acc = O.int8_gemm_i64(xq, w8)
     replay = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * s_ch.numpy()[None, :]).astype(np.float32)
@@ -588,7 +614,7 @@ def test_w4a8_linear_large_tiles(bits, cb, srdt, gs, k, m, n):
     Q = qlin()
     y = Q.w4a8_int8_linear(x.to(DEV), dev(q), dev(s_rel), dev(s_ch), dev(book), None, None, gs, g)
     w8 = O.w4a8_int8_grid(q.numpy(), s_rel.float().numpy(), None if book is None else book.numpy(), k, bits, gs)
-    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), g)
+    xq, sx = check_a8_activation_rows(Q, x.to(DEV), g, np.unique([0, m // 2, m - 1]), f"bits={bits} M={m}: activations")
     xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
     acc = O.int8_gemm_i64(xq, w8)
     replay = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * s_ch.numpy()[None, :]).astype(np.float32)

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle as O
+from a8_check import check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -200,7 +201,7 @@ def test_w4a8_linear_small_m(bits, gs, srdt, cb, k, m):
     else:
         sr32 = s_rel.float().numpy()
     w8 = O.w4a8_int8_grid(q.numpy(), sr32, None if book is None else book.numpy(), k, bits, gs)
-    xq, sx = Q.quantize_int8_rowwise(x.to(DEV), g)
+    xq, sx = check_a8_activation_rows(Q, x.to(DEV), g, np.arange(m), f"w{bits}a8 M={m} K={k}: activations")
     xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
     # exact replay of the int32 GEMM and the epilogue ((f32(acc) * sx) * s_channel) + bias
     acc = O.int8_gemm_i64(xq, w8)

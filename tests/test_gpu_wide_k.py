@@ -16,6 +16,7 @@ import pytest
 import torch
 
 import oracle as O
+from a8_check import check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -99,14 +100,13 @@ def test_w4a8_linear_wide_k(m, bits, gs):
     y = Q.w4a8_int8_linear(xd, qd, srd, scd, None, None, None, gs, g)
     what = f"w{bits}a8 M={m} K={k}"
     w8 = O.w4a8_int8_grid(q.numpy(), s_rel.float().numpy(), None, k, bits, gs)
-    xq, sx = Q.quantize_int8_rowwise(xd, g)
-    sx = sx.reshape(-1)
+    rows = rows_of(m)
+    rd = torch.from_numpy(rows).to(DEV)
+    xq, sx = check_a8_activation_rows(Q, xd, g, rows, what + ": activation quantization")
     acc = xq.double() @ torch.from_numpy(w8).to(DEV).double().T  # exact: |acc| < 2^53
     replay = ((acc.float() * sx[:, None]) * scd[None, :]).half()
     nbad = int((y.view(torch.int16) != replay.view(torch.int16)).sum().item())
     assert nbad == 0, f"{what}: {nbad} outputs differ from the exact replay"
-    rows = rows_of(m)
-    rd = torch.from_numpy(rows).to(DEV)
     acc_o = O.int8_gemm_i64(xq[rd].cpu().numpy(), w8)
     assert np.array_equal(acc[rd].cpu().numpy().astype(np.int64), acc_o), what + ": replay != int64 oracle"
     sxn = sx[rd].cpu().numpy()
