@@ -8,8 +8,6 @@ path.
 GGUF: simple absmax/min-max block quantizers writing the standard block layouts
 (docs/research/2026-10-03-gguf-on-metal.md:18-36).  They are not ggml's search-based
 quantizers; bit-exactness is judged on the decode of the same bytes, not on quantizer equality.
-Also ``random_gguf_blocks``: random legal blocks with fp16 scale fields sized for |w| ~ 0.02-0.05,
-the reference's own benchmark input (bench/bench_gguf_linear.py:34-40, 69-78).
 """
 from __future__ import annotations
 
@@ -19,29 +17,6 @@ from .gguf import GGUF_TYPES, gguf_type_id, GGUF_NAMES
 
 # ggml IQ4_NL levels (public ggml kvalues_iq4nl).
 IQ4NL_LEVELS = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int8)
-
-# Byte offsets of the fp16 scale fields and a magnitude that gives |w| ~ 0.02-0.05
-# (bench/bench_gguf_linear.py:35-40).
-F16_FIELDS = {
-    "Q4_0": ([0], 5e-3), "Q4_1": ([0, 2], 3e-3), "Q5_0": ([0], 2.5e-3), "Q5_1": ([0, 2], 1.5e-3),
-    "Q8_0": ([0], 3e-4), "Q2_K": ([80, 82], 1e-3), "Q3_K": ([108], 2e-4), "Q4_K": ([0, 2], 5e-5),
-    "Q5_K": ([0, 2], 2.5e-5), "Q6_K": ([208], 3e-5), "IQ4_NL": ([0], 3e-4), "IQ4_XS": ([0], 1e-5),
-}
-
-
-def random_gguf_blocks(qtype, n, k, seed=0):
-    """Random legal blocks (every byte pattern is a legal block) with realistic fp16 scales."""
-    name = GGUF_NAMES[gguf_type_id(qtype)]
-    _, qk, ts = GGUF_TYPES[name]
-    rng = np.random.default_rng(seed)
-    nb = n * k // qk
-    raw = rng.integers(0, 256, size=(nb, ts), dtype=np.uint8)
-    offs, mag = F16_FIELDS[name]
-    for off in offs:
-        v = np.abs(rng.standard_normal(nb) * mag + mag).astype(np.float16)
-        raw[:, off:off + 2] = v.view(np.uint8).reshape(nb, 2)
-    return raw.reshape(n, k // qk * ts) if k % qk == 0 else raw.reshape(-1)
-
 
 def _f16(x):
     return np.asarray(x, dtype=np.float32).astype(np.float16)

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle as O
+from gguf_blocks import random_gguf_blocks
 from a8_check import check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
@@ -64,7 +65,7 @@ def test_int8_linear_residual(m, rdt):
 def test_gguf_linear_residual_with_lora(name, m):
     """Bias, LoRA and residual together: residual + rs * (x W^T + b + scale x down^T up^T)."""
     n, k, r = 256, 1024, 16
-    raw = qz().random_gguf_blocks(name, n, k, seed=4)
+    raw = random_gguf_blocks(name, n, k, seed=4)
     wdec = O.gguf_dequantize(raw, name, (n, k))
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).half()
     b = torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import oracle as O
+from gguf_blocks import random_gguf_blocks
 from a8_check import assert_quantized_like_oracle, assert_rotation_close, check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
@@ -62,7 +63,7 @@ def x_fp16(m, k, seed=1, outliers=False):
 @pytest.mark.parametrize("name", GGUF)
 def test_dequantize_gguf_bit_exact(name):
     n, k = 40, 1024
-    for seed, raw in ((0, qz().random_gguf_blocks(name, n, k, seed=3)),
+    for seed, raw in ((0, random_gguf_blocks(name, n, k, seed=3)),
                       (1, qz().quantize_gguf(np.random.default_rng(4).standard_normal((n, k)).astype(np.float32) * 0.02, name))):
         want = O.gguf_dequantize(raw, name, (n, k))
         w = torch.from_numpy(np.ascontiguousarray(raw)).to(DEV)
@@ -88,7 +89,7 @@ def test_dequantize_gguf_golden(case, fmt, name):
 def test_dequantize_gguf_special_scales(name):
     """fp16 scale fields of 0, +-65504 and subnormals decode exactly."""
     _, qk, ts = O.GGUF_TYPES[name]
-    raw = qz().random_gguf_blocks(name, 8, 512, seed=9).reshape(-1, ts)
+    raw = random_gguf_blocks(name, 8, 512, seed=9).reshape(-1, ts)
     specials = np.array([0.0, 65504.0, -65504.0, 6e-8, -3e-6, 2 ** -24, 1.0, -0.0], dtype=np.float16).view(np.uint8)
     offs = {"Q8_0": [0], "Q4_K": [0, 2], "Q6_K": [208], "Q4_0": [0], "IQ4_XS": [0]}[name]
     for i in range(raw.shape[0]):
@@ -105,7 +106,7 @@ def test_dequantize_gguf_straddling_rows(name):
     blocks but K is not."""
     _, qk, ts = O.GGUF_TYPES[name]
     n, k = 32, qk * 3 // 2 if qk == 256 else 48
-    raw = qz().random_gguf_blocks(name, 1, n * k, seed=2).reshape(-1)
+    raw = random_gguf_blocks(name, 1, n * k, seed=2).reshape(-1)
     want = O.gguf_dequantize(raw, name).reshape(n, k)
     got = qlin().dequantize_gguf(torch.from_numpy(raw.copy()).to(DEV), name, (n, k)).cpu().numpy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -119,7 +120,7 @@ def test_dequantize_gguf_straddling_rows(name):
 @pytest.mark.parametrize("m", [1, 4, 5, 8, 16, 17, 64, 100, 128, 129])  # every kernel and each switch point
 def test_gguf_linear(name, m):
     n, k = 80, 1024
-    raw = qz().random_gguf_blocks(name, n, k, seed=11)
+    raw = random_gguf_blocks(name, n, k, seed=11)
     w = O.gguf_dequantize(raw, name, (n, k))
     x = x_fp16(m, k, seed=m)
     want = O.linear_ref(x.float().numpy(), w)
@@ -143,7 +144,7 @@ def test_gguf_linear(name, m):
 ])
 def test_gguf_linear_split_k(name, m, n, k):
     """The K-split kernel (M = 17..64): ragged N, uneven and single splits, bias."""
-    raw = qz().random_gguf_blocks(name, n, k, seed=21)
+    raw = random_gguf_blocks(name, n, k, seed=21)
     w = O.gguf_dequantize(raw, name, (n, k))
     x = x_fp16(m, k, seed=m + 3)
     b = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.1).half()
@@ -174,7 +175,7 @@ def test_gguf_linear_split_k_workspace_contents(fill):
     and bit-identical to the others (the partials are added in split order)."""
     Q = qlin()
     name, m, n, k = "Q4_K", 64, 4096, 4096  # 32 row blocks x 8 splits
-    raw = qz().random_gguf_blocks(name, n, k, seed=51)
+    raw = random_gguf_blocks(name, n, k, seed=51)
     w = O.gguf_dequantize(raw, name, (n, k))
     x = x_fp16(m, k, seed=52)
     want = O.linear_ref(x.float().numpy(), w)
@@ -204,7 +205,7 @@ def test_gguf_linear_split_k_graph_replays():
     activations between the replays: every replay equals the eager call on the same input."""
     Q = qlin()
     name, m, n, k = "Q6_K", 48, 4096, 2048
-    raw = torch.from_numpy(qz().random_gguf_blocks(name, n, k, seed=61)).to(DEV)
+    raw = torch.from_numpy(random_gguf_blocks(name, n, k, seed=61)).to(DEV)
     xs = [x_fp16(m, k, seed=62 + i).to(DEV) for i in range(4)]
     xin = xs[0].clone()
     s = torch.cuda.Stream()
@@ -246,7 +247,7 @@ def test_gguf_linear_decode_once(name, m, n, k):
     copy left unwritten shows."""
     from qlin import _lib
     L = _lib.load()
-    raw = qz().random_gguf_blocks(name, n, k, seed=71)
+    raw = random_gguf_blocks(name, n, k, seed=71)
     w = O.gguf_dequantize(raw, name, (n, k))
     x = x_fp16(m, k, seed=m + 7)
     b = (torch.randn(n, generator=torch.Generator().manual_seed(9)) * 0.1).half()
@@ -296,7 +297,7 @@ def test_gguf_linear_decode_once(name, m, n, k):
 @pytest.mark.parametrize("m,k", [(1, 2048), (1, 4096), (1, 8192), (8, 4096), (16, 8192)])
 def test_gguf_linear_long_k(name, m, k):
     n = 72
-    raw = qz().random_gguf_blocks(name, n, k, seed=31)
+    raw = random_gguf_blocks(name, n, k, seed=31)
     w = O.gguf_dequantize(raw, name, (n, k))
     x = x_fp16(m, k, seed=k + m)
     b = (torch.randn(n, generator=torch.Generator().manual_seed(6)) * 0.1).half()
@@ -311,7 +312,7 @@ def test_gguf_linear_decode_workload(name):
     """The benchmarked calls themselves: K = N = 4096 at M = 1, 8 and 64 (GEMV, small-M or K split,
     and the K split with its XCD-local reduction, S = 8)."""
     n = k = 4096
-    raw = qz().random_gguf_blocks(name, n, k, seed=41)
+    raw = random_gguf_blocks(name, n, k, seed=41)
     w = O.gguf_dequantize(raw, name, (n, k))
     wd = torch.from_numpy(raw).to(DEV)
     for m in (1, 8, 64):
@@ -325,7 +326,7 @@ def test_gguf_linear_decode_workload(name):
 @pytest.mark.parametrize("m", [3, 40, 200])
 def test_gguf_linear_dtypes_and_bias(xdt, odt, m):
     name, n, k = "Q4_K", 96, 512
-    raw = qz().random_gguf_blocks(name, n, k, seed=5)
+    raw = random_gguf_blocks(name, n, k, seed=5)
     w = O.gguf_dequantize(raw, name, (n, k))
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(3)).to(xdt)
     b = torch.randn(n, generator=torch.Generator().manual_seed(4)) * 0.1
@@ -344,7 +345,7 @@ def test_gguf_linear_dtypes_and_bias(xdt, odt, m):
 def test_gguf_linear_large_activations_near_max_scales():
     """|x| ~ 3e4 against near-max fp16 block scales: fp32 accumulation, no overflow."""
     name, n, k = "Q8_0", 32, 256
-    raw = qz().random_gguf_blocks(name, n, k, seed=6).reshape(-1, 34)
+    raw = random_gguf_blocks(name, n, k, seed=6).reshape(-1, 34)
     raw[:, :2] = np.array([60000.0], dtype=np.float16).view(np.uint8)
     raw = raw.reshape(n, -1)
     w = O.gguf_dequantize(raw, name, (n, k))
@@ -359,7 +360,7 @@ def test_gguf_linear_large_activations_near_max_scales():
 def test_gguf_linear_shapes_and_empty():
     Q = qlin()
     name, n, k = "Q4_0", 48, 256
-    raw = torch.from_numpy(qz().random_gguf_blocks(name, n, k, seed=1)).to(DEV)
+    raw = torch.from_numpy(random_gguf_blocks(name, n, k, seed=1)).to(DEV)
     x = torch.randn(2, 3, k, device=DEV).half()
     y = Q.gguf_linear(x, raw, name, (n, k))
     assert y.shape == (2, 3, n)

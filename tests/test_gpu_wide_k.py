@@ -16,6 +16,7 @@ import pytest
 import torch
 
 import oracle as O
+from gguf_blocks import random_gguf_blocks
 from a8_check import check_a8_activation_rows
 
 pytestmark = pytest.mark.gpu
@@ -71,7 +72,7 @@ def test_int8_linear_wide_k(m, k, g, xdt):
 @pytest.mark.parametrize("m", [1, 8, 40, 100])
 def test_gguf_linear_wide_k(name, m):
     n, k = 64, 65536
-    raw = qz().random_gguf_blocks(name, n, k, seed=m + 7)
+    raw = random_gguf_blocks(name, n, k, seed=m + 7)
     wdq = O.gguf_dequantize(raw, name, (n, k))
     # |w| ~ 0.02-0.05: activations of 0.5 keep outputs of order 10 over 65536 terms
     x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m)) * 0.5).half()

@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import oracle as O
+from gguf_blocks import random_gguf_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -42,7 +43,6 @@ def with_workspace(x, raw, name, n, k, bias=None, out_dtype=torch.float16):
 
 
 def case(name, m, n, k, seed, xdt=torch.float16, odt=torch.float16, bias=False):
-    from qlin.quantize import random_gguf_blocks
     raw = random_gguf_blocks(name, n, k, seed=seed)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(seed + 1)).to(xdt)
     b = (torch.randn(n, generator=torch.Generator().manual_seed(seed + 2)) * 0.1).half() if bias else None
