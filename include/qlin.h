@@ -62,7 +62,7 @@ typedef enum {
     QLIN_OP_INT8_GRAD_INPUT = 4,  /* qlin_int8_linear_grad_input: M rows of dy, N outputs, K inputs */
     QLIN_OP_W4A8_GRAD_INPUT = 5,  /* qlin_w4a8_linear_grad_input (holds the decoded int8 grid, N*K bytes) */
     QLIN_OP_INT8_LINEAR_LORA = 6, /* qlin_int8_linear_lora: param = the LoRA rank R */
-    QLIN_OP_W4A8_LINEAR_LORA = 7, /* qlin_w4a8_linear_lora: param = the LoRA rank R */
+    QLIN_OP_W4A8_LINEAR_LORA = 7, /* qlin_w4a8_linear_lora: param = the LoRA rank R | group_size << 16 */
 } qlin_op;
 
 /* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
@@ -77,8 +77,11 @@ const char* qlin_status_string(qlin_status s);
 const char* qlin_last_error(void);
 
 /* Bytes of device workspace an op needs for activations of M rows against an [N, K] weight.
- * `param` is the ConvRot group size (INT8), bits (W4A8: 4 or 6) or the ggml type (GGUF).
- * `x_dtype` is the activation's qlin_dtype. */
+ * `param` is the ConvRot group size (INT8), bits | group_size << 8 (W4A8: bits 4 or 6) or the ggml
+ * type (GGUF).  The W4A8 group size decides whether the call decodes the int8 weight grid once into
+ * the workspace (N*K bytes; group sizes that are multiples of 64); without it (param = bits) the
+ * grid is counted whenever the shape alone would take that path.  `x_dtype` is the activation's
+ * qlin_dtype. */
 size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, int x_dtype);
 
 /* Capability probe: QLIN_OK if the op would accept these shapes/parameters, else
@@ -113,10 +116,11 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
  * consecutive blocks over the row-major [N,K] elements (the GGUF tensor bytes, N*K/qk*ts long).
  * Replaces comfy_kitchen.gguf_linear(x, weight, qtype, shape, bias, out_dtype)
  * (docs/research/2026-10-03-gguf-on-metal.md:85; bench/bench_gguf_linear.py:120).
- * Above 64 rows the size qlin_workspace_size reports includes an fp16 copy of the decoded weight
- * (N*K*2 bytes): the call decodes W once into it and runs the GEMM on the copy.  A workspace
- * without that room still works (the GEMM then decodes every weight tile it loads, much slower);
- * both meet the same accuracy bar, with different fp32 summation orders. */
+ * Above 64 rows the size qlin_workspace_size reports includes an fp16 copy of the decoded weight,
+ * at most 256 MiB of it (min(N, 256 MiB / (2K)) rows): the call decodes W once, in chunks of
+ * weight rows that fit the workspace (multiples of 128 rows), and runs the GEMM on each chunk.  A
+ * workspace without room for 128 decoded rows still works (the GEMM then decodes every weight tile
+ * it loads, much slower); all meet the same accuracy bar, with different fp32 summation orders. */
 qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                              const qlin_tensor* bias, qlin_tensor* y,
                              void* workspace, size_t workspace_bytes, void* stream);

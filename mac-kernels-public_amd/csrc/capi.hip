@@ -1,5 +1,6 @@
 // C ABI of libqlin (include/qlin.h): argument validation, workspace layout and dispatch.
 // Host code only; kernels live in the other translation units.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -161,10 +162,26 @@ size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
 }
 // Above GGUF_SMALLM_MAX_M rows the GEMM reads the weight once per 128-row tile: decoding it once
 // into the workspace (fp16, N x K) and loading it as stored beats decoding every tile (Q4_K,
-// K = N = 4096, M = 512: 200 us decoding in the GEMM).  The call takes that path when the
-// workspace holds the decoded copy beyond ws_gguf; the size query asks for it.
+// K = N = 4096, M = 512: 200 us decoding in the GEMM).  The copy is made in chunks of weight rows
+// of at most GGUF_DECODE_BYTES_MAX (the decode of chunk c + 1 follows the GEMM over chunk c on
+// the stream), so a large tensor such as a 128256 x 4096 output head needs 256 MiB of workspace,
+// not its whole 1 GiB fp16 copy.  The call takes this path when the workspace beyond ws_gguf
+// holds at least one chunk of GGUF_DECODE_CHUNK_ROWS rows (or all N); the size query asks for
+// min(N, the rows of GGUF_DECODE_BYTES_MAX) rows.
+constexpr int64_t GGUF_DECODE_BYTES_MAX = 256ll << 20;
+constexpr int64_t GGUF_DECODE_CHUNK_ROWS = 128;  // the GEMM's tile height along N
+// Rows of one decoded chunk that `bytes` of workspace hold (a multiple of the chunk unit, or N),
+// 0 when not even one unit fits.
+int64_t gguf_decode_rows(int64_t N, int64_t K, int64_t bytes) {
+    const int64_t fit = std::min<int64_t>(bytes, GGUF_DECODE_BYTES_MAX) / (K * 2);
+    if (fit >= N) return N;
+    return fit / GGUF_DECODE_CHUNK_ROWS * GGUF_DECODE_CHUNK_ROWS;
+}
 size_t ws_gguf_decoded(int64_t M, int64_t N, int64_t K) {
-    return M > GGUF_SMALLM_MAX_M ? align_up((size_t)(N * K * 2)) : 0;
+    if (M <= GGUF_SMALLM_MAX_M || N <= 0 || K <= 0) return 0;
+    const int64_t rows = std::max<int64_t>(gguf_decode_rows(N, K, GGUF_DECODE_BYTES_MAX),
+                                           std::min<int64_t>(N, GGUF_DECODE_CHUNK_ROWS));
+    return align_up((size_t)(rows * K * 2));
 }
 // input gradient: normalized dy rows (N rounded up to 128) + row exponents (+ the W4A8 int8 grid)
 size_t ws_grad(int64_t M, int64_t N, int64_t K, bool grid) {
@@ -172,8 +189,15 @@ size_t ws_grad(int64_t M, int64_t N, int64_t K, bool grid) {
     return align_up((size_t)(M * lda * 2)) + align_up((size_t)M * 4) + (grid ? align_up((size_t)(N * K)) : 0);
 }
 
-size_t ws_w4a8(int64_t M, int64_t N, int64_t K) {
-    return align_up((size_t)(M * K)) + align_up((size_t)M * 4) + (a8_decode_once(M, N, K) ? align_up((size_t)(N * K)) : 0);
+// A8 workspace: int8 activations and their scales, plus the decoded int8 grid (N * K bytes) where
+// the call decodes the weight once (a8_decode_once, and a group size that is a multiple of 64;
+// group_size 0 = not known, the grid is counted whenever the shape alone would take that path).
+bool a8_grid_in_workspace(int64_t M, int64_t N, int64_t K, int group_size) {
+    return a8_decode_once(M, N, K) && group_size % 64 == 0;
+}
+size_t ws_w4a8(int64_t M, int64_t N, int64_t K, int group_size) {
+    return align_up((size_t)(M * K)) + align_up((size_t)M * 4) +
+           (a8_grid_in_workspace(M, N, K, group_size) ? align_up((size_t)(N * K)) : 0);
 }
 
 // LoRA's low-rank activation t = x down^T: S fp32 K-split partials and their sum, or one [M, R].
@@ -298,12 +322,13 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
     (void)x_dtype;
     switch (op) {
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
-        case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K);
+        case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K, param >> 8);  // param: bits | group_size << 8
         case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K);
         case QLIN_OP_INT8_GRAD_INPUT: return ws_grad(M, N, K, false);
         case QLIN_OP_W4A8_GRAD_INPUT: return ws_grad(M, N, K, true);
         case QLIN_OP_INT8_LINEAR_LORA: return ws_int8(M, K) + ws_lora(M, K, param);
-        case QLIN_OP_W4A8_LINEAR_LORA: return ws_w4a8(M, N, K) + ws_lora(M, K, param);
+        case QLIN_OP_W4A8_LINEAR_LORA:  // param: R | group_size << 16
+            return ws_w4a8(M, N, K, param >> 16) + ws_lora(M, K, param & 0xFFFF);
         case QLIN_OP_LORA: {  // the split partials, then their sum
             const int S = lora_splits(M, K, param);
             return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(param > 0 ? param : 0) * 4);
@@ -698,13 +723,27 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
     a.gguf_type = ggml_type;
     a.M = M; a.N = N; a.K = K;
     a.wexp = wexp;
-    if (const size_t dec = ws_gguf_decoded(M, N, K); dec && workspace_bytes - ws.used >= dec) {
-        f16* w16 = (f16*)ws.take((size_t)(N * K * 2));
-        if ((s = hip_status(run_gguf_decode_f16(ggml_type, (const uint8_t*)weight, row_bytes, N, K, wexp, w16, st),
-                            "gguf decode")))
-            return s;
+    if (const int64_t rows = M > GGUF_SMALLM_MAX_M ? gguf_decode_rows(N, K, (int64_t)(workspace_bytes - ws.used)) : 0;
+        rows > 0) {
+        f16* w16 = (f16*)ws.take((size_t)(rows * K * 2));
         a.wkind = WO_F16;
         a.w = w16; a.ldw = K;
+        a.bias_dtype = bdt;
+        a.y_dtype = Y.dtype; a.ldy = Y.ld;
+        const size_t ysz = Y.dtype == QLIN_DT_F32 ? 4 : 2, bsz = bdt == QLIN_DT_F32 ? 4 : 2;
+        for (int64_t n0 = 0; n0 < N; n0 += rows) {
+            const int64_t nc = std::min(rows, N - n0);
+            if ((s = hip_status(run_gguf_decode_f16(ggml_type, (const uint8_t*)weight + n0 * row_bytes, row_bytes, nc, K,
+                                                    wexp + n0, w16, st),
+                                "gguf decode")))
+                return s;
+            a.N = nc;
+            a.wexp = wexp + n0;
+            a.bias = bias ? (const uint8_t*)bias->data + n0 * bsz : nullptr;
+            a.y = (uint8_t*)Y.data + n0 * ysz;
+            if ((s = hip_status(run_gemm_f16(a, st), "gguf gemm"))) return s;
+        }
+        return QLIN_OK;
     } else {
         if ((s = hip_status(run_gguf_row_exp(ggml_type, (const uint8_t*)weight, N, K, wexp, st), "gguf row exponents")))
             return s;
@@ -784,12 +823,13 @@ static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     Mat D{}, U{};
     if (L && (s = lora_operands(*L, N, K, D, U))) return s;
     const int64_t M = X.rows;
-    const size_t need = ws_w4a8(M, N, K) + (L ? ws_lora(M, K, D.rows) : 0);
+    const size_t need = ws_w4a8(M, N, K, group_size) + (L ? ws_lora(M, K, D.rows) : 0);
     if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
-    // workspace: int8 activations, their scales, the decoded weight grid (M >= 1024), then LoRA's t
+    // workspace: int8 activations, their scales, the decoded weight grid (a8_grid_in_workspace), then
+    // LoRA's t
     int8_t* qo = (int8_t*)ws.take((size_t)(M * K));
     float* so = (float*)ws.take((size_t)M * 4);
     GemmI8Args g;
@@ -800,15 +840,17 @@ static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     g.s_ch = (const float*)s_channel->data; g.codebook = cb;
     g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
     g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
-    if (a8_decode_once(M, N, K)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
+    if (a8_grid_in_workspace(M, N, K, group_size)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
     float* t = nullptr;
     if (L) {
         t = (float*)ws.take(ws_lora(M, K, D.rows));
         g.lora.t = lora_t_final(t, M, K, D.rows); g.lora.up = U.data; g.lora.up_dt = U.dtype; g.lora.ld_up = U.ld;
         g.lora.R = D.rows; g.lora.scale = L->scale;
         if (!gemm_i8_fuses_lora(g))
-            return fail(QLIN_EUNSUPPORTED, "the LoRA term is fused only into the decode-once GEMM (M >= 1024, rank a "
-                                           "multiple of 8, 16-byte aligned lora_up rows)");
+            return fail(QLIN_EUNSUPPORTED, "the LoRA term is fused only into the A8 GEMM that runs after the weight grid is decoded "
+                                           "once (from 512 rows, or above 32 rows on grids of fewer than 192 tiles of 256 x "
+                                           "256; a group size that is a multiple of 64), for a rank that is a multiple of 8 "
+                                           "with 16-byte aligned lora_up rows");
         const float* tf = nullptr;
         if ((s = hip_status(run_lora_t(lora_down_args(X, D, t), st, &tf), "lora down"))) return s;
     }

@@ -335,13 +335,13 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     # once, and declines elsewhere
     if m > 32 and lora is not None:
         def run(down, up, lscale):
-            wsl = _workspace(_lib.OP_W4A8_LINEAR_LORA, m, n, k, down.shape[0], x2, stream)
+            wsl = _workspace(_lib.OP_W4A8_LINEAR_LORA, m, n, k, down.shape[0] | int(group_size) << 16, x2, stream)
             return L.qlin_w4a8_linear_lora(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
                                            _lib.desc(b), _lib.desc(y), bits, int(group_size), int(convrot_groupsize or 0),
                                            _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(), stream)
         if _fused_lora(op, lora, res, x2, run):
             return _shaped(y, shape)
-    ws = _workspace(_lib.OP_W4A8_LINEAR, m, n, k, bits, x2, stream)
+    ws = _workspace(_lib.OP_W4A8_LINEAR, m, n, k, bits | int(group_size) << 8, x2, stream)
     yb = _base_out(lora, y, res)
     st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
                             _lib.desc(b), _lib.desc(yb), bits, int(group_size), int(convrot_groupsize or 0),

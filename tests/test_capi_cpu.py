@@ -47,6 +47,31 @@ def test_query_and_workspace():
     assert ws >= 256 * 3072 * 2 + 256 * 4
 
 
+def test_workspace_sizes_follow_the_paths():
+    """The sizes the C ABI asks for: the A8 int8 grid (N*K bytes) only where the call decodes the
+    weight once (from 512 rows, with a group size that is a multiple of 64; counted when the group
+    size is not given), and the GGUF decoded fp16 copy above 64 rows, capped at 256 MiB."""
+    from qlin import _lib
+    L = _lib.load()
+    a = lambda v: (v + 255) // 256 * 256
+    m, n, k = 1024, 4096, 4096
+    act = a(m * k) + a(m * 4)
+    size = lambda p: L.qlin_workspace_size(_lib.OP_W4A8_LINEAR, m, n, k, p, _lib.DT_F16)
+    assert size(4 | 16 << 8) == act                  # group 16: decoded per tile, no grid
+    assert size(4 | 64 << 8) == act + a(n * k)       # group 64: the grid
+    assert size(6 | 128 << 8) == act + a(n * k)
+    assert size(4) == act + a(n * k)                 # group size not given: counted
+    assert L.qlin_workspace_size(_lib.OP_W4A8_LINEAR, 16, n, k, 4 | 64 << 8, _lib.DT_F16) == a(16 * k) + a(16 * 4)
+    lora = lambda p: L.qlin_workspace_size(_lib.OP_W4A8_LINEAR_LORA, m, n, k, p, _lib.DT_F16)
+    assert lora(64 | 64 << 16) - lora(64 | 16 << 16) == a(n * k)
+    # GGUF above 64 rows: the decoded copy, at most 256 MiB (32768 rows of K = 4096)
+    g = lambda m, n: L.qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, 4096, 12, _lib.DT_F16)
+    base = lambda m, n: a(m * 4096 * 2) + a(m * 4) + a(n * 4)
+    assert g(100, 4096) == base(100, 4096) + a(4096 * 4096 * 2)
+    assert g(100, 128256) == base(100, 128256) + (256 << 20)
+    assert g(64, 128256) < (64 << 20)                # K split or small-M kernels: no copy
+
+
 def _d(t, dt=None):
     from qlin import _lib
     return _lib.desc(t, dt)

@@ -321,6 +321,38 @@ def test_gguf_linear_decode_workload(name):
         check_linear(got, O.linear_ref(x.float().numpy(), w), f"{name} M={m} K=N=4096")
 
 
+@pytest.mark.parametrize("name,odt", [("Q4_K", torch.float16), ("Q6_K", torch.bfloat16), ("Q8_0", torch.float32)])
+def test_gguf_linear_decode_in_chunks(name, odt):
+    """Above 64 rows the weight is decoded once into the workspace in chunks of weight rows (at most
+    256 MiB each, multiples of 128 rows): with the workspace the size query asks for (one chunk
+    here), with room for 256 rows (four chunks, the last ragged) or 130 rows (128-row chunks), the
+    output equals the oracle's linear to the bar; with no room for 128 rows each GEMM tile decodes
+    its own weights."""
+    from qlin import _lib as L
+    m, n, k = 100, 1000, 2048
+    raw = random_gguf_blocks(name, n, k, seed=77)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    # activations of 0.25: outputs below 4, where one bf16 rounding step stays under the 2e-2 bar
+    x = (x_fp16(m, k, seed=78).float() * 0.25).half()
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(79)) * 0.1).half()
+    want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
+    if odt == torch.bfloat16:
+        want = torch.from_numpy(want.astype(np.float32)).bfloat16().double().numpy()
+    tid = O.gguf_type_id(name)
+    full = L.load().qlin_workspace_size(L.OP_GGUF_LINEAR, m, n, k, tid, L.DT_F16)
+    align = lambda v: (v + 255) // 256 * 256
+    base = full - align(n * k * 2)   # everything but the decoded copy
+    xd, rd, bd = x.to(DEV), torch.from_numpy(raw).to(DEV), b.to(DEV)
+    for rows in (n, 256, 130, 100):
+        nbytes = base + align(rows * k * 2)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        y = torch.full((m, n), float("nan"), dtype=odt, device=DEV)
+        st = L.load().qlin_gguf_linear(L.desc(xd), rd.data_ptr(), tid, n, k, L.desc(bd), L.desc(y), ws.data_ptr(),
+                                       ws.numel(), L.stream_of(xd.device))
+        L.check(st, "qlin_gguf_linear")
+        check_linear(y, want, f"{name} M={m} N={n} K={k}, workspace for {rows} decoded rows")
+
+
 @pytest.mark.parametrize("xdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                      (torch.float32, torch.float32), (torch.float16, torch.float32)])
 @pytest.mark.parametrize("m", [3, 40, 200])
