@@ -4,7 +4,8 @@
 
 Each .hip translation unit is compiled to an object in parallel, then linked into
 mac-kernels-public_amd/qlin/libqlin.so.  The hardware-floor probes of the measurement suite
-(probe/floors.hip) go into a library of their own, qlin/libqlin_floors.so.  Packed-FP32 VALU
+(probe/floors.hip) go into a library of their own, qlin/libqlin_floors.so, and the eager PyTorch
+entry points (csrc/torch_ops.cpp) into the module qlin/_qlin_torch.so.  Packed-FP32 VALU
 instructions are disabled for all device code (-Xclang -target-feature -Xclang -packed-fp32-ops).
 """
 import argparse
@@ -69,7 +70,35 @@ def build(jobs=None, verbose=False, force=True):
         raise RuntimeError("link failed")
     os.replace(tmp, OUT)
     build_floors()
+    build_torch_ops()
     return OUT
+
+
+def build_torch_ops():
+    """qlin/_qlin_torch.so: the eager PyTorch entry points (csrc/torch_ops.cpp), a host-only C++
+    module linked against libqlin.so and torch; built with the system C++ compiler."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+    src = os.path.join(CSRC, "torch_ops.cpp")
+    out = os.path.join(HERE, "qlin", "_qlin_torch.so")
+    tmp = out + ".tmp"
+    tlib = ce.library_paths()[0]
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w", src, "-o", tmp,
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=_qlin_torch",
+           "-DTORCH_API_INCLUDE_EXTENSION_H", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           "-I", os.path.join(HERE, "..", "include"), "-I", "/opt/rocm/include", "-I", sysconfig.get_paths()["include"],
+           *[a for p in ce.include_paths() for a in ("-I", p)],
+           "-L", os.path.dirname(OUT), "-lqlin", "-L", tlib, "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", "-L", "/opt/rocm/lib", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}", "-Wl,-rpath,/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        print(r.stderr, file=sys.stderr)
+        raise RuntimeError("g++ failed on torch_ops.cpp")
+    os.replace(tmp, out)
+    return out
 
 
 def build_floors():

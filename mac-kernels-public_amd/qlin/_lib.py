@@ -162,6 +162,11 @@ def workspace(nbytes: int, device: torch.device, stream: int) -> torch.Tensor:
 def release_workspaces() -> None:
     """Drop the cached per-stream workspaces (their memory returns to torch's allocator)."""
     _ws_cache.clear()
+    try:
+        from . import _qlin_torch
+    except ImportError:  # pragma: no cover
+        return
+    _qlin_torch.release_workspaces()
 
 
 def check(status: int, op: str):

@@ -19,8 +19,31 @@ import os
 import torch
 
 from . import _lib
-from .exceptions import NoCapableBackendError
+from .exceptions import NoCapableBackendError, QlinError
 from .gguf import GGUF_TYPES, gguf_type_id
+
+# The eager entry points of csrc/torch_ops.cpp (qlin/_qlin_torch.so): plain linears (no LoRA, no
+# residual) go from Python to the C ABI in one C++ call.  Every other call, and every call when the
+# module is not built, takes the ctypes route below; both run the same kernels through the same
+# C ABI.
+try:
+    from . import _qlin_torch as _FAST
+except ImportError:  # pragma: no cover - only when the module was not built
+    _FAST = None
+if _FAST is not None:
+    _FAST.set_gguf_types({tid: (qk, ts) for tid, qk, ts in GGUF_TYPES.values()})
+    _FastError = _FAST.QlinStatusError
+
+
+def _fast_error(op, e):
+    """The exception ops raise for a status the C++ entry point reported as "<status>:<message>"."""
+    status, _, msg = str(e).partition(":")
+    status = int(status)
+    if status == _lib.QLIN_EUNSUPPORTED:
+        return NoCapableBackendError(op, {"hip": msg})
+    if status in (_lib.QLIN_EINVAL, _lib.QLIN_EWORKSPACE):
+        return ValueError(f"{op}: {msg}")
+    return QlinError(f"{op}: {msg}")
 
 _FLOAT = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -191,13 +214,17 @@ _WS_SIZES: dict = {}
 
 
 def _workspace(op, m, n, k, param, x2, stream=None):
-    """The per-stream workspace for one call (sizes cached per shape; the C ABI computes them)."""
+    """The per-stream workspace for one call (sizes cached per shape; the C ABI computes them).  With
+    the C++ module the buffer comes from its cache, which its own calls use too (the current stream
+    of x2's device is the stream every op here runs on)."""
     key = (op, m, n, k, param, x2.dtype)
     nbytes = _WS_SIZES.get(key)
     if nbytes is None:
         if len(_WS_SIZES) > 4096:
             _WS_SIZES.clear()
         nbytes = _WS_SIZES[key] = _lib.load().qlin_workspace_size(op, m, n, k, param, _lib._TORCH_DT[x2.dtype])
+    if _FAST is not None:
+        return _FAST.workspace(nbytes, x2)
     return _lib.workspace(nbytes, x2.device, _lib.stream_of(x2.device) if stream is None else stream)
 
 
@@ -231,6 +258,12 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
     ([.., N]): y = residual + residual_scale * (linear + bias + LoRA), one rounding."""
     op = "int8_linear"
     _disabled(op)
+    if _FAST is not None and lora_down is None and lora_up is None and lora_scale is None and residual is None \
+            and residual_scale is None:
+        try:
+            return _FAST.int8_linear(x, qdata, scale, bias, out_dtype, int(convrot_groupsize) if convrot else 0)
+        except _FastError as e:
+            raise _fast_error(op, e) from None
     _check_device(op, x, qdata, scale, bias)
     if qdata.dtype != torch.int8 or qdata.dim() != 2:
         raise NoCapableBackendError(op, {"hip": "qdata must be a 2-D int8 tensor"})
@@ -313,6 +346,13 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
     _disabled(op)
     if correction is not None:
         raise NoCapableBackendError(op, {"hip": "the asymmetric `correction` variant is not implemented"})
+    if _FAST is not None and lora_down is None and lora_up is None and lora_scale is None and residual is None \
+            and residual_scale is None:
+        try:
+            return _FAST.w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook, bias, int(group_size),
+                                          int(convrot_groupsize or 0), out_dtype)
+        except _FastError as e:
+            raise _fast_error(op, e) from None
     _check_device(op, x, qdata, s_rel, s_channel, codebook, bias)
     if x.dtype not in _FLOAT:
         raise NoCapableBackendError(op, {"hip": f"x dtype {x.dtype} unsupported"})
@@ -418,9 +458,15 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
     int8_linear."""
     op = "gguf_linear"
     _disabled(op)
-    _check_device(op, x, weight, bias)
     tid = gguf_type_id(qtype)
     n, k = int(shape[0]), int(shape[1])
+    if _FAST is not None and lora_down is None and lora_up is None and lora_scale is None and residual is None \
+            and residual_scale is None:
+        try:
+            return _FAST.gguf_linear(x, weight, tid, n, k, bias, out_dtype)
+        except _FastError as e:
+            raise _fast_error(op, e) from None
+    _check_device(op, x, weight, bias)
     lora = _lora_args(op, lora_down, lora_up, lora_scale, n, k)
     if weight.dtype != torch.uint8:
         raise NoCapableBackendError(op, {"hip": "weight must be the uint8 block bytes"})
