@@ -614,6 +614,22 @@ def profile_pass(which, reps=3, n=4096, k=4096, ms=(1, 8, 64)):
     64 MiB out as the byte-counter reference."""
     import torch
     import qlin
+    if which == "residual":
+        # the residual keyword on large-M calls: INT8-ConvRot M4608 K=N=3072 G=128 (a DiT output
+        # projection with its residual stream) and W6A8 M1024 K5120 N13824 group 64
+        q, s = int8_weight(3072, 3072, 128, seed=20)
+        x = gpu_activations(4608, 3072, 40)
+        r = gpu_activations(4608, 3072, 41)
+        for qd, sd in permuted_copies((q, s), 3072, reps, seed=30):
+            qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=128, residual=r)
+        qa, sr, sc = a8_weight(13824, 5120, 6, 64, seed=11)
+        xa = gpu_activations(1024, 5120, 13)
+        ra = gpu_activations(1024, 13824, 14)
+        for qd, srd, scd in permuted_copies((qa, sr, sc), 13824, reps, seed=12):
+            qlin.w4a8_int8_linear(xa, qd, srd, scd, None, None, None, 64, 256, residual=ra)
+        torch.cuda.synchronize()
+        log("[profile] done")
+        return
     if which == "gguf":
         weights = {t: make_gguf_weights(t, n, k, reps * len(ms), seed=i) for i, t in enumerate(GGUF_SUITE)}
         g = torch.Generator().manual_seed(1)
@@ -728,7 +744,8 @@ def floors_suite(steps, warmup):
 
 
 def other_suites(which, steps, warmup):
-    """LoRA beside the quantized linears and the frozen-weight input gradient (stderr JSON lines)."""
+    """LoRA beside the quantized linears, the residual epilogue and the frozen-weight input gradient
+    (stderr JSON lines)."""
     import torch
     import qlin
     from qlin.quantize import quantize_int8_convrot_weight, quantize_w4a8_int8_weight
@@ -778,6 +795,32 @@ def other_suites(which, steps, warmup):
                 y.addmm_(torch.nn.functional.linear(x, down), up.t(), alpha=0.8)
             timed(f"lora unfused {fmt} r{r} (bf16 addmm beside the call)", unfused, fl + flr,
                   n * k + m * k * 2 + m * n * 4, peak, unit)
+    if which in ("residual", "all"):
+        # the residual keyword at large M: y = residual + residual_scale * (x W^T + b) applied in the
+        # GEMM epilogue, beside the plain call and the two-kernel route (the linear in fp32, then the
+        # residual epilogue kernel) that the fused epilogue replaces
+        from qlin import _lib
+        q, s = int8_weight(3072, 3072, 128, seed=20)
+        qd, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+        x = gpu_activations(4608, 3072, 40)
+        r = gpu_activations(4608, 3072, 41)
+        rs = torch.full((3072,), 0.5, device="cuda").half()
+        m, n, k = 4608, 3072, 3072
+        fl = 2 * m * n * k
+        plain = lambda: qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=128)
+        timed(f"residual base int8_convrot M{m} K{k} N{n}", plain, fl, n * k + m * k * 2 + m * n * 2,
+              FP16_PEAK_TFLOPS, "TFLOPs")
+        timed("residual fused int8_convrot", lambda: qlin.int8_linear(x, qd, sd, convrot=True, convrot_groupsize=128,
+                                                                    residual=r, residual_scale=rs),
+              fl, n * k + m * k * 2 + m * n * 4, FP16_PEAK_TFLOPS, "TFLOPs")
+
+        def two_kernels():
+            base = qlin.int8_linear(x, qd, sd, None, torch.float32, convrot=True, convrot_groupsize=128)
+            y = torch.empty(m, n, dtype=torch.float16, device="cuda")
+            _lib.load().qlin_residual_epilogue(_lib.desc(base), _lib.desc(r), _lib.desc(rs), _lib.desc(y),
+                                               _lib.stream_of(y.device))
+        timed("residual two-kernel int8_convrot (fp32 linear, then the residual kernel)", two_kernels, fl,
+              n * k + m * k * 2 + m * n * 4, FP16_PEAK_TFLOPS, "TFLOPs")
     if which in ("grad", "all"):
         # frozen-weight input gradient at the reference's training shapes: 1056 tokens, Krea 2
         # layers attn.wq 6144->6144, attn.wk 6144->1536, mlp.up 6144->16384, mlp.down 16384->6144;
@@ -806,13 +849,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--suite", default="main", choices=["main", "lora", "grad", "floors", "all"],
-                    help="main: the JSON line (GGUF headline + configs); lora / grad / floors: extra suites on "
-                         "stderr (floors: MFMA issue rates, HBM read / copy floors, empty launch)")
+    ap.add_argument("--suite", default="main", choices=["main", "lora", "grad", "residual", "floors", "all"],
+                    help="main: the JSON line (GGUF headline + configs); lora / grad / residual / floors: extra "
+                         "suites on stderr (floors: MFMA issue rates, HBM read / copy floors, empty launch)")
     ap.add_argument("--configs", default="all",
                     help="comma-separated names from CONFIGS for the `configs` object, 'all' or 'none'")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--profile", default=None, choices=["gguf", *CONFIGS],
+    ap.add_argument("--profile", default=None, choices=["gguf", "residual", *CONFIGS],
                     help="eager launches of one workload for rocprofv3 kernel-trace / counter runs (no timing, "
                          "no JSON): each call three times on distinct weights, then a 64 MiB elementwise pass as "
                          "the byte-counter reference")

@@ -63,6 +63,9 @@ typedef enum {
     QLIN_OP_W4A8_GRAD_INPUT = 5,  /* qlin_w4a8_linear_grad_input (holds the decoded int8 grid, N*K bytes) */
     QLIN_OP_INT8_LINEAR_LORA = 6, /* qlin_int8_linear_lora: param = the LoRA rank R */
     QLIN_OP_W4A8_LINEAR_LORA = 7, /* qlin_w4a8_linear_lora: param = the LoRA rank R | group_size << 16 */
+    QLIN_OP_INT8_LINEAR_RESIDUAL = 8,  /* qlin_int8_linear_residual: param as QLIN_OP_INT8_LINEAR */
+    QLIN_OP_W4A8_LINEAR_RESIDUAL = 9,  /* qlin_w4a8_linear_residual: param as QLIN_OP_W4A8_LINEAR */
+    QLIN_OP_GGUF_LINEAR_RESIDUAL = 10, /* qlin_gguf_linear_residual: param = the ggml type */
 } qlin_op;
 
 /* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
@@ -200,6 +203,32 @@ qlin_status qlin_lora_apply_base(const qlin_tensor* x, const qlin_tensor* lora_d
  * adds "bias and residual in eager's order" (docs/upstream/comfy-kitchen-mps-backend.md:52). */
 qlin_status qlin_residual_epilogue(const qlin_tensor* base, const qlin_tensor* residual,
                                    const qlin_tensor* residual_scale, qlin_tensor* y, void* stream);
+
+/* The three linears with a residual in their epilogue: y[m,n] = dtype(residual[m,n] +
+ * residual_scale[n] * (linear + bias)[m,n]), each output rounded once -- the arithmetic of
+ * qlin_residual_epilogue over the linear's f32 output, to the bit.  The large-M kernels (the INT8
+ * GEMMs above 16 rows with 16-byte aligned operands; the A8 decode-once and 256 x 256 fused-decode
+ * GEMMs; the GGUF GEMM over the decoded weight above 64 rows) apply it in their epilogue with no
+ * f32 [M,N] buffer and no second launch; other calls write the linear in f32 to the end of the
+ * workspace and run the residual epilogue after it.  residual: f32/f16/bf16 [M,N] with a unit
+ * column stride; residual_scale: optional (NULL = 1) f32/f16/bf16 [N].  Workspace:
+ * qlin_workspace_size(QLIN_OP_*_LINEAR_RESIDUAL, M, N, K, param, x_dtype).  The residual keyword has
+ * no LoRA form here: with LoRA factors, run qlin_*_linear into an f32 base, qlin_lora_apply_base and
+ * qlin_residual_epilogue.
+ * Replace the residual / residual_scale of the reference's fused epilogue (see qlin_residual_epilogue). */
+qlin_status qlin_int8_linear_residual(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                      const qlin_tensor* bias, const qlin_tensor* residual,
+                                      const qlin_tensor* residual_scale, qlin_tensor* y, int convrot_groupsize,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+qlin_status qlin_w4a8_linear_residual(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                      const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                                      const qlin_tensor* residual, const qlin_tensor* residual_scale, qlin_tensor* y,
+                                      int bits, int group_size, int convrot_groupsize, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+qlin_status qlin_gguf_linear_residual(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                                      const qlin_tensor* bias, const qlin_tensor* residual,
+                                      const qlin_tensor* residual_scale, qlin_tensor* y, void* workspace,
+                                      size_t workspace_bytes, void* stream);
 
 /* Input gradient of the frozen INT8 linear: dx [M,K] = dy [M,N] @ W with W = rotate(q * scale) the
  * weight in the original basis (convrot_groupsize 0 = no rotation), i.e. dx = ((dy * scale) @ q) H.

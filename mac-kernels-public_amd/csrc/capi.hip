@@ -125,6 +125,11 @@ qlin_status check_xy(const qlin_tensor* x, qlin_tensor* y, int64_t N, int64_t K,
     return QLIN_OK;
 }
 
+// Internal status of an impl asked for a residual its kernel does not apply (nothing launched); never
+// returned through the C ABI (the public codes are 0 .. 4).
+constexpr qlin_status QLIN_NOT_FUSED = (qlin_status)7;
+static_assert(QLIN_NOT_FUSED != QLIN_OK && QLIN_NOT_FUSED > QLIN_EWORKSPACE, "internal status");
+
 // Workspace carve-out (256-byte aligned pieces).
 struct Carver {
     uint8_t* base;
@@ -329,6 +334,13 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_INT8_LINEAR_LORA: return ws_int8(M, K) + ws_lora(M, K, param);
         case QLIN_OP_W4A8_LINEAR_LORA:  // param: R | group_size << 16
             return ws_w4a8(M, N, K, param >> 16) + ws_lora(M, K, param & 0xFFFF);
+        // the residual variants: the linear's workspace, then room for its fp32 output when the
+        // call's kernel does not apply the residual itself
+        case QLIN_OP_INT8_LINEAR_RESIDUAL: return ws_int8(M, K) + align_up((size_t)(M * N * 4)) + 256;
+        case QLIN_OP_W4A8_LINEAR_RESIDUAL:
+            return ws_w4a8(M, N, K, param >> 8) + align_up((size_t)(M * N * 4)) + 256;
+        case QLIN_OP_GGUF_LINEAR_RESIDUAL:
+            return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K) + align_up((size_t)(M * N * 4)) + 256;
         case QLIN_OP_LORA: {  // the split partials, then their sum
             const int S = lora_splits(M, K, param);
             return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(param > 0 ? param : 0) * 4);
@@ -546,9 +558,12 @@ qlin_status qlin_residual_epilogue(const qlin_tensor* base, const qlin_tensor* r
 
 // The INT8 weight-only linear; with L, the LoRA term joins the epilogue of the large-M DMA GEMM
 // (QLIN_EUNSUPPORTED, before anything is launched, when another kernel would take the call).
+// R: a residual the GEMM epilogue applies; when the call would take another kernel the impl returns
+// QLIN_NOT_FUSED before launching anything (linear_with_residual then adds it in a second kernel).
 static qlin_status int8_linear_impl(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
                                     const qlin_tensor* bias, qlin_tensor* y, int convrot_groupsize, const LoraIn* L,
-                                    void* workspace, size_t workspace_bytes, void* stream) {
+                                    void* workspace, size_t workspace_bytes, void* stream,
+                                    const ResidualTile* R = nullptr) {
     Mat Q, X, Y;
     qlin_status s = as_matrix(qdata, "qdata", Q);
     if (s) return s;
@@ -572,6 +587,16 @@ static qlin_status int8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
+    if (R) {
+        // only the large-M GEMM applies a residual: its operands as run_gemm_f16 will see them
+        if (L || M <= INT8_SMALLM_MAX_M) return QLIN_NOT_FUSED;
+        GemmF16Args p;
+        p.wkind = WO_INT8;
+        p.K = K; p.w = Q.data; p.ldw = Q.ld;
+        const bool direct = convrot_groupsize == 0 && X.dtype == QLIN_DT_F16 && X.ld % 8 == 0 && (uintptr_t)X.data % 16 == 0;
+        p.x = direct ? (const f16*)X.data : (const f16*)ws.base; p.ldx = direct ? X.ld : K;
+        if (!gemm_f16_fuses_residual(p)) return QLIN_NOT_FUSED;
+    }
     if (L) {
         // the GEMM's operands are known before anything is launched: the activations are x itself
         // or the prologue's rows at the start of the workspace, t follows
@@ -638,7 +663,61 @@ static qlin_status int8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     a.scale = scale->data; a.scale_dtype = scale->dtype; a.scale_stride = sst;
     a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
     a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+    if (R) a.res = *R;
     return hip_status(run_gemm_f16(a, st), "int8 gemm");
+}
+
+// y = dtype(residual + residual_scale * linear): `run(yo, R, ws, bytes)` runs the linear into yo,
+// applying R in its GEMM epilogue; when it returns QLIN_NOT_FUSED (another kernel takes the call,
+// nothing launched), the linear goes to an fp32 [M, N] buffer at the end of the workspace and the
+// residual kernel adds it with the same fma and rounding.
+extern "C++" template <class Run>
+static qlin_status linear_with_residual(const qlin_tensor* y, const qlin_tensor* residual,
+                                        const qlin_tensor* residual_scale, void* workspace, size_t workspace_bytes,
+                                        void* stream, Run run) {
+    Mat Y, Rm;
+    qlin_status s;
+    if ((s = as_matrix(y, "y", Y)) || (s = as_matrix(residual, "residual", Rm))) return s;
+    if (!is_float(Rm.dtype)) return fail(QLIN_EUNSUPPORTED, "residual must be f32/f16/bf16");
+    if (Rm.rows != Y.rows || Rm.cols != Y.cols)
+        return fail(QLIN_EINVAL, "residual must be [%lld, %lld]", (long long)Y.rows, (long long)Y.cols);
+    ResidualTile R;
+    R.r = Rm.data; R.r_dt = Rm.dtype; R.ldr = Rm.ld;
+    if (residual_scale && residual_scale->data) {
+        int64_t rst;
+        if ((s = as_vector(residual_scale, "residual_scale", Y.cols, false, rst))) return s;
+        if (!is_float(residual_scale->dtype)) return fail(QLIN_EUNSUPPORTED, "residual_scale must be f32/f16/bf16");
+        R.rs = residual_scale->data;
+        R.rs_dt = residual_scale->dtype;
+    }
+    const size_t bb = align_up((size_t)(Y.rows * Y.cols * 4));
+    if (workspace_bytes < bb + 256) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, bb + 256);
+    if ((s = run(const_cast<qlin_tensor*>(y), &R, workspace, workspace_bytes - bb - 256)) != QLIN_NOT_FUSED) return s;
+    uintptr_t b = (uintptr_t)workspace + workspace_bytes - bb;
+    b &= ~(uintptr_t)255;
+    qlin_tensor yb{};
+    yb.data = (void*)b; yb.dtype = QLIN_DT_F32; yb.ndim = 2;
+    yb.shape[0] = Y.rows; yb.shape[1] = Y.cols; yb.stride[0] = Y.cols; yb.stride[1] = 1;
+    if ((s = run(&yb, nullptr, workspace, b - (uintptr_t)workspace))) return s;
+    if (Y.rows == 0 || Y.cols == 0) return QLIN_OK;
+    ResidualArgs a;
+    a.base = (const float*)yb.data; a.ldb = Y.cols;
+    a.res = Rm.data; a.res_dt = Rm.dtype; a.ldr = Rm.ld;
+    a.rscale = R.rs; a.rscale_dt = R.rs_dt;
+    a.y = Y.data; a.y_dt = Y.dtype; a.ldy = Y.ld;
+    a.M = Y.rows; a.N = Y.cols;
+    return hip_status(run_residual(a, (hipStream_t)stream), "residual epilogue");
+}
+
+qlin_status qlin_int8_linear_residual(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
+                                      const qlin_tensor* bias, const qlin_tensor* residual,
+                                      const qlin_tensor* residual_scale, qlin_tensor* y, int convrot_groupsize,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    return linear_with_residual(y, residual, residual_scale, workspace, workspace_bytes, stream,
+                                [&](qlin_tensor* yo, const ResidualTile* R, void* w, size_t wb) {
+                                    return int8_linear_impl(x, qdata, scale, bias, yo, convrot_groupsize, nullptr, w, wb,
+                                                            stream, R);
+                                });
 }
 
 qlin_status qlin_int8_linear(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* scale,
@@ -658,7 +737,7 @@ qlin_status qlin_int8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata
 // The GGUF linear over a given workspace (the caller's, or the no-allocation entry point's scratch).
 static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
                                     const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
-                                    void* stream) {
+                                    void* stream, const ResidualTile* R = nullptr) {
     int qk, ts;
     if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
     if (!weight) return fail(QLIN_EINVAL, "weight is missing");
@@ -678,6 +757,11 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
     const bool aligned = ((uintptr_t)weight % 4) == 0;
+    // a residual rides in the epilogue of the GEMM over the decoded fp16 weight (above 64 rows, with
+    // room for the decoded rows); every other kernel returns QLIN_NOT_FUSED before any launch
+    if (R && (M <= GGUF_SMALLM_MAX_M || K % 64 || (uintptr_t)workspace % 16 ||
+              gguf_decode_rows(N, K, (int64_t)workspace_bytes - (int64_t)ws_gguf(M, N, K, ggml_type)) <= 0))
+        return QLIN_NOT_FUSED;
     if (M == 1 && aligned) {
         const f16* xo;
         int64_t ldx;
@@ -741,6 +825,11 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
             a.wexp = wexp + n0;
             a.bias = bias ? (const uint8_t*)bias->data + n0 * bsz : nullptr;
             a.y = (uint8_t*)Y.data + n0 * ysz;
+            if (R) {
+                a.res = *R;
+                a.res.r = (const uint8_t*)R->r + n0 * (R->r_dt == QLIN_DT_F32 ? 4 : 2);
+                if (R->rs) a.res.rs = (const uint8_t*)R->rs + n0 * (R->rs_dt == QLIN_DT_F32 ? 4 : 2);
+            }
             if ((s = hip_status(run_gemm_f16(a, st), "gguf gemm"))) return s;
         }
         return QLIN_OK;
@@ -759,6 +848,16 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
                              const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
                              void* stream) {
     return gguf_linear_impl(x, weight, ggml_type, N, K, bias, y, workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_gguf_linear_residual(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                                      const qlin_tensor* bias, const qlin_tensor* residual,
+                                      const qlin_tensor* residual_scale, qlin_tensor* y, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    return linear_with_residual(y, residual, residual_scale, workspace, workspace_bytes, stream,
+                                [&](qlin_tensor* yo, const ResidualTile* R, void* w, size_t wb) {
+                                    return gguf_linear_impl(x, weight, ggml_type, N, K, bias, yo, w, wb, stream, R);
+                                });
 }
 
 qlin_status qlin_gguf_linear_noalloc(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
@@ -785,7 +884,8 @@ qlin_status qlin_gguf_linear_noalloc(const qlin_tensor* x, const void* weight, i
 static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
                                     const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
                                     qlin_tensor* y, int bits, int group_size, int convrot_groupsize, const LoraIn* L,
-                                    void* workspace, size_t workspace_bytes, void* stream) {
+                                    void* workspace, size_t workspace_bytes, void* stream,
+                                    const ResidualTile* R = nullptr) {
     if (bits != 4 && bits != 6) return fail(QLIN_EUNSUPPORTED, "bits=%d unsupported (4 or 6)", bits);
     Mat Q, X, Y, SR;
     qlin_status s = as_matrix(qdata, "qdata", Q);
@@ -841,6 +941,10 @@ static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     g.bias = bias ? bias->data : nullptr; g.bias_dtype = bdt;
     g.y = Y.data; g.y_dtype = Y.dtype; g.ldy = Y.ld;
     if (a8_grid_in_workspace(M, N, K, group_size)) g.w8 = (int8_t*)ws.take((size_t)(N * K));
+    if (R) {  // only the large-tile GEMMs apply a residual in their epilogue
+        if (L || !gemm_i8_fuses_residual(g)) return QLIN_NOT_FUSED;
+        g.res = *R;
+    }
     float* t = nullptr;
     if (L) {
         t = (float*)ws.take(ws_lora(M, K, D.rows));
@@ -875,6 +979,18 @@ qlin_status qlin_w4a8_linear(const qlin_tensor* x, const qlin_tensor* qdata, con
                              size_t workspace_bytes, void* stream) {
     return w4a8_linear_impl(x, qdata, s_rel, s_channel, codebook, bias, y, bits, group_size, convrot_groupsize, nullptr,
                             workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_w4a8_linear_residual(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,
+                                      const qlin_tensor* s_channel, const qlin_tensor* codebook, const qlin_tensor* bias,
+                                      const qlin_tensor* residual, const qlin_tensor* residual_scale, qlin_tensor* y,
+                                      int bits, int group_size, int convrot_groupsize, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    return linear_with_residual(y, residual, residual_scale, workspace, workspace_bytes, stream,
+                                [&](qlin_tensor* yo, const ResidualTile* R, void* w, size_t wb) {
+                                    return w4a8_linear_impl(x, qdata, s_rel, s_channel, codebook, bias, yo, bits,
+                                                            group_size, convrot_groupsize, nullptr, w, wb, stream, R);
+                                });
 }
 
 qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata, const qlin_tensor* s_rel,

@@ -478,19 +478,21 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
     const int64_t nc = n0 + 8 * cc;
     const int ncount = (int)max<int64_t>(0, min<int64_t>(8, a.N - nc));
     const int xer = a.xexp ? a.xexp[min(m0 + min(tid, BMT - 1), (int64_t)a.M - 1)] : 0;
-    uint32_t csb[8], bvb[8];
+    uint32_t csb[8], bvb[8], rsb[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int64_t n = min(nc + e, a.N - 1);
         csb[e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
         bvb[e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
     }
-    float cs[8], bv[8];
+    residual_scale_bits8(a.res, nc, a.N, rsb);
+    float cs[8], bv[8], rsv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         cs[e] = bits_to_f32_rt(csb[e], a.scale_dtype);
         bv[e] = a.bias ? bits_to_f32_rt(bvb[e], a.bias_dtype) : 0.0f;
     }
+    residual_scales8(a.res, rsb, rsv);
     const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
@@ -520,9 +522,13 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[q][e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
         }
+        int64_t mq[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) mq[q] = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+        if (a.res.r) residual_apply8<Q>(a.res, mq, nc, a.M, a.N, rsv, v);
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int64_t m = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+            const int64_t m = mq[q];
             if (m < a.M && ncount > 0) store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v[q], ncount, vec);
         }
     }
@@ -676,6 +682,8 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
             bvb[e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
         }
     }
+    uint32_t rsb[8];
+    residual_scale_bits8(a.res, nc, a.N, rsb);
     const bool vec = (a.ldy % 8 == 0) && ((uintptr_t)a.y % 16 == 0);
     if constexpr (LDU >= 0) {
         constexpr int RC = lora_max_rank<LDU, BMT, BNT>((int)sizeof(smem) - BMT * 4);
@@ -702,7 +710,8 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
         }
         lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(a.lora, smem, m0, n0, a.M, a.N, wm * WM, wn * WN, tid, lane, acc);
     }
-    float cs[CB8], bv[CB8];
+    float cs[CB8], bv[CB8], rsv[8];
+    residual_scales8(a.res, rsb, rsv);
     if constexpr (LDU < 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -742,9 +751,13 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
                 for (int e = 0; e < 8; ++e) v[q][e] = __builtin_ldexpf(e < 4 ? v0[e] : v1[e - 4], e2) * cs[e] + bv[e];
             }
         }
+        int64_t mq[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) mq[q] = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+        if (a.res.r) residual_apply8<Q>(a.res, mq, nc, a.M, a.N, rsv, v);
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int64_t m = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+            const int64_t m = mq[q];
             if (m < a.M && ncount > 0) store8_rt(a.y, a.y_dtype, m * a.ldy + nc, v[q], ncount, vec);
         }
     }
@@ -936,7 +949,7 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
     float* ot = reinterpret_cast<float*>(smem);
     float* op = ot + 4 * h * ORW + 32 * tn + r32;
     int xeq[Q];
-    uint32_t csb[Q][8], bvb[Q][8];
+    uint32_t csb[Q][8], bvb[Q][8], rsb[Q][8];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
         const int c = min(tid + NT * q, BMT * CPR - 1), row = c / CPR, cq = c % CPR;
@@ -948,6 +961,7 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
             else csb[q][e] = load_bits_rt(a.scale, a.scale_dtype, n * a.scale_stride);
             bvb[q][e] = a.bias ? load_bits_rt(a.bias, a.bias_dtype, n) : 0u;
         }
+        residual_scale_bits8(a.res, n0 + 8 * cq, a.N, rsb[q]);
     }
 #pragma unroll
     for (int part = 0; part < KH; ++part) {
@@ -977,6 +991,18 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
                 v[q][e] = __builtin_ldexpf(ot[row * ORW + 8 * cq + e], xeq[q]) * cs + bv;
             }
         }
+    }
+    if (a.res.r) {
+        int64_t mq[Q], ncq[Q];
+        float rsq[Q][8];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int c = min(tid + NT * q, BMT * CPR - 1);
+            mq[q] = m0 + c / CPR;
+            ncq[q] = n0 + 8 * (c % CPR);
+            residual_scales8(a.res, rsb[q], rsq[q]);
+        }
+        residual_apply8<Q>(a.res, mq, ncq, a.M, a.N, rsq, v);
     }
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
@@ -1080,6 +1106,7 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
 #undef QLIN_WOS16
         }
     }
+    if (a.res.r) return hipErrorInvalidValue;  // the caller checks gemm_f16_fuses_residual first
     dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM)), block(256);
     hipLaunchKernelGGL((gemm_f16_kernel<WK, GT>), grid, block, 0, st, a);
     return hipGetLastError();
@@ -1122,6 +1149,18 @@ bool gemm_f16_fuses_lora(const GemmF16Args& a) {
            (uintptr_t)L.t % 16 == 0 &&
            (uintptr_t)L.up % 16 == 0 && (L.ld_up * es) % 16 == 0 &&
            (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);
+}
+
+// launch1 ends in a kernel with the staged 8-output epilogue (which applies a.res) whenever the
+// operands allow its 16-byte loads: the INT8 DMA / register-staged kernels and the DMA-ring kernel
+// on decoded fp16 weights; the generic 128 x 128 kernel (GGUF tiles decoded as loaded, unaligned
+// operands) does not take a residual.
+bool gemm_f16_fuses_residual(const GemmF16Args& a) {
+    if (a.wkind == WO_INT8)
+        return a.K % WBK == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 16 == 0 && (uintptr_t)a.w % 16 == 0;
+    if (a.wkind == WO_F16)
+        return a.K % 64 == 0 && a.ldx % 8 == 0 && (uintptr_t)a.x % 16 == 0 && a.ldw % 8 == 0 && (uintptr_t)a.w % 16 == 0;
+    return false;
 }
 
 hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st) {

@@ -555,9 +555,12 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
         sc[e] = p.s_ch[n];
         bvb[e] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, n) : 0u;
     }
-    float bv[8];
+    uint32_t rsb[8];
+    residual_scale_bits8(p.res, nc, p.N, rsb);
+    float bv[8], rsv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) bv[e] = p.bias ? bits_to_f32_rt(bvb[e], p.bias_dtype) : 0.0f;
+    residual_scales8(p.res, rsb, rsv);
     const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
 #pragma unroll
     for (int pass = 0; pass < BMT / RP; ++pass) {
@@ -591,9 +594,13 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
                 }
             }
         }
+        int64_t mq[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) mq[q] = m0 + RP * pass + tid / CPR + (NT / CPR) * q;
+        if (p.res.r) residual_apply8<Q>(p.res, mq, nc, p.M, p.N, rsv, v);
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int64_t m = m0 + RP * pass + tid / CPR + (NT / CPR) * q;
+            const int64_t m = mq[q];
             if (m < p.M && ncount > 0) store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v[q], ncount, vec);
         }
     }
@@ -855,6 +862,8 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
             bvb[e] = p.bias ? load_bits_rt(p.bias, p.bias_dtype, n) : 0u;
         }
     }
+    uint32_t rsb[8];
+    residual_scale_bits8(p.res, nc, p.N, rsb);
     const bool vec = (p.ldy % 8 == 0) && ((uintptr_t)p.y % 16 == 0);
     if constexpr (LDU >= 0) {
         // the tile's activation scales at the end of LDS, past the LoRA chunks
@@ -887,7 +896,8 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
         }
         lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(p.lora, smem, m0, n0, p.M, p.N, wm * WM, wn * WN, tid, lane, acc);
     }
-    float bv[CB8];
+    float bv[CB8], rsv[8];
+    residual_scales8(p.res, rsb, rsv);
     if constexpr (LDU < 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) bv[e] = p.bias ? bits_to_f32_rt(bvb[e], p.bias_dtype) : 0.0f;
@@ -932,9 +942,13 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
                 }
             }
         }
+        int64_t mq[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) mq[q] = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+        if (p.res.r) residual_apply8<Q>(p.res, mq, nc, p.M, p.N, rsv, v);
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int64_t m = m0 + pass * RP + tid / CPR + (NT / CPR) * q;
+            const int64_t m = mq[q];
             if (m < p.M && ncount > 0) store8_rt(p.y, p.y_dtype, m * p.ldy + nc, v[q], ncount, vec);
         }
     }
@@ -1075,6 +1089,7 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
     if (p.lora.t && !gemm_i8_fuses_lora(p)) return hipErrorInvalidValue;  // only the DMA GEMM adds LoRA
     if (a8_smallm_ok(p)) {
+        if (p.res.r) return hipErrorInvalidValue;  // the caller checks gemm_i8_fuses_residual first
         const dim3 grid((unsigned)((p.N + 15) / 16)), block(512);
         if (p.M <= 16) hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 1>), grid, block, 0, st, p);
         else hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 2>), grid, block, 0, st, p);
@@ -1123,6 +1138,7 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
             hipLaunchKernelGGL((gemm_a8_kernel<BITS, CB, TSrel, false>), grid, block, 0, st, p);
         return hipGetLastError();
     }
+    if (p.res.r) return hipErrorInvalidValue;  // the caller checks gemm_i8_fuses_residual first
     dim3 grid((unsigned)((p.N + BN - 1) / BN), (unsigned)((p.M + BM - 1) / BM)), block(256);
     hipLaunchKernelGGL((gemm_i8_kernel<BITS, CB, TSrel>), grid, block, 0, st, p);
     return hipGetLastError();
@@ -1166,6 +1182,17 @@ bool gemm_i8_fuses_lora(const GemmI8Args& p) {
     return dma && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= i8dma_lora_rank(L.up_dt) &&
            (uintptr_t)L.t % 16 == 0 && (uintptr_t)L.up % 16 == 0 &&
            (L.ld_up * es) % 16 == 0 && (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);
+}
+
+// The large-tile kernels launch_o takes (the decode-once DMA GEMM, the fused-decode 256 x 256
+// GEMM) apply p.res in their staged epilogue; the small-M and 128 x 128 kernels do not.
+bool gemm_i8_fuses_residual(const GemmI8Args& p) {
+    if (a8_smallm_ok(p)) return false;
+    if (p.w8 && a8_decode_once(p.M, p.N, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
+        (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0)
+        return true;
+    const int64_t big_tiles = ((p.N + 255) / 256) * ((p.M + 255) / 256);
+    return p.group_size % 64 == 0 && p.K % BKA == 0 && p.ldq % 16 == 0 && big_tiles >= 192;
 }
 
 bool a8_grid_supported(const GemmI8Args& p) {

@@ -138,6 +138,81 @@ struct LoraTile {
     float scale = 1.0f;
 };
 
+// Residual operand of a GEMM epilogue: y = dtype(r[m, n] + rs[n] * base[m, n]) with base the
+// epilogue's fp32 value (bias and any LoRA term added), one fma and one rounding -- the arithmetic
+// of the separate residual kernel (run_residual), so both give the same bits.  r == nullptr: none.
+struct ResidualTile {
+    const void* r = nullptr;     // [M, N], row stride ldr (elements)
+    int r_dt = DT_F16;
+    int64_t ldr = 0;
+    const void* rs = nullptr;    // [N], or nullptr for 1
+    int rs_dt = DT_F16;
+};
+
+// Residual scales of the 8 columns nc .. nc + 7 (1 where rs is absent), as raw bits to convert at use.
+__device__ __forceinline__ void residual_scale_bits8(const ResidualTile& R, int64_t nc, int64_t N, uint32_t (&b)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[e] = (R.r && R.rs) ? load_bits_rt(R.rs, R.rs_dt, min<int64_t>(nc + e, N - 1)) : 0u;
+}
+__device__ __forceinline__ void residual_scales8(const ResidualTile& R, const uint32_t (&b)[8], float (&s)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = R.rs ? bits_to_f32_rt(b[e], R.rs_dt) : 1.0f;
+}
+// v[q][e] = fma(rs[q][e], v[q][e], r[m[q], nc[q] + e]) for Q staged pieces of 8 outputs: every
+// residual value is requested before the first one is used (the caller's stores follow).  Rows
+// past M and columns past N read the last valid ones (their outputs are not stored).
+template <int Q>
+__device__ __forceinline__ void residual_apply8(const ResidualTile& R, const int64_t (&m)[Q], const int64_t (&nc)[Q],
+                                                int64_t M, int64_t N, const float (&rsv)[Q][8], float (&v)[Q][8]) {
+    uint32_t raw[Q][8];
+    const bool f32 = R.r_dt == DT_F32;
+    const bool aligned = R.ldr % 8 == 0 && (uintptr_t)R.r % 16 == 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int64_t row = min<int64_t>(m[q], M - 1) * R.ldr;
+        if (aligned && nc[q] + 8 <= N) {
+            if (f32) {
+                const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(R.r) + row + nc[q]);
+                const u32x4 a = p[0], b = p[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    raw[q][e] = a[e];
+                    raw[q][e + 4] = b[e];
+                }
+            } else {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(R.r) + row + nc[q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    raw[q][2 * e] = a[e] & 0xFFFFu;
+                    raw[q][2 * e + 1] = a[e] >> 16;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                raw[q][e] = load_bits_rt(R.r, R.r_dt, row + min<int64_t>(min<int64_t>(nc[q], N - 1) + e, N - 1));
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[q][e] = __builtin_fmaf(rsv[q][e], v[q][e], bits_to_f32_rt(raw[q][e], R.r_dt));
+}
+// The same for Q rows that share the columns nc .. nc + 7 and their scales.
+template <int Q>
+__device__ __forceinline__ void residual_apply8(const ResidualTile& R, const int64_t (&m)[Q], int64_t nc, int64_t M,
+                                                int64_t N, const float (&rs)[8], float (&v)[Q][8]) {
+    int64_t ncq[Q];
+    float rsq[Q][8];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        ncq[q] = nc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rsq[q][e] = rs[e];
+    }
+    residual_apply8<Q>(R, m, ncq, M, N, rsq, v);
+}
+
 struct GemmF16Args {
     int wkind = WO_INT8;
     int gguf_type = 0;
@@ -157,6 +232,7 @@ struct GemmF16Args {
     int y_dtype = DT_F16;
     int64_t ldy = 0;
     LoraTile lora;                   // INT8, 256 x 256 DMA tiles only (gemm_f16_fuses_lora)
+    ResidualTile res;                // the staged-epilogue kernels only (gemm_f16_fuses_residual)
 };
 hipError_t run_gemm_f16(const GemmF16Args& a, hipStream_t st);
 // The GGUF weight's row exponents e[n] (as run_gguf_row_exp) and the weight decoded once as
@@ -166,6 +242,8 @@ hipError_t run_gguf_decode_f16(int type, const uint8_t* w, int64_t row_bytes, in
                                f16* out, hipStream_t st);
 // Whether run_gemm_f16 takes a kernel that adds a.lora in its epilogue for these operands.
 bool gemm_f16_fuses_lora(const GemmF16Args& a);
+// Whether run_gemm_f16 takes a kernel that applies a.res in its epilogue for these operands.
+bool gemm_f16_fuses_residual(const GemmF16Args& a);
 
 // GGUF per-row weight exponent: e[n] = exponent bounding max |w[n, :]| (gemm_f16.hip).
 hipError_t run_gguf_row_exp(int type, const uint8_t* w, int64_t N, int64_t K, int32_t* e, hipStream_t st);
@@ -192,9 +270,12 @@ struct GemmI8Args {
     int64_t ldy = 0;
     int8_t* w8 = nullptr;            // workspace for the decoded int8 grid [N, K] (decode-once path)
     LoraTile lora;                   // decode-once DMA GEMM only (gemm_i8_fuses_lora)
+    ResidualTile res;                // the large-tile kernels only (gemm_i8_fuses_residual)
 };
 // Whether run_gemm_i8 takes a kernel that adds p.lora in its epilogue for these operands.
 bool gemm_i8_fuses_lora(const GemmI8Args& p);
+// Whether run_gemm_i8 takes a kernel that applies p.res in its epilogue for these operands.
+bool gemm_i8_fuses_residual(const GemmI8Args& p);
 // A8 calls that decode the weight grid once into the workspace (N * K bytes) and run the int8 DMA
 // GEMM on it: from 512 activation rows (two or more 256-row tiles would each decode the weight in
 // the fused-decode kernel: W6A8 K5120 M512 N27648 138 vs 167 us, M960 N13824 110 vs 160 us), and

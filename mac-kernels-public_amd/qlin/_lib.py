@@ -21,6 +21,7 @@ QLIN_OK, QLIN_EUNSUPPORTED, QLIN_EINVAL, QLIN_EHIP, QLIN_EWORKSPACE = 0, 1, 2, 3
 DT_F32, DT_F16, DT_BF16, DT_I8, DT_U8, DT_I32, DT_E4M3 = 0, 1, 2, 3, 4, 5, 6
 OP_INT8_LINEAR, OP_W4A8_LINEAR, OP_GGUF_LINEAR, OP_LORA, OP_INT8_GRAD_INPUT, OP_W4A8_GRAD_INPUT = 0, 1, 2, 3, 4, 5
 OP_INT8_LINEAR_LORA, OP_W4A8_LINEAR_LORA = 6, 7
+OP_INT8_LINEAR_RESIDUAL, OP_W4A8_LINEAR_RESIDUAL, OP_GGUF_LINEAR_RESIDUAL = 8, 9, 10
 
 _TORCH_DT = {
     torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.int8: DT_I8,
@@ -34,6 +35,7 @@ EXPORTS = (
     "qlin_dequantize_int8", "qlin_dequantize_w4a8", "qlin_quantize_act_int8", "qlin_lora_apply", "qlin_lora_apply_base",
     "qlin_residual_epilogue", "qlin_int8_linear_lora", "qlin_w4a8_linear_lora",
     "qlin_int8_linear_grad_input", "qlin_w4a8_linear_grad_input",
+    "qlin_int8_linear_residual", "qlin_w4a8_linear_residual", "qlin_gguf_linear_residual",
 )
 
 
@@ -72,6 +74,9 @@ def load():
         "qlin_int8_linear_lora": (I, [T, T, T, T, T, I, T, T, ctypes.c_float, P, SZ, P]),
         "qlin_w4a8_linear_lora": (I, [T, T, T, T, T, T, T, I, I, I, T, T, ctypes.c_float, P, SZ, P]),
         "qlin_gguf_linear": (I, [T, P, I, I64, I64, T, T, P, SZ, P]),
+        "qlin_int8_linear_residual": (I, [T, T, T, T, T, T, T, I, P, SZ, P]),
+        "qlin_w4a8_linear_residual": (I, [T, T, T, T, T, T, T, T, T, I, I, I, P, SZ, P]),
+        "qlin_gguf_linear_residual": (I, [T, P, I, I64, I64, T, T, T, T, P, SZ, P]),
         "qlin_gguf_linear_noalloc": (I, [T, P, I, I64, I64, T, T, P]),
         "qlin_dequantize_gguf": (I, [P, I, I64, I64, T, P]),
         "qlin_dequantize_int8": (I, [T, T, T, I, P]),

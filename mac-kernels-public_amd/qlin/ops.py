@@ -289,6 +289,14 @@ def int8_linear(x, qdata, scale, bias=None, out_dtype=None, *, convrot=False, co
                                            _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(), stream)
         if _fused_lora(op, lora, res, x2, run):
             return _shaped(y, shape)
+    if res is not None and lora is None:  # the residual joins the linear's epilogue (or its own kernel)
+        r, rs = res
+        _check_device(op, r, rs)
+        ws = _workspace(_lib.OP_INT8_LINEAR_RESIDUAL, m, n, k, g, x2, stream)
+        st = L.qlin_int8_linear_residual(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(r),
+                                         _lib.desc(rs), _lib.desc(y), g, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(st, op)
+        return _shaped(y, shape)
     ws = _workspace(_lib.OP_INT8_LINEAR, m, n, k, g, x2, stream)
     yb = _base_out(lora, y, res)
     st = L.qlin_int8_linear(_lib.desc(x2), _lib.desc(qdata), _lib.desc(s), _lib.desc(b), _lib.desc(yb), g,
@@ -381,6 +389,15 @@ def w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook=None, correction=None,
                                            _lib.desc(down), _lib.desc(up), lscale, wsl.data_ptr(), wsl.numel(), stream)
         if _fused_lora(op, lora, res, x2, run):
             return _shaped(y, shape)
+    if res is not None and lora is None:  # the residual joins the linear's epilogue (or its own kernel)
+        r, rs = res
+        _check_device(op, r, rs)
+        ws = _workspace(_lib.OP_W4A8_LINEAR_RESIDUAL, m, n, k, bits | int(group_size) << 8, x2, stream)
+        st = L.qlin_w4a8_linear_residual(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
+                                         _lib.desc(b), _lib.desc(r), _lib.desc(rs), _lib.desc(y), bits, int(group_size),
+                                         int(convrot_groupsize or 0), ws.data_ptr(), ws.numel(), stream)
+        _lib.check(st, op)
+        return _shaped(y, shape)
     ws = _workspace(_lib.OP_W4A8_LINEAR, m, n, k, bits | int(group_size) << 8, x2, stream)
     yb = _base_out(lora, y, res)
     st = L.qlin_w4a8_linear(_lib.desc(x2), _lib.desc(q), _srel_desc(s_rel), _lib.desc(sch), _lib.desc(cb),
@@ -484,6 +501,14 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
         return _shaped(y, oshape)
     b = _bias(bias, n)
     stream = _lib.stream_of(x.device)
+    if res is not None and lora is None:  # the residual joins the linear's epilogue (or its own kernel)
+        r, rs = res
+        _check_device(op, r, rs)
+        ws = _workspace(_lib.OP_GGUF_LINEAR_RESIDUAL, x2.shape[0], n, k, tid, x2, stream)
+        st = _lib.load().qlin_gguf_linear_residual(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(r),
+                                                   _lib.desc(rs), _lib.desc(y), ws.data_ptr(), ws.numel(), stream)
+        _lib.check(st, op)
+        return _shaped(y, oshape)
     ws = _workspace(_lib.OP_GGUF_LINEAR, x2.shape[0], n, k, tid, x2, stream)
     yb = _base_out(lora, y, res)
     st = _lib.load().qlin_gguf_linear(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b), _lib.desc(yb),

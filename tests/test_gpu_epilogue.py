@@ -135,3 +135,76 @@ def test_carriers_dispatch_to_the_ops(case):
                                                        convrot_groupsize=256, orig_dtype=torch.float32))
         assert torch.equal(wa.dequantize(), Q.dequantize_w4a8_int8_weight(qa, sr, sc, cb, None, 16, 256))
         assert torch.equal(linear(x, wa), Q.w4a8_int8_linear(x, qa, sr, sc, cb, None, None, 16, 256))
+
+
+def _separate(Q, linear, res, rs, odt):
+    """The linear in fp32, then the residual epilogue kernel: the reference bits for the fused call."""
+    from qlin import _lib
+    base = linear(torch.float32)
+    y = torch.empty(base.shape, dtype=odt, device=DEV)
+    st = _lib.load().qlin_residual_epilogue(_lib.desc(base), _lib.desc(res), _lib.desc(rs), _lib.desc(y),
+                                            _lib.stream_of(base.device))
+    _lib.check(st, "qlin_residual_epilogue")
+    return y
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (2048, 5120, 1024),   # 160 tiles of 256 x 256: the LDS-DMA GEMM
+    (1000, 2560, 1024),   # register-staged 128 x 128 tiles, a ragged M
+    (100, 512, 1024),     # the DMA-ring kernel (a few hundred rows)
+    (5, 512, 1024),       # small M: the linear in fp32, then the residual kernel
+])
+@pytest.mark.parametrize("odt,rdt", [(torch.float16, torch.float16), (torch.bfloat16, torch.float32)])
+def test_int8_residual_fused_equals_separate(m, n, k, odt, rdt):
+    """The residual applied in the GEMM epilogue gives the bits of the fp32 linear followed by the
+    residual kernel (the same fma and rounding); small M takes that second route itself."""
+    Q = qlin()
+    g = torch.Generator().manual_seed(m + n)
+    q = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(DEV)
+    s = (torch.rand(n, generator=g) * 1e-3).to(DEV)
+    x = torch.randn(m, k, generator=g).half().to(DEV)
+    b = torch.randn(n, generator=g).half().to(DEV)
+    res = (torch.randn(m, n, generator=g) * 3).to(rdt).to(DEV)
+    rs = torch.linspace(-2, 2, n).to(rdt).to(DEV)
+    y = Q.int8_linear(x, q, s, b, odt, convrot=True, convrot_groupsize=128, residual=res, residual_scale=rs)
+    want = _separate(Q, lambda dt: Q.int8_linear(x, q, s, b, dt, convrot=True, convrot_groupsize=128), res, rs, odt)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16)), f"M={m} N={n}: fused != separate"
+
+
+@pytest.mark.parametrize("m,n,k,bits,gs", [
+    (1024, 4096, 1024, 4, 64),   # grid decoded once, then the int8 DMA GEMM
+    (300, 24600, 1024, 6, 64),   # one 256-row tile over a wide grid: the fused-decode GEMM
+    (100, 1000, 1024, 4, 16),    # group 16: the 128 x 128 decode-in-load kernel, residual kernel after
+    (8, 512, 1024, 6, 64),       # small M
+])
+def test_w4a8_residual_fused_equals_separate(m, n, k, bits, gs):
+    from qlin.quantize import pack_codes
+    Q = qlin()
+    g = torch.Generator().manual_seed(m + n + bits)
+    hi = 15 if bits == 4 else 63
+    q = pack_codes(torch.randint(1, hi + 1, (n, k), generator=g, dtype=torch.int32), bits).to(DEV)
+    s_rel = (2 + 2 * torch.rand(n, k // gs, generator=g)).half().to(DEV)
+    s_ch = (torch.rand(n, generator=g) * 2e-4 + 1e-4).to(DEV)
+    x = torch.randn(m, k, generator=g).half().to(DEV)
+    b = torch.randn(n, generator=g).half().to(DEV)
+    res = (torch.randn(m, n, generator=g) * 3).half().to(DEV)
+    rs = torch.linspace(-2, 2, n).half().to(DEV)
+    args = (x, q, s_rel, s_ch, None, None, b, gs, 256)
+    y = Q.w4a8_int8_linear(*args, residual=res, residual_scale=rs)
+    want = _separate(Q, lambda dt: Q.w4a8_int8_linear(*args, out_dtype=dt), res, rs, torch.float16)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16)), f"w{bits}a8 M={m} N={n}: fused != separate"
+
+
+@pytest.mark.parametrize("name,m", [("Q4_K", 100), ("Q6_K", 512), ("Q8_0", 65), ("IQ4_XS", 8), ("Q4_0", 64)])
+def test_gguf_residual_fused_equals_separate(name, m):
+    """Above 64 rows the GEMM over the decoded weight applies the residual; fewer rows take the
+    weight-streaming kernels and the residual kernel after them."""
+    Q = qlin()
+    n, k = 1000, 2048
+    raw = torch.from_numpy(random_gguf_blocks(name, n, k, seed=m)).to(DEV)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).half().to(DEV)
+    b = torch.randn(n, generator=torch.Generator().manual_seed(1)).to(DEV)
+    res = torch.randn(m, n, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
+    y = Q.gguf_linear(x, raw, name, (n, k), b, torch.bfloat16, residual=res)
+    want = _separate(Q, lambda dt: Q.gguf_linear(x, raw, name, (n, k), b, dt), res, None, torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), want.view(torch.int16)), f"{name} M={m}: fused != separate"
