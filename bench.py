@@ -21,7 +21,7 @@ and CPU baseline: INT8-ConvRot M256 K=N=3072; W4A8 M4096 K3072 N12288; W6A8 M in
 5120 -> 13824 and 13824 -> 5120; and one INT8-ConvRot DiT block layer (4 linears at 4608 tokens),
 reported per layer and x60 beside torch's fp16 F.linear on resident fp16 weights.
 
-Other suites (--suite lora|grad) print their own JSON lines to stderr.
+Other suites (--suite lora|grad|residual|floors) print their own JSON lines to stderr.
 """
 import argparse
 import concurrent.futures as cf
@@ -801,7 +801,7 @@ def other_suites(which, steps, warmup):
         # residual epilogue kernel) that the fused epilogue replaces
         from qlin import _lib
         q, s = int8_weight(3072, 3072, 128, seed=20)
-        qd, sd = torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda()
+        qd, sd = q.cuda(), s.cuda()
         x = gpu_activations(4608, 3072, 40)
         r = gpu_activations(4608, 3072, 41)
         rs = torch.full((3072,), 0.5, device="cuda").half()
