@@ -343,7 +343,8 @@ CONFIGS = {
     "w6a8_m9504_k13824_n5120": dict(kind="a8", bits=6, gs=64, g=256, m=9504, k=13824, n=5120),
     "dit_layer_int8_convrot_m4608": dict(kind="dit", m=4608, g=128,
                                          linears=((9216, 3072), (3072, 3072), (12288, 3072), (3072, 12288))),
-    # a GGUF prefill: 512 activation rows (the weight decoded once into the workspace, then the GEMM)
+    # a GGUF prefill: 512 activation rows (the split kernel's 64-row m-tiles, the weight decoded in
+    # the load stage; one split at this size)
     "gguf_q4_k_m512_k4096_n4096": dict(kind="gguf", type="Q4_K", m=512, k=4096, n=4096),
 }
 
@@ -357,7 +358,7 @@ CONFIG_KERNELS = {
     "w6a8_m9504_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m9504_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "dit_layer_int8_convrot_m4608": "4x (prologue_kernel+gemm_wo_dma_kernel<256,3>)",
-    "gguf_q4_k_m512_k4096_n4096": "prologue_kernel+gguf_decode_f16_kernel+gemm_wo_dmas_kernel<64,128,128,3,true>",
+    "gguf_q4_k_m512_k4096_n4096": "prologue_kernel+gguf_split_kernel<Q4_K,MT=2,32x32>",
 }
 
 

@@ -143,8 +143,9 @@ struct Carver {
 
 size_t ws_int8(int64_t M, int64_t K) { return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4); }
 // GGUF paths by activation rows: one row -> the VALU GEMV; up to GGUF_SMALLM_MAX_M rows -> the
-// MFMA kernels that stream the weights once (K split across workgroups from gguf_split_min_m
-// rows on); more -> row exponents + the tiled fp16 GEMM.
+// MFMA kernels that stream the weights once (the split kernel, K split across workgroups, from
+// gguf_split_min_m rows on); up to gguf_fused_max_m rows -> the split kernel's 64-row m-tiles;
+// more (or K not a whole number of its stages) -> the weight decoded once + the fp16 GEMM.
 constexpr int64_t GGUF_SMALLM_MAX_M = 64;
 // Largest M of the INT8 weight-streaming kernels (the GEMV for one or two rows, then small-M MFMA).
 constexpr int64_t INT8_SMALLM_MAX_M = 16;
@@ -152,11 +153,17 @@ constexpr int64_t INT8_SMALLM_MAX_M = 16;
 // wins from M = 17 on, except Q6_K, whose 16-value units make the per-wave K-split kernel slower
 // (11.8 vs 13.9 us at M = 8).
 int64_t gguf_split_min_m(int type) { return type == gguf::Q6_K ? 5 : 17; }
+// Largest M of the split kernel, whose 64-row m-tiles decode the weight in the load stage (above
+// it: the weight decoded once to fp16, then the fp16-weight GEMM).  Measured at K = N = 4096: the
+// split kernel is 2x faster at 65-128 rows and 1.1-1.3x at 512 rows (one round of 256 workgroups),
+// slower from 640 rows on (a second round); Q6_K, whose 16-value units cost more to decode per
+// m-tile, is 1.16x faster at 256 rows and slower at 384.
+int64_t gguf_fused_max_m(int type) { return (type == gguf::Q6_K || type == gguf::Q3_K || type == gguf::Q2_K) ? 256 : 512; }
 
 // K splits of the shared-activation kernel for this call, 0 when another kernel takes it.
 int gguf_split_for(int type, int64_t M, int64_t N, int64_t K) {
     int qk, ts;
-    if (M < gguf_split_min_m(type) || M > GGUF_SMALLM_MAX_M || !gguf::type_info(type, qk, ts) || K % qk) return 0;
+    if (M < gguf_split_min_m(type) || M > gguf_fused_max_m(type) || !gguf::type_info(type, qk, ts) || K % qk) return 0;
     return gguf_split_parts(type, M, N, K, (K / qk) * ts);
 }
 
@@ -165,9 +172,9 @@ size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
     return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
            (S > 1 ? align_up((size_t)S * M * N * 4) : 0);
 }
-// Above GGUF_SMALLM_MAX_M rows the GEMM reads the weight once per 128-row tile: decoding it once
-// into the workspace (fp16, N x K) and loading it as stored beats decoding every tile (Q4_K,
-// K = N = 4096, M = 512: 200 us decoding in the GEMM).  The copy is made in chunks of weight rows
+// Where the split kernel does not take a call above GGUF_SMALLM_MAX_M rows, the tiled GEMM reads
+// the weight once per 128-row tile: decoding it once into the workspace (fp16, N x K) and loading
+// it as stored beats decoding every tile in that GEMM (Q4_K, K = N = 4096, M = 512: 200 us).  The copy is made in chunks of weight rows
 // of at most GGUF_DECODE_BYTES_MAX (the decode of chunk c + 1 follows the GEMM over chunk c on
 // the stream), so a large tensor such as a 128256 x 4096 output head needs 256 MiB of workspace,
 // not its whole 1 GiB fp16 copy.  The call takes this path when the workspace beyond ws_gguf
@@ -182,8 +189,8 @@ int64_t gguf_decode_rows(int64_t N, int64_t K, int64_t bytes) {
     if (fit >= N) return N;
     return fit / GGUF_DECODE_CHUNK_ROWS * GGUF_DECODE_CHUNK_ROWS;
 }
-size_t ws_gguf_decoded(int64_t M, int64_t N, int64_t K) {
-    if (M <= GGUF_SMALLM_MAX_M || N <= 0 || K <= 0) return 0;
+size_t ws_gguf_decoded(int64_t M, int64_t N, int64_t K, int type) {
+    if (M <= GGUF_SMALLM_MAX_M || N <= 0 || K <= 0 || gguf_split_for(type, M, N, K) > 0) return 0;
     const int64_t rows = std::max<int64_t>(gguf_decode_rows(N, K, GGUF_DECODE_BYTES_MAX),
                                            std::min<int64_t>(N, GGUF_DECODE_CHUNK_ROWS));
     return align_up((size_t)(rows * K * 2));
@@ -328,7 +335,7 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
     switch (op) {
         case QLIN_OP_INT8_LINEAR: return ws_int8(M, K);
         case QLIN_OP_W4A8_LINEAR: return ws_w4a8(M, N, K, param >> 8);  // param: bits | group_size << 8
-        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K);
+        case QLIN_OP_GGUF_LINEAR: return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K, param);
         case QLIN_OP_INT8_GRAD_INPUT: return ws_grad(M, N, K, false);
         case QLIN_OP_W4A8_GRAD_INPUT: return ws_grad(M, N, K, true);
         case QLIN_OP_INT8_LINEAR_LORA: return ws_int8(M, K) + ws_lora(M, K, param);
@@ -340,7 +347,7 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_W4A8_LINEAR_RESIDUAL:
             return ws_w4a8(M, N, K, param >> 8) + align_up((size_t)(M * N * 4)) + 256;
         case QLIN_OP_GGUF_LINEAR_RESIDUAL:
-            return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K) + align_up((size_t)(M * N * 4)) + 256;
+            return ws_gguf(M, N, K, param) + ws_gguf_decoded(M, N, K, param) + align_up((size_t)(M * N * 4)) + 256;
         case QLIN_OP_LORA: {  // the split partials, then their sum
             const int S = lora_splits(M, K, param);
             return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(param > 0 ? param : 0) * 4);
@@ -757,10 +764,13 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
     const bool aligned = ((uintptr_t)weight % 4) == 0;
-    // a residual rides in the epilogue of the GEMM over the decoded fp16 weight (above 64 rows, with
-    // room for the decoded rows); every other kernel returns QLIN_NOT_FUSED before any launch
-    if (R && (M <= GGUF_SMALLM_MAX_M || K % 64 || (uintptr_t)workspace % 16 ||
-              gguf_decode_rows(N, K, (int64_t)workspace_bytes - (int64_t)ws_gguf(M, N, K, ggml_type)) <= 0))
+    // a residual rides in the epilogue of the split kernel (or its reduction) and of the GEMM over
+    // the decoded fp16 weight (with room for the decoded rows); the GEMV and the small-M kernel
+    // return QLIN_NOT_FUSED before any launch
+    const int S = aligned ? gguf_split_for(ggml_type, M, N, K) : 0;
+    if (R && S == 0 &&
+        (M <= GGUF_SMALLM_MAX_M || K % 64 || (uintptr_t)workspace % 16 ||
+         gguf_decode_rows(N, K, (int64_t)workspace_bytes - (int64_t)ws_gguf(M, N, K, ggml_type)) <= 0))
         return QLIN_NOT_FUSED;
     if (M == 1 && aligned) {
         const f16* xo;
@@ -778,7 +788,7 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
             return hip_status(run_gguf_gemv(g, st), "gguf gemv");
         }
     }
-    if (const int S = aligned ? gguf_split_for(ggml_type, M, N, K) : 0; S > 0) {
+    if (S > 0) {
         GgufSplitArgs a;
         a.type = ggml_type;
         if ((s = wo_activations(X, 0, ws, st, a.x, a.ldx, a.xexp))) return s;
@@ -787,6 +797,7 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
         a.w = (const uint8_t*)weight; a.row_bytes = row_bytes;
         a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
         a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+        if (R) a.res = *R;
         return hip_status(run_gguf_split(a, st), "gguf split-K");
     }
     if (aligned && M <= GGUF_SMALLM_MAX_M && gguf_smallm_supported(ggml_type, M, K, row_bytes)) {

@@ -1,5 +1,5 @@
-// GGUF linear for a few dozen activation rows (M up to 64) with the activations shared in LDS and
-// K split across workgroups.
+// GGUF linear from a few dozen to a few hundred activation rows, with the weight decoded in the
+// load stage, the activations shared in LDS and K split across workgroups where the grid is short.
 //
 // A kernel that keeps all of K inside one workgroup of 16 weight rows makes every CU stream all
 // of x: M x K x 2 bytes (512 KiB at M = 64, K = 4096) against 36 KiB of weights, through loads
@@ -15,9 +15,13 @@
 //     the policies the small-M kernel uses (exact fp16 integers, fp32 scales) and reuses each B
 //     fragment for its MT m-tiles; the two halves' accumulators are added through LDS at the end;
 //   * the next stage's activations and weights are in flight while a stage is computed;
+//   * above 64 rows the grid's z dimension holds m-tiles of 64 rows, each decoding the weight
+//     again (measured at K = N = 4096: 2x faster than decoding the weight once to fp16 and running
+//     the fp16-weight GEMM at 65-128 rows, 1.15-1.3x at 512, slower from ~1024 rows);
 //   * S > 1: each workgroup stores its fp32 partial tile to the workspace ([S][M][N]) and a second
 //     kernel adds the S partials in split order (the result does not depend on timing) and applies
-//     the epilogue; S = 1: the epilogue runs in place.
+//     the epilogue; S = 1: the epilogue runs in place.  The epilogue is y = ldexp(acc, xexp[m]) +
+//     bias[n], then, with a residual, y = r[m, n] + rs[n] * y (one fma), rounded once to y's type.
 #include "gguf_mfma_decode.h"
 
 namespace qlin {
@@ -37,7 +41,7 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
     const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K, int S,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy,
-    float* __restrict__ part) {
+    float* __restrict__ part, ResidualTile res) {
     using F = SM<T>;
     constexpr int QK = F::QK, TS = F::TS, UNIT = F::UNIT, VPL = UNIT / 4, SBLK = F::SBLK;
     constexpr int SV = SBLK * QK;                    // values per stage
@@ -73,6 +77,11 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     const int n0 = blockIdx.x * SP_ROWS + np * 32;  // this wave pair's first weight row
     const int nl = lane & 15, g = lane >> 4;
     const int split = blockIdx.y;
+    // m-tile blockIdx.z holds activation rows m0 .. m0 + XR - 1; from here on M counts its rows
+    const int m0 = blockIdx.z * XR, Mall = M;
+    x += (int64_t)m0 * ldx;
+    if (xexp) xexp += m0;
+    M = min(XR, Mall - m0);
     const int stages = K / SV;
     const int st0 = (int)((int64_t)stages * split / S), st1 = (int)((int64_t)stages * (split + 1) / S);
     const int last = st1 - 1;  // the host keeps S <= stages, so every split has a stage
@@ -384,7 +393,7 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
             const int c = tid + SP_THREADS * j, r = c / (SP_ROWS / 4), n = nt0 + 4 * (c % (SP_ROWS / 4));
             if (r >= M || n >= N) continue;
             const f32x4 v = *reinterpret_cast<const f32x4*>(xs + r * ORS + 16 * (c % (SP_ROWS / 4)));
-            float* d = part + ((int64_t)split * M + r) * N + n;
+            float* d = part + ((int64_t)split * Mall + m0 + r) * N + n;
             if (N % 4 == 0) {
                 __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(d));
             } else {
@@ -404,7 +413,8 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             o[q] = __builtin_ldexpf(v[q], e) + (bias ? load_rt(bias, bias_dt, min(n + q, N - 1)) : 0.0f);
-        store4_rt(y, y_dt, (int64_t)r * ldy + n, o, min(4, N - n), vec);
+        if (res.r) residual_apply4(res, m0 + r, n, N, o);
+        store4_rt(y, y_dt, (int64_t)(m0 + r) * ldy + n, o, min(4, N - n), vec);
     }
 }
 
@@ -413,7 +423,8 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
 template <int S>
 __global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
     const float* __restrict__ part, int M, int N, const int32_t* __restrict__ xexp,
-    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy, int xcd_blocks) {
+    const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy, int xcd_blocks,
+    ResidualTile res) {
     int m, n;
     if (xcd_blocks) {
         // The split kernel's workgroup (x, s) is dispatched to XCD (s * blocks + x) % 8 = x % 8 when
@@ -458,6 +469,7 @@ __global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
 #pragma unroll
     for (int q = 0; q < 4; ++q)
         o[q] = __builtin_ldexpf(s[q], e) + (bias ? load_rt(bias, bias_dt, min(n + q, N - 1)) : 0.0f);
+    if (res.r) residual_apply4(res, m, n, N, o);
     // one 8-byte (f16, bf16) or 16-byte (f32) store per thread where rows allow it
     const bool vec = ldy % 4 == 0 && (uintptr_t)y % (y_dt == 0 ? 16 : 8) == 0;
     store4_rt(y, y_dt, (int64_t)m * ldy + n, o, min(4, N - n), vec);
@@ -468,17 +480,17 @@ constexpr int stage_values() { return SM<T>::SBLK * SM<T>::QK; }
 
 template <int T>
 hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
-    dim3 grid((unsigned)((a.N + SP_ROWS - 1) / SP_ROWS), (unsigned)a.S), block(SP_THREADS);
+    // above 64 rows: m-tiles of 64 rows (32 x 32 MFMA tiles) along the grid's z
+    dim3 grid((unsigned)((a.N + SP_ROWS - 1) / SP_ROWS), (unsigned)a.S, (unsigned)((a.M + 63) / 64)), block(SP_THREADS);
     float* part = a.S > 1 ? a.part : nullptr;
 #define QLIN_SP_LAUNCH(MTV, W32V)                                                                          \
     hipLaunchKernelGGL((gguf_split_kernel<T, MTV, W32V>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
-                       a.row_bytes, a.N, a.K, a.S, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, part)
+                       a.row_bytes, a.N, a.K, a.S, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, part, a.res)
     // 16-row m-tiles up to 16 rows, then 32 x 32 tiles (the 32 x 32 x 16 MFMA moves about 1.7x the
     // values per cycle of the 16 x 16 x 32 form)
     if (a.M <= 16) QLIN_SP_LAUNCH(1, false);
     else if (a.M <= 32) QLIN_SP_LAUNCH(1, true);
-    else if (a.M <= 64) QLIN_SP_LAUNCH(2, true);
-    else return hipErrorInvalidValue;
+    else QLIN_SP_LAUNCH(2, true);
 #undef QLIN_SP_LAUNCH
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || a.S == 1) return err;
@@ -490,7 +502,7 @@ hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
                                 : (unsigned)((threads + 255) / 256));
 #define QLIN_SP_REDUCE(SV)                                                                                    \
     hipLaunchKernelGGL(gguf_split_reduce_kernel<SV>, rgrid, dim3(256), 0, st, a.part, a.M, a.N, a.xexp, a.bias, \
-                       a.bias_dtype, a.y, a.y_dtype, a.ldy, xcd_blocks)
+                       a.bias_dtype, a.y, a.y_dtype, a.ldy, xcd_blocks, a.res)
     switch (a.S) {
         case 2: QLIN_SP_REDUCE(2); break;
         case 3: QLIN_SP_REDUCE(3); break;
@@ -508,13 +520,15 @@ hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
 }  // namespace
 
 int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes) {
-    if (M < 1 || M > 64 || N < 1) return 0;
+    if (M < 1 || N < 1) return 0;
     int parts = 0;
     gguf::dispatch_type(type, [&]<int T>() {
         constexpr int SV = stage_values<T>(), RSB = SM<T>::SBLK * SM<T>::TS;
         if (K % SV || RSB % 4 || row_bytes % 4) return;
-        const int64_t stages = K / SV, tiles = (N + SP_ROWS - 1) / SP_ROWS;
-        const int64_t s = (SP_TARGET_BLOCKS + tiles - 1) / tiles;
+        const int64_t stages = K / SV, tiles = (N + SP_ROWS - 1) / SP_ROWS * ((M + 63) / 64);
+        // from 3/4 of the target on, one split: the partials and the reduction cost more than the
+        // idle quarter (K = N = 4096, M = 384, 192 tiles: 2 splits 42-58 us, one split ~37-52)
+        const int64_t s = tiles * 4 >= SP_TARGET_BLOCKS * 3 ? 1 : (SP_TARGET_BLOCKS + tiles - 1) / tiles;
         parts = (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(s, stages), SP_MAX_SPLITS));
     });
     return parts;

@@ -53,6 +53,17 @@ bool gguf_smallm_supported(int type, int64_t M, int64_t K, int64_t row_bytes);
 hipError_t run_gguf_smallm(const GgufSmallMArgs& a, hipStream_t st);
 
 // ---- GGUF linear with activations shared in LDS and K split across workgroups (gguf_split.hip) ----
+// Residual operand of a GEMM epilogue: y = dtype(r[m, n] + rs[n] * base[m, n]) with base the
+// epilogue's fp32 value (bias and any LoRA term added), one fma and one rounding -- the arithmetic
+// of the separate residual kernel (run_residual), so both give the same bits.  r == nullptr: none.
+struct ResidualTile {
+    const void* r = nullptr;     // [M, N], row stride ldr (elements)
+    int r_dt = DT_F16;
+    int64_t ldr = 0;
+    const void* rs = nullptr;    // [N], or nullptr for 1
+    int rs_dt = DT_F16;
+};
+
 struct GgufSplitArgs {
     int type = 0;
     const f16* x = nullptr;          // fp16 activations, 16-byte aligned, ldx % 8 == 0
@@ -64,6 +75,7 @@ struct GgufSplitArgs {
     int N = 0, K = 0;
     int S = 1;                       // K splits (gguf_split_parts)
     float* part = nullptr;           // S > 1: fp32 partials [S][M][N]
+    ResidualTile res;                // y = r + rs * (linear + bias), in the kernel that writes y
     const void* bias = nullptr;
     int bias_dtype = DT_NONE;
     void* y = nullptr;
@@ -138,17 +150,6 @@ struct LoraTile {
     float scale = 1.0f;
 };
 
-// Residual operand of a GEMM epilogue: y = dtype(r[m, n] + rs[n] * base[m, n]) with base the
-// epilogue's fp32 value (bias and any LoRA term added), one fma and one rounding -- the arithmetic
-// of the separate residual kernel (run_residual), so both give the same bits.  r == nullptr: none.
-struct ResidualTile {
-    const void* r = nullptr;     // [M, N], row stride ldr (elements)
-    int r_dt = DT_F16;
-    int64_t ldr = 0;
-    const void* rs = nullptr;    // [N], or nullptr for 1
-    int rs_dt = DT_F16;
-};
-
 // Residual scales of the 8 columns nc .. nc + 7 (1 where rs is absent), as raw bits to convert at use.
 __device__ __forceinline__ void residual_scale_bits8(const ResidualTile& R, int64_t nc, int64_t N, uint32_t (&b)[8]) {
 #pragma unroll
@@ -197,6 +198,19 @@ __device__ __forceinline__ void residual_apply8(const ResidualTile& R, const int
     for (int q = 0; q < Q; ++q)
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[q][e] = __builtin_fmaf(rsv[q][e], v[q][e], bits_to_f32_rt(raw[q][e], R.r_dt));
+}
+// o[q] = fma(rs[n + q], o[q], r[m, n + q]) for the 4 outputs n .. n + 3 of row m (columns past N
+// read column N - 1; their outputs are not stored): the four residual values are requested first.
+__device__ __forceinline__ void residual_apply4(const ResidualTile& R, int64_t m, int64_t n, int64_t N, float (&o)[4]) {
+    float r[4], s[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t c = min<int64_t>(n + q, N - 1);
+        r[q] = load_rt(R.r, R.r_dt, m * R.ldr + c);
+        s[q] = R.rs ? load_rt(R.rs, R.rs_dt, c) : 1.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = __builtin_fmaf(s[q], o[q], r[q]);
 }
 // The same for Q rows that share the columns nc .. nc + 7 and their scales.
 template <int Q>

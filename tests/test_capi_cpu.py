@@ -50,7 +50,8 @@ def test_query_and_workspace():
 def test_workspace_sizes_follow_the_paths():
     """The sizes the C ABI asks for: the A8 int8 grid (N*K bytes) only where the call decodes the
     weight once (from 512 rows, with a group size that is a multiple of 64; counted when the group
-    size is not given), and the GGUF decoded fp16 copy above 64 rows, capped at 256 MiB."""
+    size is not given), and the GGUF decoded fp16 copy above the split kernel's 512 rows (256 for
+    Q6_K), capped at 256 MiB; the split kernel's fp32 partials where it splits K."""
     from qlin import _lib
     L = _lib.load()
     a = lambda v: (v + 255) // 256 * 256
@@ -64,12 +65,19 @@ def test_workspace_sizes_follow_the_paths():
     assert L.qlin_workspace_size(_lib.OP_W4A8_LINEAR, 16, n, k, 4 | 64 << 8, _lib.DT_F16) == a(16 * k) + a(16 * 4)
     lora = lambda p: L.qlin_workspace_size(_lib.OP_W4A8_LINEAR_LORA, m, n, k, p, _lib.DT_F16)
     assert lora(64 | 64 << 16) - lora(64 | 16 << 16) == a(n * k)
-    # GGUF above 64 rows: the decoded copy, at most 256 MiB (32768 rows of K = 4096)
-    g = lambda m, n: L.qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, 4096, 12, _lib.DT_F16)
+    # GGUF above 512 rows (Q4_K, type 12): the decoded copy, at most 256 MiB (32768 rows of K = 4096)
+    g = lambda m, n, t=12: L.qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, 4096, t, _lib.DT_F16)
     base = lambda m, n: a(m * 4096 * 2) + a(m * 4) + a(n * 4)
-    assert g(100, 4096) == base(100, 4096) + a(4096 * 4096 * 2)
-    assert g(100, 128256) == base(100, 128256) + (256 << 20)
+    assert g(600, 4096) == base(600, 4096) + a(4096 * 4096 * 2)
+    assert g(600, 128256) == base(600, 128256) + (256 << 20)
     assert g(64, 128256) < (64 << 20)                # K split or small-M kernels: no copy
+    # the split kernel's m-tiles up to 512 rows: 32 row blocks x 2 m-tiles = 64 tiles -> 4 splits
+    # of fp32 partials at M = 100; 32 x 8 tiles fill the GPU at M = 512 -> one split, no partials
+    assert g(100, 4096) == base(100, 4096) + a(4 * 100 * 4096 * 4)
+    assert g(512, 4096) == base(512, 4096)
+    assert g(384, 4096) == base(384, 4096)           # 192 tiles, 3/4 of the GPU: one split
+    assert g(256, 4096) == base(256, 4096) + a(2 * 256 * 4096 * 4)  # 128 tiles: two splits
+    assert g(512, 4096, 14) == base(512, 4096) + a(4096 * 4096 * 2)  # Q6_K: the split kernel to 256 rows
 
 
 def _d(t, dt=None):

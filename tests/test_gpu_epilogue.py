@@ -195,12 +195,19 @@ def test_w4a8_residual_fused_equals_separate(m, n, k, bits, gs):
     assert torch.equal(y.view(torch.int16), want.view(torch.int16)), f"w{bits}a8 M={m} N={n}: fused != separate"
 
 
-@pytest.mark.parametrize("name,m", [("Q4_K", 100), ("Q6_K", 512), ("Q8_0", 65), ("IQ4_XS", 8), ("Q4_0", 64)])
-def test_gguf_residual_fused_equals_separate(name, m):
-    """Above 64 rows the GEMM over the decoded weight applies the residual; fewer rows take the
-    weight-streaming kernels and the residual kernel after them."""
+@pytest.mark.parametrize("name,m,n,k", [
+    ("Q4_K", 100, 1000, 2048),  # split kernel, m-tiles, 8 splits: the reduction applies it
+    ("Q4_0", 64, 1000, 2048),   # split kernel, 8 splits
+    ("Q8_0", 65, 1000, 2048),   # split kernel, two m-tiles (the second one row)
+    ("Q5_K", 512, 4096, 1024),  # split kernel, 256 tiles, one split: the kernel's own epilogue
+    ("Q6_K", 512, 1000, 2048),  # the GEMM over the decoded weight
+    ("IQ4_XS", 8, 1000, 2048),  # small-M kernel, then the residual kernel
+])
+def test_gguf_residual_fused_equals_separate(name, m, n, k):
+    """From 17 to 512 rows (Q6_K 5 to 256) the split kernel, or its reduction, applies the residual;
+    above, the GEMM over the decoded weight; fewer rows take the weight-streaming kernels and the
+    residual kernel after them.  Every route gives the bits of the separate residual kernel."""
     Q = qlin()
-    n, k = 1000, 2048
     raw = torch.from_numpy(random_gguf_blocks(name, n, k, seed=m)).to(DEV)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).half().to(DEV)
     b = torch.randn(n, generator=torch.Generator().manual_seed(1)).to(DEV)

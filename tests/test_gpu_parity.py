@@ -153,6 +153,39 @@ def test_gguf_linear_split_k(name, m, n, k):
     check_linear(got, want, f"{name} M={m} N={n} K={k}")
 
 
+@pytest.mark.parametrize("name,m,n,k", [
+    ("Q4_K", 65, 131, 512),     # two m-tiles, the second one row; ragged N; 2 splits
+    ("Q4_0", 100, 1000, 2048),  # 8 row blocks x 2 m-tiles, 8 splits
+    ("Q8_0", 200, 4096, 1024),  # 32 x 4 tiles, 2 splits (XCD-local reduction)
+    ("Q6_K", 256, 256, 2048),   # 2 x 4 tiles, 4 splits (two-block stages)
+    ("IQ4_XS", 300, 4096, 512), # 32 x 5 tiles, 2 splits
+    ("Q4_0", 384, 4096, 1024),  # 32 x 6 tiles, 3/4 of the GPU: one split
+    ("Q5_K", 512, 4096, 1024),  # 32 x 8 tiles: one split, the epilogue in the kernel
+    ("Q3_K", 130, 200, 1024),   # sub-block minimum MFMA across three m-tiles
+    ("Q2_K", 193, 136, 512),    # 16-value units, four m-tiles, the last one row
+])
+def test_gguf_linear_split_m_tiles(name, m, n, k):
+    """From 65 to 512 rows (Q2_K, Q3_K, Q6_K: 256) the split kernel runs 64-row m-tiles along the
+    grid's z, each decoding the weight in its load stage: ragged M and N, single and multiple splits,
+    bias; no decoded copy is asked for."""
+    from qlin import _lib
+    raw = random_gguf_blocks(name, n, k, seed=23)
+    w = O.gguf_dequantize(raw, name, (n, k))
+    x = x_fp16(m, k, seed=m + 5)
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(7)) * 0.1).half()
+    want = O.linear_ref(x.float().numpy(), w, b.float().numpy())
+    tid = qlin().GGUF_TYPES[name][0]
+    size = _lib.load().qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, k, tid, _lib._TORCH_DT[torch.float16])
+    # fp16 activations, row and column exponents, fp32 partials of S splits; no decoded copy
+    a = lambda v: (v + 255) // 256 * 256
+    stages = k // (512 if name in ("Q6_K", "Q3_K") else 256)
+    tiles = -(-n // 128) * -(-m // 64)
+    splits = 1 if 4 * tiles >= 3 * 256 else max(1, min(-(-256 // tiles), stages, 8))
+    assert size == a(m * k * 2) + a(m * 4) + a(n * 4) + (a(splits * m * n * 4) if splits > 1 else 0)
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), bias=b.to(DEV))
+    check_linear(got, want, f"{name} M={m} N={n} K={k}")
+
+
 def _split_call(raw, name, n, k, x, ws=None):
     """qlin_gguf_linear through the C ABI with a caller-owned workspace (None: the cached one)."""
     Q = qlin()
@@ -229,18 +262,20 @@ def test_gguf_linear_split_k_graph_replays():
 
 
 @pytest.mark.parametrize("name,m,n,k", [
+    # from 17 to 512 rows the split kernel takes K a whole number of its 256-value stages (Q6_K 512):
+    # these shapes have other K or more rows
     ("Q4_0", 65, 131, 1056),    # K % 64 == 32: the last k-tile's upper half is past K; ragged N
     ("Q8_0", 200, 300, 96),     # two k-tiles, the second half empty
     ("IQ4_NL", 129, 257, 2080),
-    ("Q4_K", 300, 520, 2048),
+    ("Q4_K", 600, 520, 2048),
     ("Q6_K", 96, 1000, 768),
-    ("Q2_K", 77, 64, 512),      # one column tile, half of it past N
-    ("Q5_K", 130, 256, 6144),   # the decode keeps 3 chunks of 8 per thread (4 slots)
-    ("Q8_0", 70, 96, 8448),     # K > 8192: the decode reads each row twice
+    ("Q2_K", 577, 64, 512),     # one column tile, half of it past N
+    ("Q5_K", 530, 256, 6144),   # the decode keeps 3 chunks of 8 per thread (4 slots)
+    ("Q8_0", 520, 96, 8448),    # K > 8192: the decode reads each row twice
     ("Q4_K", 1024, 512, 1024),  # 128 x 128 tiles
 ])
 def test_gguf_linear_decode_once(name, m, n, k):
-    """Above 64 rows, with the workspace qlin_workspace_size reports, the weight is decoded once into
+    """Above the split kernel's rows, with the workspace qlin_workspace_size reports, the weight is decoded once into
     it as fp16 and a DMA-ring GEMM loads that copy (K % 64 == 32: the tiled GEMM loads it); with the
     minimum workspace (no room for the copy) the tiled GEMM decodes every tile it loads.  Both meet
     the oracle's bar.  The workspaces start as all-ones bytes (fp16 NaN), so any element of the
@@ -323,13 +358,13 @@ def test_gguf_linear_decode_workload(name):
 
 @pytest.mark.parametrize("name,odt", [("Q4_K", torch.float16), ("Q6_K", torch.bfloat16), ("Q8_0", torch.float32)])
 def test_gguf_linear_decode_in_chunks(name, odt):
-    """Above 64 rows the weight is decoded once into the workspace in chunks of weight rows (at most
+    """Above 512 rows the weight is decoded once into the workspace in chunks of weight rows (at most
     256 MiB each, multiples of 128 rows): with the workspace the size query asks for (one chunk
     here), with room for 256 rows (four chunks, the last ragged) or 130 rows (128-row chunks), the
     output equals the oracle's linear to the bar; with no room for 128 rows each GEMM tile decodes
     its own weights."""
     from qlin import _lib as L
-    m, n, k = 100, 1000, 2048
+    m, n, k = 520, 1000, 2048  # above the split kernel's rows
     raw = random_gguf_blocks(name, n, k, seed=77)
     w = O.gguf_dequantize(raw, name, (n, k))
     # activations of 0.25: outputs below 4, where one bf16 rounding step stays under the 2e-2 bar

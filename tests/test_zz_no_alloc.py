@@ -56,9 +56,13 @@ def case(name, m, n, k, seed, xdt=torch.float16, odt=torch.float16, bias=False):
     # bf16 activations (normalized into the scratch by the prologue), then one fp16 row (GEMV)
     (("Q6_K", 40, 3072, 4096, torch.bfloat16, torch.float32, True), ("IQ4_XS", 1, 2048, 4096, torch.float16,
                                                                      torch.float16, False)),
-    # the tiled GEMM (M > 64: row exponents and normalized rows in the scratch), then small M
-    (("Q5_K", 200, 1024, 2048, torch.float16, torch.bfloat16, False), ("Q4_0", 8, 512, 1024, torch.float16,
+    # the weight decoded once into the scratch and the fp16 GEMM (above the split kernel's 512 rows),
+    # then small M
+    (("Q5_K", 600, 1024, 2048, torch.float16, torch.bfloat16, False), ("Q4_0", 8, 512, 1024, torch.float16,
                                                                        torch.float16, True)),
+    # the split kernel's m-tiles (8 splits of partials in the scratch), then a single-split call
+    (("Q4_K", 200, 1024, 2048, torch.float16, torch.float16, True), ("Q8_0", 512, 4096, 1024, torch.float16,
+                                                                     torch.float16, False)),
 ])
 def test_noalloc_matches_the_workspace_entry_point(first, second):
     for i, (name, m, n, k, xdt, odt, bias) in enumerate((first, second)):
