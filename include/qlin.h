@@ -134,8 +134,8 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
  * qlin_lora_apply (lora_down [R, K], lora_up [N, R], f32/f16/bf16; x is the caller's activation,
  * before any ConvRot rotation).  The kernels that carry the term are the 256 x 256 INT8 GEMM (M > 16,
  * grids of 160 tiles or more, 16-byte aligned operands) and the A8 decode-once GEMM (M >= 512, or M > 32 on grids of fewer than 192 tiles of 256 x 256), for a
- * rank that is a multiple of 8, at most 64 (at most 32 for fp32 lora_up in the A8 GEMM), with
- * 16-byte aligned lora_up rows; other calls return
+ * rank that is a multiple of 8, at most 128 (at most 64 for fp32 lora_up in the A8 GEMM; ranks
+ * above 64, or 32, in two passes over the tile), with 16-byte aligned lora_up rows; other calls return
  * QLIN_EUNSUPPORTED before launching anything, and the caller runs the plain linear and
  * qlin_lora_apply_base instead.  Workspace: qlin_workspace_size(QLIN_OP_INT8_LINEAR_LORA or
  * QLIN_OP_W4A8_LINEAR_LORA, M, N, K, R, x_dtype).

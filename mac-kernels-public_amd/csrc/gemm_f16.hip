@@ -549,7 +549,8 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
 // their fp32 base values ldexp(acc, E) * scale + bias, then base + lora_scale * t up^T with t and up
 // staged through LDS (lora_tile_epilogue), the order of the separate LoRA kernel; the staged values
 // are final, so the output is rounded once.
-// Largest LoRA rank the 256 x 256, 3-stage kernel stages in its LDS (the row exponents aside).
+// Largest LoRA rank the 256 x 256, 3-stage kernel stages in its LDS at once (the row exponents
+// aside); twice that is added in two passes.
 constexpr int wo_dma_lora_rank(int du) {
     constexpr int lds = 3 * (256 * 64 * 2 + 256 * 64) - 256 * 4;
     return du == DT_F32 ? lora_max_rank<DT_F32, 256, 256>(lds) : lora_max_rank<DT_BF16, 256, 256>(lds);
@@ -708,7 +709,7 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
                 for (int r = 0; r < 16; ++r)
                     acc[i][j][r] = __builtin_ldexpf(acc[i][j][r], erow[wm * WM + 32 * i + 8 * (r / 4) + 4 * h + r % 4]) * csn + bvn;
         }
-        lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(a.lora, smem, m0, n0, a.M, a.N, wm * WM, wn * WN, tid, lane, acc);
+        lora_tile_epilogue_ranks<LDU, BMT, BNT, RC, NT, TI, TJ>(a.lora, smem, m0, n0, a.M, a.N, wm * WM, wn * WN, tid, lane, acc);
     }
     float cs[CB8], bv[CB8], rsv[8];
     residual_scales8(a.res, rsb, rsv);
@@ -1145,7 +1146,7 @@ bool gemm_f16_fuses_lora(const GemmF16Args& a) {
     const int64_t tiles = ((a.M + 255) / 256) * ((a.N + 255) / 256);
     const LoraTile& L = a.lora;
     const int es = L.up_dt == DT_F32 ? 4 : 2;
-    return vec && tiles >= 160 && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= wo_dma_lora_rank(L.up_dt) &&
+    return vec && tiles >= 160 && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= 2 * wo_dma_lora_rank(L.up_dt) &&
            (uintptr_t)L.t % 16 == 0 &&
            (uintptr_t)L.up % 16 == 0 && (L.ld_up * es) % 16 == 0 &&
            (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);

@@ -894,7 +894,7 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
                     acc[i][j][r] = __float_as_int(base);
                 }
         }
-        lora_tile_epilogue<LDU, BMT, BNT, RC, NT, TI, TJ>(p.lora, smem, m0, n0, p.M, p.N, wm * WM, wn * WN, tid, lane, acc);
+        lora_tile_epilogue_ranks<LDU, BMT, BNT, RC, NT, TI, TJ>(p.lora, smem, m0, n0, p.M, p.N, wm * WM, wn * WN, tid, lane, acc);
     }
     float bv[CB8], rsv[8];
     residual_scales8(p.res, rsb, rsv);
@@ -1179,7 +1179,7 @@ bool gemm_i8_fuses_lora(const GemmI8Args& p) {
                      (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0 && !a8_smallm_ok(p);
     const LoraTile& L = p.lora;
     const int es = L.up_dt == DT_F32 ? 4 : 2;
-    return dma && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= i8dma_lora_rank(L.up_dt) &&
+    return dma && L.t && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= 2 * i8dma_lora_rank(L.up_dt) &&
            (uintptr_t)L.t % 16 == 0 && (uintptr_t)L.up % 16 == 0 &&
            (L.ld_up * es) % 16 == 0 && (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);
 }

@@ -171,12 +171,13 @@ __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* l
     uint8_t* us = lds + 2 * BMT * TBPR;
     const int r32 = lane & 31, h = lane >> 5;
     u32x4 tv[TP][2], uv[UP];
+    const int64_t ldt = L.ld_t ? L.ld_t : L.R;
 #pragma unroll
     for (int i = 0; i < TP; ++i) {
         const int p = tid + NT * i, row = p / (RC / 8), c = 8 * (p % (RC / 8));
         const int64_t m = min(m0 + row, M - 1), k = min<int64_t>(c, L.R - 8);
-        tv[i][0] = *reinterpret_cast<const u32x4*>(L.t + m * L.R + k);
-        tv[i][1] = *reinterpret_cast<const u32x4*>(L.t + m * L.R + k + 4);
+        tv[i][0] = *reinterpret_cast<const u32x4*>(L.t + m * ldt + k);
+        tv[i][1] = *reinterpret_cast<const u32x4*>(L.t + m * ldt + k + 4);
     }
 #pragma unroll
     for (int i = 0; i < UP; ++i) {
@@ -249,6 +250,25 @@ __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* l
         (col.template operator()<J>(), ...);
     }(std::make_integer_sequence<int, TJ>{});
     __syncthreads();  // LDS free for the caller's staging
+}
+
+// The same for ranks up to 2 RC: ranks 0 .. RC - 1 first, then the rest, each pass staged on its
+// own; the second pass continues the MFMA chain of the first on the same accumulators, so the
+// terms are added in rank order.  Requires R % 8 == 0 and 8 <= R <= 2 RC.
+template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, typename AccT>
+__device__ __forceinline__ void lora_tile_epilogue_ranks(const LoraTile& L, uint8_t* lds, int64_t m0, int64_t n0,
+                                                         int64_t M, int64_t N, int wr0, int wc0, int tid, int lane,
+                                                         AccT (&acc)[TI][TJ]) {
+    LoraTile p = L;
+    p.ld_t = L.R;
+    p.R = L.R < RC ? L.R : RC;
+    lora_tile_epilogue<DU, BMT, BNT, RC, NT, TI, TJ>(p, lds, m0, n0, M, N, wr0, wc0, tid, lane, acc);
+    if (L.R > RC) {
+        p.t = L.t + RC;
+        p.up = reinterpret_cast<const uint8_t*>(L.up) + RC * (DU == DT_F32 ? 4 : 2);
+        p.R = L.R - RC;
+        lora_tile_epilogue<DU, BMT, BNT, RC, NT, TI, TJ>(p, lds, m0, n0, M, N, wr0, wc0, tid, lane, acc);
+    }
 }
 
 }  // namespace qlin

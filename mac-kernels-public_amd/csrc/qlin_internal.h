@@ -148,6 +148,7 @@ struct LoraTile {
     int64_t ld_up = 0;
     int64_t R = 0;
     float scale = 1.0f;
+    int64_t ld_t = 0;                // row stride of t (0: R)
 };
 
 // Residual scales of the 8 columns nc .. nc + 7 (1 where rs is absent), as raw bits to convert at use.

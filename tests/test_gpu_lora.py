@@ -247,9 +247,12 @@ def _close_or_equal(fused, plain, what):
 
 
 @pytest.mark.parametrize("r,fdt,xdt", [(64, torch.bfloat16, torch.bfloat16), (16, torch.float16, torch.float16),
-                                       (48, torch.float32, torch.bfloat16), (8, torch.bfloat16, torch.float32)])
+                                       (48, torch.float32, torch.bfloat16), (8, torch.bfloat16, torch.float32),
+                                       (128, torch.bfloat16, torch.bfloat16), (72, torch.float16, torch.float16),
+                                       (120, torch.float32, torch.bfloat16)])
 def test_int8_lora_fused_into_gemm(r, fdt, xdt, fused_calls):
-    """M2048 N5120: 160 tiles of 256 x 256, the GEMM that carries the LoRA term."""
+    """M2048 N5120: 160 tiles of 256 x 256, the GEMM that carries the LoRA term; ranks above 64
+    in two passes over the tile."""
     Q = qlin()
     m, n, k, g = 2048, 5120, 1024, 128
     w = (torch.randn(n, k, generator=torch.Generator().manual_seed(20)) * 0.02).numpy()
@@ -281,6 +284,9 @@ def test_int8_lora_fused_into_gemm(r, fdt, xdt, fused_calls):
     (4, 1024, 2048, 64, torch.bfloat16),   # 128 x 128 tiles
     (6, 1100, 1024, 32, torch.float32),    # 128 x 64 tiles (fewer than 128 tiles of 128 x 128)
     (4, 200, 2048, 16, torch.bfloat16),    # 128 x 64 tiles, a few hundred rows
+    (4, 2048, 6144, 128, torch.bfloat16),  # 256 x 256 tiles, rank 128 in two passes of 64
+    (6, 2048, 4096, 96, torch.float16),    # 128 x 256 tiles, passes of 64 and 32
+    (6, 1024, 2048, 64, torch.float32),    # 128 x 128 tiles, fp32 up factors in passes of 32
 ])
 def test_w4a8_lora_fused_into_gemm(bits, m, n, r, fdt, fused_calls):
     """A8 calls whose weight grid is decoded once (from 512 rows, and above 32 rows on grids of fewer
@@ -308,10 +314,10 @@ def test_w4a8_lora_fused_into_gemm(bits, m, n, r, fdt, fused_calls):
     check_side(y, base, side_ref(x.cpu(), down, up, 1.5), f"w{bits}a8 fused m={m} r={r}")
 
 
-@pytest.mark.parametrize("r,fdt", [(12, torch.bfloat16), (72, torch.bfloat16), (40, torch.float32)])
+@pytest.mark.parametrize("r,fdt", [(12, torch.bfloat16), (136, torch.bfloat16), (72, torch.float32)])
 def test_lora_fused_declines_to_the_separate_kernels(r, fdt, fused_calls):
-    """Ranks the GEMM epilogue does not take at a fused shape (not a multiple of 8; above 64; fp32 up
-    factors above 32 in the A8 GEMM): the fused entry point declines before launching and the
+    """Ranks the GEMM epilogue does not take at a fused shape (not a multiple of 8; above 128; fp32 up
+    factors above 64 in the A8 GEMM): the fused entry point declines before launching and the
     separate LoRA kernels give the result."""
     Q = qlin()
     m, n, k = 2048, 5120, 512
@@ -321,7 +327,7 @@ def test_lora_fused_declines_to_the_separate_kernels(r, fdt, fused_calls):
     from qlin import _lib
     L = _lib.load()
     if fdt == torch.float32:
-        # the INT8 GEMM takes fp32 up factors to rank 64; the A8 GEMM's LDS holds 32
+        # the INT8 GEMM takes fp32 up factors to rank 128; the A8 GEMM's LDS holds 32 at a time
         codes = torch.randint(1, 16, (n, k), generator=torch.Generator().manual_seed(43), dtype=torch.int32)
         qp = qz().pack_codes(codes, 4).to(DEV)
         s_rel = torch.full((n, k // 64), 10.0, dtype=torch.float16, device=DEV)
