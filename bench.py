@@ -796,6 +796,26 @@ def other_suites(which, steps, warmup):
                 y.addmm_(torch.nn.functional.linear(x, down), up.t(), alpha=0.8)
             timed(f"lora unfused {fmt} r{r} (bf16 addmm beside the call)", unfused, fl + flr,
                   n * k + m * k * 2 + m * n * 4, peak, unit)
+        # GGUF Q4_K at K = N = 4096 (the decode shape and a prefill), rank 64, fp16: the base call, the
+        # call with the LoRA in the K-split reduction, and torch's fp16 LoRA beside the call
+        n = k = 4096
+        raw = make_gguf_weights("Q4_K", n, k, 1, seed=5)[0]
+        tid = qlin.GGUF_TYPES["Q4_K"][0]
+        d16 = (torch.randn(r, k, generator=gen) * 0.02).half().cuda()
+        u16 = (torch.randn(n, r, generator=gen) * 0.02).half().cuda()
+        for m in (64, 256):
+            xg = torch.randn(m, k, generator=gen).half().cuda()
+            g = lambda **kw: qlin.gguf_linear(xg, raw, tid, (n, k), **kw)
+            fl, flr, nb = 2 * m * n * k, 2 * m * r * (k + n), gguf_bytes("Q4_K", n, k) + m * k * 2 + m * n * 2
+            timed(f"lora base gguf_q4_k M{m} K{k} N{n}", lambda: g(), fl, nb, FP16_PEAK_TFLOPS, "TFLOPs")
+            timed(f"lora fused gguf_q4_k M{m} r{r}", lambda: g(lora_down=d16, lora_up=u16, lora_scale=0.8), fl + flr,
+                  nb, FP16_PEAK_TFLOPS, "TFLOPs")
+
+            def unfused_g(xg=xg, g=g):
+                y = g()
+                y.addmm_(torch.nn.functional.linear(xg, d16), u16.t(), alpha=0.8)
+            timed(f"lora unfused gguf_q4_k M{m} r{r} (fp16 addmm beside the call)", unfused_g, fl + flr, nb,
+                  FP16_PEAK_TFLOPS, "TFLOPs")
     if which in ("residual", "all"):
         # the residual keyword at large M: y = residual + residual_scale * (x W^T + b) applied in the
         # GEMM epilogue, beside the plain call and the two-kernel route (the linear in fp32, then the

@@ -66,6 +66,7 @@ typedef enum {
     QLIN_OP_INT8_LINEAR_RESIDUAL = 8,  /* qlin_int8_linear_residual: param as QLIN_OP_INT8_LINEAR */
     QLIN_OP_W4A8_LINEAR_RESIDUAL = 9,  /* qlin_w4a8_linear_residual: param as QLIN_OP_W4A8_LINEAR */
     QLIN_OP_GGUF_LINEAR_RESIDUAL = 10, /* qlin_gguf_linear_residual: param = the ggml type */
+    QLIN_OP_GGUF_LINEAR_LORA = 11,     /* qlin_gguf_linear_lora: param = the ggml type | R << 8 */
 } qlin_op;
 
 /* ggml type ids accepted by the GGUF entry points (enum ggml_type). */
@@ -151,6 +152,21 @@ qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata
                                   qlin_tensor* y, int bits, int group_size, int convrot_groupsize,
                                   const qlin_tensor* lora_down, const qlin_tensor* lora_up, float lora_scale,
                                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* qlin_gguf_linear with unmerged LoRA in the epilogue: t = x @ lora_down^T (fp32, in the workspace),
+ * then the K-split reduction of the split kernel adds lora_scale * t @ lora_up^T to each output tile
+ * in fp32 after the bias and rounds once into y.  Taken from 17 rows to the split kernel's limit
+ * (512 rows; 256 for Q2_K, Q3_K, Q6_K) where K holds at least two of its stages (the call then splits
+ * K at least in two), for a rank that is a multiple of 8 up to 128 with 16-byte aligned lora_up rows;
+ * other calls return QLIN_EUNSUPPORTED before launching anything, and the caller runs the plain
+ * linear and qlin_lora_apply_base.  Workspace: qlin_workspace_size(QLIN_OP_GGUF_LINEAR_LORA, M, N, K,
+ * ggml_type | R << 8, x_dtype).  Replaces the lora_down / lora_up / lora_scale keywords of
+ * comfy_kitchen gguf_linear (tests/test_gguf_node.py:110-174; the GGUF LoRA in the epilogue,
+ * docs/research/2026-10-03-gguf-on-metal.md:97, 107). */
+qlin_status qlin_gguf_linear_lora(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                                  const qlin_tensor* bias, qlin_tensor* y, const qlin_tensor* lora_down,
+                                  const qlin_tensor* lora_up, float lora_scale, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 /* Bytes of the fixed per-GPU scratch behind qlin_gguf_linear_noalloc. */
 #define QLIN_NOALLOC_SCRATCH_BYTES (16u << 20)

@@ -167,6 +167,16 @@ int gguf_split_for(int type, int64_t M, int64_t N, int64_t K) {
     return gguf_split_parts(type, M, N, K, (K / qk) * ts);
 }
 
+// K splits of a GGUF call with a LoRA term: the split kernel's count, at least two (its reduction
+// carries the term); 0 when the call cannot take it (16 rows or fewer, past the split kernel's rows,
+// K of a single stage).
+int gguf_lora_splits(int type, int64_t M, int64_t N, int64_t K) {
+    int qk, ts;
+    if (M <= 16 || M > gguf_fused_max_m(type) || !gguf::type_info(type, qk, ts) || K % qk) return 0;
+    const int S = gguf_split_parts(type, M, N, K, (K / qk) * ts, 2);
+    return S >= 2 ? S : 0;
+}
+
 size_t ws_gguf(int64_t M, int64_t N, int64_t K, int type) {
     const int S = gguf_split_for(type, M, N, K);
     return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
@@ -341,6 +351,11 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_INT8_LINEAR_LORA: return ws_int8(M, K) + ws_lora(M, K, param);
         case QLIN_OP_W4A8_LINEAR_LORA:  // param: R | group_size << 16
             return ws_w4a8(M, N, K, param >> 16) + ws_lora(M, K, param & 0xFFFF);
+        case QLIN_OP_GGUF_LINEAR_LORA: {  // param: ggml type | R << 8
+            const int S = gguf_lora_splits(param & 0xFF, M, N, K);
+            return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
+                   align_up((size_t)std::max(S, 1) * M * N * 4) + ws_lora(M, K, param >> 8);
+        }
         // the residual variants: the linear's workspace, then room for its fp32 output when the
         // call's kernel does not apply the residual itself
         case QLIN_OP_INT8_LINEAR_RESIDUAL: return ws_int8(M, K) + align_up((size_t)(M * N * 4)) + 256;
@@ -859,6 +874,50 @@ qlin_status qlin_gguf_linear(const qlin_tensor* x, const void* weight, int ggml_
                              const qlin_tensor* bias, qlin_tensor* y, void* workspace, size_t workspace_bytes,
                              void* stream) {
     return gguf_linear_impl(x, weight, ggml_type, N, K, bias, y, workspace, workspace_bytes, stream);
+}
+
+qlin_status qlin_gguf_linear_lora(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,
+                                  const qlin_tensor* bias, qlin_tensor* y, const qlin_tensor* lora_down,
+                                  const qlin_tensor* lora_up, float lora_scale, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    int qk, ts;
+    if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
+    if (!weight) return fail(QLIN_EINVAL, "weight is missing");
+    if (K % qk) return fail(QLIN_EUNSUPPORTED, "K=%lld is not a whole number of %d-value blocks", (long long)K, qk);
+    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
+    Mat X, Y, D, U;
+    qlin_status s = check_xy(x, y, N, K, X, Y);
+    if (s) return s;
+    int bdt;
+    if ((s = check_bias(bias, N, bdt))) return s;
+    const LoraIn L{lora_down, lora_up, lora_scale};
+    if ((s = lora_operands(L, N, K, D, U))) return s;
+    const int64_t M = X.rows, R = D.rows;
+    const int S = ((uintptr_t)weight % 4) == 0 ? gguf_lora_splits(ggml_type, M, N, K) : 0;
+    GgufSplitArgs a;
+    a.type = ggml_type;
+    a.M = (int)M; a.N = (int)N; a.K = (int)K; a.S = S;
+    a.w = (const uint8_t*)weight; a.row_bytes = (K / qk) * ts;
+    a.bias = bias ? bias->data : nullptr; a.bias_dtype = bdt;
+    a.y = Y.data; a.y_dtype = Y.dtype; a.ldy = Y.ld;
+    a.lora.up = U.data; a.lora.up_dt = U.dtype; a.lora.ld_up = U.ld; a.lora.R = R; a.lora.scale = lora_scale;
+    if (S < 2 || !gguf_split_fuses_lora(a) || (uintptr_t)workspace % 16)
+        return fail(QLIN_EUNSUPPORTED, "the GGUF LoRA term is fused only into the split kernel's reduction (17 to 512 "
+                                       "rows, 256 for Q2_K/Q3_K/Q6_K, K of two stages or more, a 4-byte aligned weight), "
+                                       "for a rank that is a multiple of 8 up to 128 with 16-byte aligned lora_up rows");
+    const size_t need = align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
+                        align_up((size_t)S * M * N * 4) + ws_lora(M, K, R);
+    if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
+    if (M == 0 || N == 0) return QLIN_OK;
+    hipStream_t st = (hipStream_t)stream;
+    Carver ws{(uint8_t*)workspace, workspace_bytes};
+    float* t = (float*)ws.take(ws_lora(M, K, R));
+    const float* tf = nullptr;
+    if ((s = hip_status(run_lora_t(lora_down_args(X, D, t), st, &tf), "lora down"))) return s;
+    a.lora.t = tf;
+    if ((s = wo_activations(X, 0, ws, st, a.x, a.ldx, a.xexp))) return s;
+    a.part = (float*)ws.take((size_t)S * M * N * 4);
+    return hip_status(run_gguf_split(a, st), "gguf split-K with LoRA");
 }
 
 qlin_status qlin_gguf_linear_residual(const qlin_tensor* x, const void* weight, int ggml_type, int64_t N, int64_t K,

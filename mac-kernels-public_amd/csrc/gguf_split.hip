@@ -23,6 +23,7 @@
 //     the epilogue; S = 1: the epilogue runs in place.  The epilogue is y = ldexp(acc, xexp[m]) +
 //     bias[n], then, with a residual, y = r[m, n] + rs[n] * y (one fma), rounded once to y's type.
 #include "gguf_mfma_decode.h"
+#include "lora_frag.h"
 
 namespace qlin {
 
@@ -475,6 +476,65 @@ __global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
     store4_rt(y, y_dt, (int64_t)m * ldy + n, o, min(4, N - n), vec);
 }
 
+// The reduction with an unmerged LoRA term (S > 1): one workgroup per 64 x 128 output tile, each
+// wave a 32 x 32 sub-tile in the MFMA C layout (lane l, register r: row 8 (r / 4) + 4 (l / 32) +
+// r % 4, column l % 32).  The S partials are added in split order and the base ldexp(sum, xexp[m]) +
+// bias[n] formed as in gguf_split_reduce_kernel; lora_tile_epilogue_ranks then adds lora_scale *
+// t up^T to those fp32 values (bf16 MFMAs on exact hi / lo parts, ranks up to 2 x 64), and the tile
+// leaves through LDS as 8-output row pieces, rounded once.  Workgroup b takes row block b % blocks,
+// so with a multiple of 8 row blocks it runs on the XCD that wrote that block's partials (measured
+// at K = N = 4096, M = 64: 1.3 us faster than 32 x 64 tiles, whose grid is 4x larger).
+constexpr int SPL_BM = 64, SPL_BN = SP_ROWS, SPL_NT = SP_THREADS, SPL_LDS = 48 * 1024;
+template <int DU, int S>
+__global__ __launch_bounds__(SPL_NT) void gguf_split_lora_reduce_kernel(
+    const float* __restrict__ part, int M, int N, const int32_t* __restrict__ xexp, const void* __restrict__ bias,
+    int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy, LoraTile L) {
+    constexpr int BNT = SPL_BN, NT = SPL_NT, ORW = BNT + 4;
+    constexpr int RC = lora_max_rank<DU, SPL_BM, BNT>(SPL_LDS);
+    static_assert(RC == 64, "one pass of 64 ranks fits (two passes to 128)");
+    static_assert(SPL_BM * ORW * 4 <= SPL_LDS, "output staging must fit");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[SPL_LDS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, h = lane >> 5, wi = wave >> 2, wj = wave & 3;
+    const int blocks = (N + BNT - 1) / BNT;
+    const int64_t n0 = (int64_t)(blockIdx.x % blocks) * BNT, m0 = (int64_t)(blockIdx.x / blocks) * SPL_BM;
+    const int64_t n = min(n0 + 32 * wj + r32, (int64_t)N - 1), mn = (int64_t)M * N;
+    // every partial of the sub-tile is requested before the first add; rows past M re-read row M - 1
+    f32x16 v[S];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t m = min(m0 + 32 * wi + 8 * (r / 4) + 4 * h + r % 4, (int64_t)M - 1);
+#pragma unroll
+        for (int s = 0; s < S; ++s) v[s][r] = part[s * mn + m * N + n];
+    }
+    const float bvn = bias ? load_rt(bias, bias_dt, n) : 0.0f;
+    f32x16 acc[1][1];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float sum = v[0][r];
+#pragma unroll
+        for (int s = 1; s < S; ++s) sum += v[s][r];
+        const int64_t m = min(m0 + 32 * wi + 8 * (r / 4) + 4 * h + r % 4, (int64_t)M - 1);
+        acc[0][0][r] = __builtin_ldexpf(sum, xexp ? xexp[m] : 0) + bvn;
+    }
+    lora_tile_epilogue_ranks<DU, SPL_BM, BNT, RC, NT, 1, 1>(L, lds, m0, n0, M, N, 32 * wi, 32 * wj, tid, lane, acc);
+    float* ot = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ot[(32 * wi + 8 * (r / 4) + 4 * h + r % 4) * ORW + 32 * wj + r32] = acc[0][0][r];
+    __syncthreads();
+    const bool vec = ldy % 8 == 0 && (uintptr_t)y % 16 == 0;
+#pragma unroll
+    for (int q = 0; q < SPL_BM * BNT / 8 / NT; ++q) {
+        const int c = tid + NT * q, row = c / (BNT / 8), col = 8 * (c % (BNT / 8));
+        const int64_t m = m0 + row, nc = n0 + col;
+        if (m >= M || nc >= N) continue;
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = ot[row * ORW + col + e];
+        store8_rt(y, y_dt, m * ldy + nc, o, (int)min<int64_t>(8, N - nc), vec);
+    }
+}
+
 template <int T>
 constexpr int stage_values() { return SM<T>::SBLK * SM<T>::QK; }
 
@@ -494,6 +554,29 @@ hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
 #undef QLIN_SP_LAUNCH
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || a.S == 1) return err;
+    if (a.lora.t) {
+        const dim3 lgrid((unsigned)(((a.N + SPL_BN - 1) / SPL_BN) * ((a.M + SPL_BM - 1) / SPL_BM)));
+#define QLIN_SPL_REDUCE(DU, SV)                                                                                      \
+    hipLaunchKernelGGL((gguf_split_lora_reduce_kernel<DU, SV>), lgrid, dim3(SPL_NT), 0, st, a.part, a.M, a.N,       \
+                       a.xexp, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, a.lora)
+#define QLIN_SPL_S(DU)                      \
+    switch (a.S) {                          \
+        case 2: QLIN_SPL_REDUCE(DU, 2); break; \
+        case 3: QLIN_SPL_REDUCE(DU, 3); break; \
+        case 4: QLIN_SPL_REDUCE(DU, 4); break; \
+        case 5: QLIN_SPL_REDUCE(DU, 5); break; \
+        case 6: QLIN_SPL_REDUCE(DU, 6); break; \
+        case 7: QLIN_SPL_REDUCE(DU, 7); break; \
+        case 8: QLIN_SPL_REDUCE(DU, 8); break; \
+        default: return hipErrorInvalidValue; \
+    }
+        if (a.lora.up_dt == DT_F32) QLIN_SPL_S(DT_F32)
+        else if (a.lora.up_dt == DT_F16) QLIN_SPL_S(DT_F16)
+        else QLIN_SPL_S(DT_BF16)
+#undef QLIN_SPL_S
+#undef QLIN_SPL_REDUCE
+        return hipGetLastError();
+    }
     // row blocks in multiples of 8 (N a multiple of 1024): reduce each block on the XCD that wrote it
     const int blocks = (int)((a.N + SP_ROWS - 1) / SP_ROWS);
     const int xcd_blocks = (a.N % SP_ROWS == 0 && blocks % 8 == 0) ? blocks : 0;
@@ -519,7 +602,7 @@ hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
 
 }  // namespace
 
-int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes) {
+int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes, int min_parts) {
     if (M < 1 || N < 1) return 0;
     int parts = 0;
     gguf::dispatch_type(type, [&]<int T>() {
@@ -529,13 +612,23 @@ int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_byte
         // from 3/4 of the target on, one split: the partials and the reduction cost more than the
         // idle quarter (K = N = 4096, M = 384, 192 tiles: 2 splits 42-58 us, one split ~37-52)
         const int64_t s = tiles * 4 >= SP_TARGET_BLOCKS * 3 ? 1 : (SP_TARGET_BLOCKS + tiles - 1) / tiles;
-        parts = (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(s, stages), SP_MAX_SPLITS));
+        parts = (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(std::max<int64_t>(s, min_parts), stages),
+                                                           SP_MAX_SPLITS));
     });
     return parts;
 }
 
+bool gguf_split_fuses_lora(const GgufSplitArgs& a) {
+    const LoraTile& L = a.lora;
+    const int es = L.up_dt == DT_F32 ? 4 : 2;
+    return a.M > 16 && a.S > 1 && !a.res.r && L.up && L.R >= 8 && L.R % 8 == 0 && L.R <= 128 &&
+           (uintptr_t)L.up % 16 == 0 && (L.ld_up * es) % 16 == 0 &&
+           (L.up_dt == DT_BF16 || L.up_dt == DT_F16 || L.up_dt == DT_F32);
+}
+
 hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st) {
     if (a.y_dtype != DT_F32 && a.y_dtype != DT_F16 && a.y_dtype != DT_BF16) return hipErrorInvalidValue;
+    if (a.lora.t && (!gguf_split_fuses_lora(a) || (uintptr_t)a.lora.t % 16)) return hipErrorInvalidValue;
     if (a.S < 1 || a.S > SP_MAX_SPLITS || (a.S > 1 && !a.part) || (a.ldx % 8) || ((uintptr_t)a.x % 16)) return hipErrorInvalidValue;
     hipError_t err = hipErrorInvalidValue;
     bool ok = gguf::dispatch_type(a.type, [&]<int T>() {

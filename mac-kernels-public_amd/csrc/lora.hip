@@ -100,13 +100,151 @@ __global__ __launch_bounds__(256) void lora_down_kernel(LoraArgs a) {
     }
 }
 
+// The same partials for ranks up to 128 with both operands staged in LDS: one workgroup per 32 rows
+// and all ranks (R <= 32 NH, NH in {1, 2, 4}) over split blockIdx.z's k-tiles of LD_KT values.  The
+// tiles arrive by LDS DMA through a ring of LD_STAGES, every row as whole 16-byte chunks (64 lanes of
+// an instruction cover 1 KiB of consecutive row bytes: a few cache lines, against 32 rows touched by
+// each fragment load of lora_down_kernel), chunk c of row r stored at c ^ (r % chunks per row) so
+// the 32 rows of a fragment read spread over the banks.  Wave w takes rank block w % NH and k part
+// w / NH of each tile's 16-value steps; the 4 / NH parts are added through LDS in order at the end.
+// Rows past M repeat row M - 1 and ranks past R repeat rank R - 1; neither is stored.
+constexpr int LD_KT = 64;
+template <int DX, int DD, int NH>
+constexpr int lora_lds_stages() {
+    constexpr int bytes = 32 * LD_KT * (DX == DT_F32 ? 4 : 2) + 32 * NH * LD_KT * (DD == DT_F32 ? 4 : 2);
+    return bytes <= 24 * 1024 ? 4 : 3;
+}
+template <int DX, int DD, int NH>
+__global__ __launch_bounds__(256) void lora_down_lds_kernel(LoraArgs a) {
+    constexpr int EX = DX == DT_F32 ? 4 : 2, ED = DD == DT_F32 ? 4 : 2;
+    constexpr int CX = LD_KT * EX / 16, CD = LD_KT * ED / 16;           // 16-byte chunks per row
+    constexpr int XSZ = 32 * LD_KT * EX, DSZ = 32 * NH * LD_KT * ED;     // bytes per stage
+    constexpr int NXI = XSZ / 1024, NDI = DSZ / 1024;                    // 1 KiB DMA instructions per stage
+    constexpr int NI = (NXI + NDI) / 4, KQ = 4 / NH, SPP = LD_KT / 16 / KQ;
+    constexpr int STAGES = lora_lds_stages<DX, DD, NH>();
+    static_assert((NXI + NDI) % 4 == 0 && NI <= 16 && (STAGES - 2) * NI < 64, "DMA rounds");
+    static_assert(KQ * NH == 4 && SPP >= 1, "wave split");
+    constexpr int RW = 33;                                               // reduction row stride (floats)
+    static_assert(KQ * NH * 32 * RW * 4 <= STAGES * (XSZ + DSZ), "reduction buffer must fit");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (XSZ + DSZ)];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, h = lane >> 5, rb = wave % NH, kq = wave / NH;
+    const int64_t m0 = (int64_t)blockIdx.y * 32, sp = blockIdx.z;
+    const int64_t tiles = a.K / LD_KT, t0 = tiles * sp / a.S, t1 = tiles * (sp + 1) / a.S;
+    // DMA instruction i of this wave is instruction g = wave + 4 i of the stage: x (g < NXI) or down
+    const uint8_t* src[NI];
+    int dst[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int g = wave + 4 * i;
+        if (g < NXI) {
+            const int u = 64 * g + lane, row = u / CX, c = (u % CX) ^ (row % CX);
+            src[i] = reinterpret_cast<const uint8_t*>(a.x) + (min(m0 + row, a.M - 1) * a.ldx) * EX + 16 * c;
+            dst[i] = 1024 * g;
+        } else {
+            const int u = 64 * (g - NXI) + lane, row = u / CD, c = (u % CD) ^ (row % CD);
+            src[i] = reinterpret_cast<const uint8_t*>(a.down) + (min<int64_t>(row, a.R - 1) * a.ld_down) * ED + 16 * c;
+            dst[i] = XSZ + 1024 * (g - NXI);
+        }
+    }
+    auto dma = [&](int64_t kt, int buf) {
+        const int64_t k0 = min(kt, t1 - 1) * LD_KT;  // past the split: re-reads its last tile
+#pragma unroll
+        for (int i = 0; i < NI; ++i) lds_dma16(src[i] + k0 * (dst[i] < XSZ ? EX : ED), smem + buf * (XSZ + DSZ) + dst[i]);
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    // fragment of step s: row r32 (x) or 32 rb + r32 (down), values 16 s + 8 h .. + 7
+    auto frag_x = [&](const uint8_t* st, int s) {
+        Raw8<DX> r;
+        const uint8_t* row = st + r32 * (LD_KT * EX);
+        if constexpr (DX == DT_F32) {
+            r.v[0] = *reinterpret_cast<const u32x4*>(row + 16 * ((4 * s + 2 * h) ^ (r32 % CX)));
+            r.v[1] = *reinterpret_cast<const u32x4*>(row + 16 * ((4 * s + 2 * h + 1) ^ (r32 % CX)));
+        } else {
+            r.v[0] = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * s + h) ^ (r32 % CX)));
+        }
+        return r;
+    };
+    auto frag_d = [&](const uint8_t* st, int s) {
+        Raw8<DD> r;
+        const int rr = 32 * rb + r32;
+        const uint8_t* row = st + XSZ + rr * (LD_KT * ED);
+        if constexpr (DD == DT_F32) {
+            r.v[0] = *reinterpret_cast<const u32x4*>(row + 16 * ((4 * s + 2 * h) ^ (rr % CD)));
+            r.v[1] = *reinterpret_cast<const u32x4*>(row + 16 * ((4 * s + 2 * h + 1) ^ (rr % CD)));
+        } else {
+            r.v[0] = *reinterpret_cast<const u32x4*>(row + 16 * ((2 * s + h) ^ (rr % CD)));
+        }
+        return r;
+    };
+    // Barrier without a memory fence: each wave's wait covers its own DMAs, the loop writes LDS only
+    // by DMA, and the fragment reads of a buffer complete before the barrier after which it is refilled.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) dma(t0 + s, s);
+    wait_vmcnt<(STAGES - 2) * NI>();
+    __builtin_amdgcn_s_barrier();
+    for (int64_t kt = t0; kt < t1; ++kt) {
+        dma(kt + STAGES - 1, (int)((kt - t0 + STAGES - 1) % STAGES));
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* st = smem + ((kt - t0) % STAGES) * (XSZ + DSZ);
+        Raw8<DX> xr[SPP];
+        Raw8<DD> dr[SPP];
+#pragma unroll
+        for (int j = 0; j < SPP; ++j) {
+            xr[j] = frag_x(st, kq * SPP + j);
+            dr[j] = frag_d(st, kq * SPP + j);
+        }
+#pragma unroll
+        for (int j = 0; j < SPP; ++j) mfma_raw<DX, DD>(xr[j], dr[j], acc);
+        wait_lgkmcnt0();
+        wait_vmcnt<(STAGES - 2) * NI>();
+        __builtin_amdgcn_s_barrier();
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    // C layout: lane l, register e holds row 8 (e / 4) + 4 (l / 32) + e % 4, rank 32 rb + l % 32
+    float* red = reinterpret_cast<float*>(smem);
+    if constexpr (KQ > 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[((kq * NH + rb) * 32 + 8 * (e / 4) + 4 * h + e % 4) * RW + r32] = acc[e];
+        __syncthreads();
+        if (kq == 0) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float v = acc[e];
+#pragma unroll
+                for (int q = 1; q < KQ; ++q) v += red[((q * NH + rb) * 32 + 8 * (e / 4) + 4 * h + e % 4) * RW + r32];
+                acc[e] = v;
+            }
+        }
+    }
+    if (kq == 0) {
+        const int64_t q = 32 * rb + r32;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t m = m0 + 8 * (e / 4) + 4 * h + e % 4;
+            if (m < a.M && q < a.R) a.t[(sp * a.M + m) * a.R + q] = acc[e];
+        }
+    }
+}
+
 // t[i] = sum over s, in split order, of partial s (for S > 1), written after the partials.
+// Partials go in groups of 8 whose loads are all issued before the first add (a group past S
+// re-reads partial S - 1 and drops it), so the latency is paid once per 8 partials.
 __global__ __launch_bounds__(256) void lora_sum_kernel(const float* __restrict__ part, int S, int64_t n,
                                                        float* __restrict__ t) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    float v = part[i];
-    for (int sp = 1; sp < S; ++sp) v += part[sp * n + i];
+    float v = 0.f;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = part[min(s0 + j, S - 1) * n + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v = s0 + j == 0 ? p[j] : (s0 + j < S ? v + p[j] : v);
+    }
     t[i] = v;
 }
 
@@ -284,14 +422,21 @@ __global__ __launch_bounds__(256) void lora_up_kernel(LoraArgs a) {
 
 hipError_t run_lora_t(const LoraArgs& a, hipStream_t st, const float** t_final) {
     if (a.R < 1 || !a.t) return hipErrorInvalidValue;
-    if (a.S < 1 || a.S > 8) return hipErrorInvalidValue;
+    if (a.S < 1 || a.S > LORA_MAX_SPLITS) return hipErrorInvalidValue;
     const int nh = a.R <= 32 ? 1 : 2;  // rank halves per workgroup
     const dim3 dgrid((unsigned)((a.R + 32 * nh - 1) / (32 * nh)), (unsigned)((a.M + 31) / 32), (unsigned)a.S);
     bool ok = false;
     const bool vd = a.vec_x && a.vec_down;
+    // ranks to 128 with rows of whole 64-value tiles: the LDS-staged kernel, every rank in one workgroup
+    const bool lds = vd && a.R <= 128 && a.K % LD_KT == 0 && a.K / LD_KT >= a.S;
+    const int nl = a.R <= 32 ? 1 : a.R <= 64 ? 2 : 4;
+    const dim3 lgrid(1u, (unsigned)((a.M + 31) / 32), (unsigned)a.S);
     auto down = [&]<int DX, int DD>() {
         if (a.x_dt == DX && a.down_dt == DD) {
-            if (vd && nh == 1) hipLaunchKernelGGL((lora_down_kernel<DX, DD, true, 1>), dgrid, dim3(256), 0, st, a);
+            if (lds && nl == 1) hipLaunchKernelGGL((lora_down_lds_kernel<DX, DD, 1>), lgrid, dim3(256), 0, st, a);
+            else if (lds && nl == 2) hipLaunchKernelGGL((lora_down_lds_kernel<DX, DD, 2>), lgrid, dim3(256), 0, st, a);
+            else if (lds) hipLaunchKernelGGL((lora_down_lds_kernel<DX, DD, 4>), lgrid, dim3(256), 0, st, a);
+            else if (vd && nh == 1) hipLaunchKernelGGL((lora_down_kernel<DX, DD, true, 1>), dgrid, dim3(256), 0, st, a);
             else if (vd) hipLaunchKernelGGL((lora_down_kernel<DX, DD, true, 2>), dgrid, dim3(256), 0, st, a);
             else if (nh == 1) hipLaunchKernelGGL((lora_down_kernel<DX, DD, false, 1>), dgrid, dim3(256), 0, st, a);
             else hipLaunchKernelGGL((lora_down_kernel<DX, DD, false, 2>), dgrid, dim3(256), 0, st, a);
@@ -309,14 +454,15 @@ hipError_t run_lora_t(const LoraArgs& a, hipStream_t st, const float** t_final) 
     if (!ok) return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    *t_final = a.t;  // one t: the partials' sum when K was split
+    const float* fin = a.t;  // one t: the partials' sum when K was split
     if (a.S > 1) {
         const int64_t n = a.M * a.R;
         float* sum = a.t + (int64_t)a.S * n;
         hipLaunchKernelGGL(lora_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.t, a.S, n, sum);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        *t_final = sum;
+        fin = sum;
     }
+    if (t_final) *t_final = fin;
     return hipSuccess;
 }
 
@@ -342,13 +488,14 @@ hipError_t run_lora(const LoraArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// As many splits as fit one round of about 3 workgroups per CU (768), at least 256 k-values each.
+// Splits so that the 32-row tiles make about 512 workgroups (2 per CU), at least 256 k-values each,
+// at most LORA_MAX_SPLITS: a few rows (a decode step) still spread their K over the GPU.
 int lora_splits(int64_t M, int64_t K, int64_t R) {
-    const int64_t nh = R <= 32 ? 1 : 2;
-    const int64_t tiles = ((M + 31) / 32) * ((R + 32 * nh - 1) / (32 * nh));
-    int64_t s = 768 / std::max<int64_t>(tiles, 1);
+    (void)R;
+    const int64_t tiles = (M + 31) / 32;
+    int64_t s = (512 + tiles - 1) / std::max<int64_t>(tiles, 1);
     s = std::min<int64_t>(s, std::max<int64_t>(K / 256, 1));
-    return (int)std::max<int64_t>(1, std::min<int64_t>(s, 8));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(s, LORA_MAX_SPLITS));
 }
 
 }  // namespace qlin

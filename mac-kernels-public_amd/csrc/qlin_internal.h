@@ -64,6 +64,19 @@ struct ResidualTile {
     int rs_dt = DT_F16;
 };
 
+// LoRA term added by a GEMM epilogue to its own output tile: y = dtype(base + scale * t up^T), t the
+// fp32 low-rank activation [M, R] (row stride R), up [N, R] (f32 / f16 / bf16, row stride ld_up).
+// t == nullptr: no LoRA term.
+struct LoraTile {
+    const float* t = nullptr;
+    const void* up = nullptr;
+    int up_dt = DT_BF16;
+    int64_t ld_up = 0;
+    int64_t R = 0;
+    float scale = 1.0f;
+    int64_t ld_t = 0;                // row stride of t (0: R)
+};
+
 struct GgufSplitArgs {
     int type = 0;
     const f16* x = nullptr;          // fp16 activations, 16-byte aligned, ldx % 8 == 0
@@ -76,6 +89,7 @@ struct GgufSplitArgs {
     int S = 1;                       // K splits (gguf_split_parts)
     float* part = nullptr;           // S > 1: fp32 partials [S][M][N]
     ResidualTile res;                // y = r + rs * (linear + bias), in the kernel that writes y
+    LoraTile lora;                   // + scale * t up^T in the reduction (gguf_split_fuses_lora)
     const void* bias = nullptr;
     int bias_dtype = DT_NONE;
     void* y = nullptr;
@@ -83,7 +97,10 @@ struct GgufSplitArgs {
     int64_t ldy = 0;
 };
 // Number of K splits this path uses for the shape, 0 when it does not take it.
-int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes);
+int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_bytes, int min_parts = 1);
+// The reduction carries a LoRA term (lora.t, 16-byte aligned): more than 16 rows (32 x 32 tiles),
+// S > 1, no residual, rank a multiple of 8 up to 128, 16-byte aligned up rows.
+bool gguf_split_fuses_lora(const GgufSplitArgs& a);
 hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st);
 
 // ---- GGUF single-row linear (gguf_gemv.hip) ----
@@ -138,19 +155,6 @@ hipError_t run_gguf_gemv(const GgufGemvArgs& a, hipStream_t st);
 
 // ---- weight-only fp16 MFMA tile GEMM (gemm_f16.hip) ----
 enum { WO_INT8 = 0, WO_GGUF = 1, WO_F16 = 2 };  // WO_F16: fp16 weights w[n] 2^-e[n] (a decoded GGUF tensor)
-// LoRA term added by a GEMM epilogue to its own output tile: y = dtype(base + scale * t up^T), t the
-// fp32 low-rank activation [M, R] (row stride R), up [N, R] (f32 / f16 / bf16, row stride ld_up).
-// t == nullptr: no LoRA term.
-struct LoraTile {
-    const float* t = nullptr;
-    const void* up = nullptr;
-    int up_dt = DT_BF16;
-    int64_t ld_up = 0;
-    int64_t R = 0;
-    float scale = 1.0f;
-    int64_t ld_t = 0;                // row stride of t (0: R)
-};
-
 // Residual scales of the 8 columns nc .. nc + 7 (1 where rs is absent), as raw bits to convert at use.
 __device__ __forceinline__ void residual_scale_bits8(const ResidualTile& R, int64_t nc, int64_t N, uint32_t (&b)[8]) {
 #pragma unroll
@@ -366,6 +370,7 @@ hipError_t run_bwd_rows(const void* dy, int dy_dt, int64_t ldd, int64_t M, int64
                         int64_t s_stride, f16* a, int64_t lda, int32_t* e, hipStream_t st);
 hipError_t run_bwd_gemm(const BwdGemmArgs& p, hipStream_t st);
 // K splits of the LoRA down-projection for this shape (the workspace holds that many partials).
+constexpr int LORA_MAX_SPLITS = 32;
 int lora_splits(int64_t M, int64_t K, int64_t R);
 hipError_t run_gemm_i8(const GemmI8Args& a, hipStream_t st);
 

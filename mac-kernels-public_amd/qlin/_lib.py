@@ -22,6 +22,7 @@ DT_F32, DT_F16, DT_BF16, DT_I8, DT_U8, DT_I32, DT_E4M3 = 0, 1, 2, 3, 4, 5, 6
 OP_INT8_LINEAR, OP_W4A8_LINEAR, OP_GGUF_LINEAR, OP_LORA, OP_INT8_GRAD_INPUT, OP_W4A8_GRAD_INPUT = 0, 1, 2, 3, 4, 5
 OP_INT8_LINEAR_LORA, OP_W4A8_LINEAR_LORA = 6, 7
 OP_INT8_LINEAR_RESIDUAL, OP_W4A8_LINEAR_RESIDUAL, OP_GGUF_LINEAR_RESIDUAL = 8, 9, 10
+OP_GGUF_LINEAR_LORA = 11
 
 _TORCH_DT = {
     torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16, torch.int8: DT_I8,
@@ -36,6 +37,7 @@ EXPORTS = (
     "qlin_residual_epilogue", "qlin_int8_linear_lora", "qlin_w4a8_linear_lora",
     "qlin_int8_linear_grad_input", "qlin_w4a8_linear_grad_input",
     "qlin_int8_linear_residual", "qlin_w4a8_linear_residual", "qlin_gguf_linear_residual",
+    "qlin_gguf_linear_lora",
 )
 
 
@@ -74,6 +76,7 @@ def load():
         "qlin_int8_linear_lora": (I, [T, T, T, T, T, I, T, T, ctypes.c_float, P, SZ, P]),
         "qlin_w4a8_linear_lora": (I, [T, T, T, T, T, T, T, I, I, I, T, T, ctypes.c_float, P, SZ, P]),
         "qlin_gguf_linear": (I, [T, P, I, I64, I64, T, T, P, SZ, P]),
+        "qlin_gguf_linear_lora": (I, [T, P, I, I64, I64, T, T, T, T, ctypes.c_float, P, SZ, P]),
         "qlin_int8_linear_residual": (I, [T, T, T, T, T, T, T, I, P, SZ, P]),
         "qlin_w4a8_linear_residual": (I, [T, T, T, T, T, T, T, T, T, I, I, I, P, SZ, P]),
         "qlin_gguf_linear_residual": (I, [T, P, I, I64, I64, T, T, T, T, P, SZ, P]),

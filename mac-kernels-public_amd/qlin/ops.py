@@ -501,6 +501,15 @@ def gguf_linear(x, weight, qtype, shape, bias=None, out_dtype=None, lora_down=No
         return _shaped(y, oshape)
     b = _bias(bias, n)
     stream = _lib.stream_of(x.device)
+    m = x2.shape[0]
+    if m > 16 and lora is not None:
+        def run(down, up, lscale):
+            wsl = _workspace(_lib.OP_GGUF_LINEAR_LORA, m, n, k, tid | down.shape[0] << 8, x2, stream)
+            return _lib.load().qlin_gguf_linear_lora(_lib.desc(x2), weight.data_ptr(), tid, n, k, _lib.desc(b),
+                                                     _lib.desc(y), _lib.desc(down), _lib.desc(up), lscale,
+                                                     wsl.data_ptr(), wsl.numel(), stream)
+        if _fused_lora(op, lora, res, x2, run):
+            return _shaped(y, oshape)
     if res is not None and lora is None:  # the residual joins the linear's epilogue (or its own kernel)
         r, rs = res
         _check_device(op, r, rs)

@@ -314,6 +314,57 @@ def test_w4a8_lora_fused_into_gemm(bits, m, n, r, fdt, fused_calls):
     check_side(y, base, side_ref(x.cpu(), down, up, 1.5), f"w{bits}a8 fused m={m} r={r}")
 
 
+@pytest.mark.parametrize("name,m,n,k,r,fdt", [
+    ("Q4_K", 64, 4096, 4096, 64, torch.bfloat16),  # the decode shape: 32 row blocks x 8 splits
+    ("Q6_K", 40, 1000, 2048, 128, torch.float16),  # ragged N, rank 128 in two passes
+    ("Q8_0", 200, 4096, 1024, 32, torch.float32),  # four m-tiles (the last 8 rows), 2 splits, fp32 up
+    ("Q4_0", 512, 4096, 1024, 16, torch.bfloat16), # 256 tiles: one split without the LoRA, two with it
+    ("IQ4_XS", 17, 520, 512, 8, torch.bfloat16),   # one m-tile of 17 rows, a ragged column block
+    ("Q2_K", 100, 136, 1024, 24, torch.bfloat16),  # 16-value units, 2 m-tiles
+])
+def test_gguf_lora_fused_into_split(name, m, n, k, r, fdt, fused_calls):
+    """GGUF calls from 17 rows to the split kernel's limit: the K-split reduction adds the LoRA term
+    to each 64 x 128 output tile before its one rounding (the reference's GGUF LoRA in the epilogue,
+    to rank 128).  Against the separate kernels, the exact side term and the oracle's linear."""
+    Q = qlin()
+    from gguf_blocks import random_gguf_blocks
+    raw = random_gguf_blocks(name, n, k, seed=m + r)
+    rd = torch.from_numpy(raw).to(DEV)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m)) * 0.5).half()
+    b = (torch.randn(n, generator=torch.Generator().manual_seed(3)) * 0.1).half().to(DEV)
+    down, up = factors(n, k, r, fdt, fdt, seed=r)
+    kw = dict(lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.7)
+    base = Q.gguf_linear(x.to(DEV), rd, name, (n, k), b)
+    y = Q.gguf_linear(x.to(DEV), rd, name, (n, k), b, **kw)
+    plain = Q.gguf_linear(x.to(DEV), rd, name, (n, k), b, residual=torch.zeros(m, n, dtype=y.dtype, device=DEV), **kw)
+    torch.cuda.synchronize()
+    assert fused_calls == [True, False]
+    _close_or_equal(y, plain, f"{name} m={m} r={r}")
+    ref = side_ref(x, down, up, 0.7)
+    check_side(y, base, ref, f"{name} fused m={m} r={r}")
+    want = O.linear_ref(x.float().numpy(), O.gguf_dequantize(raw, name, (n, k)), b.double().cpu().numpy()) + ref
+    check_full(y, want, f"{name} fused full m={m} r={r}")
+
+
+@pytest.mark.parametrize("name,m,r", [("Q4_K", 16, 16), ("Q4_K", 600, 16), ("Q4_K", 64, 136), ("Q6_K", 300, 16),
+                                      ("Q4_K", 64, 12)])
+def test_gguf_lora_declines_to_the_separate_kernels(name, m, r, fused_calls):
+    """16 rows or fewer (the GEMV and small-M kernels), past the split kernel's rows (Q4_K 512, Q6_K
+    256: the GEMM over the decoded weight), rank above 128 or not a multiple of 8: the fused entry
+    point declines before launching and the separate kernels give the result."""
+    Q = qlin()
+    from gguf_blocks import random_gguf_blocks
+    n, k = 256, 1024
+    rd = torch.from_numpy(random_gguf_blocks(name, n, k, seed=9)).to(DEV)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(10)).half()
+    down, up = factors(n, k, r, torch.bfloat16, torch.bfloat16, seed=11)
+    base = Q.gguf_linear(x.to(DEV), rd, name, (n, k))
+    y = Q.gguf_linear(x.to(DEV), rd, name, (n, k), lora_down=down.to(DEV), lora_up=up.to(DEV), lora_scale=0.5)
+    torch.cuda.synchronize()
+    assert fused_calls == ([] if m <= 16 else [False])
+    check_side(y, base, side_ref(x, down, up, 0.5), f"{name} m={m} r={r}")
+
+
 @pytest.mark.parametrize("r,fdt", [(12, torch.bfloat16), (136, torch.bfloat16), (72, torch.float32)])
 def test_lora_fused_declines_to_the_separate_kernels(r, fdt, fused_calls):
     """Ranks the GEMM epilogue does not take at a fused shape (not a multiple of 8; above 128; fp32 up
