@@ -706,23 +706,35 @@ constexpr int i8dma_lora_rank(int du) {
     return du == DT_F32 ? i8dma_lora_rank_t<DT_F32>() : i8dma_lora_rank_t<DT_BF16>();
 }
 
-template <int BMT, int BNT, int BK, int STAGES, bool L2PF, int LDU = -1>
-__global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int8_t* __restrict__ w8) {
-    constexpr int NT = 512;
-    constexpr int WM = BMT / 4, WN = BNT / 2, TI = WM / 32, TJ = WN / 32;
-    static_assert(TI >= 1 && TJ >= 1 && (BK == 64 || BK == 128), "tile shape");
+// WVM x WVN waves (default 4 x 2) of (BMT / WVM) x (BNT / WVN).  With other wave grids (2 x 5 for
+// 128 x 160 tiles: M1024 N5120 makes 256 of them, one round on 256 CUs, where 128 x 256 tiles leave
+// 96 CUs idle) the DMA instructions of a k-tile do not split evenly over the waves: instruction j
+// (1 KiB of one operand) is issued by wave j % waves, and two stages without the prefetch wait for
+// all of a wave's copies, whatever their count.
+template <int WVM, int WVN>
+constexpr int i8dma_threads() { return 64 * WVM * WVN; }
+template <int BMT, int BNT, int BK, int STAGES, bool L2PF, int LDU = -1, int WVM = 4, int WVN = 2>
+__global__ __launch_bounds__(64 * WVM * WVN) void gemm_i8dma_kernel(GemmI8Args p, const int8_t* __restrict__ w8) {
+    constexpr int NT = i8dma_threads<WVM, WVN>(), NW = WVM * WVN;
+    constexpr int WM = BMT / WVM, WN = BNT / WVN, TI = WM / 32, TJ = WN / 32;
+    static_assert(TI >= 1 && TJ >= 1 && WM % 32 == 0 && WN % 32 == 0 && (BK == 64 || BK == 128), "tile shape");
     constexpr int CPRW = BK / 16;                   // 16-byte chunks per row
     constexpr int RPS = 16 / CPRW;                  // rows per swizzle step
     constexpr int ASZ = BMT * BK, BSZ = BNT * BK;   // bytes per buffer
-    constexpr int NA = ASZ / 16 / NT, NB = BSZ / 16 / NT;  // DMA instructions per thread and k-tile
-    static_assert(NA * 16 * NT == ASZ && NB * 16 * NT == BSZ, "tile must split into whole DMA rounds");
+    constexpr bool EVEN = NT == 512;                // every wave issues the same DMAs (the 4 x 2 grid)
+    constexpr int NIA = ASZ / 1024, NIB = BSZ / 1024, NIT = NIA + NIB;  // 1 KiB DMA instructions per k-tile
+    constexpr int NA = EVEN ? ASZ / 16 / NT : 0, NB = EVEN ? BSZ / 16 / NT : 0;  // per thread and k-tile
+    constexpr int NIW = EVEN ? 1 : (NIT + NW - 1) / NW;  // uneven grids: instructions per wave (at most)
+    static_assert(!EVEN || (NA * 16 * NT == ASZ && NB * 16 * NT == BSZ), "tile must split into whole DMA rounds");
+    static_assert(EVEN || (ASZ % 1024 == 0 && BSZ % 1024 == 0 && STAGES == 2 && !L2PF && LDU < 0),
+                  "uneven wave grids: whole 1 KiB instructions, two stages, no prefetch, no LoRA");
     // operand buffers, then (L2PF) a 4-byte-per-thread sink for the prefetch DMAs; one LDS object,
     // so that the compiler's alias tracking does not make fragment reads wait for the prefetches
     constexpr int SINK = L2PF ? NT * 4 : 0;
     __shared__ __attribute__((aligned(16))) uint8_t smem[STAGES * (ASZ + BSZ) + SINK];
     uint8_t (*buf_of)[ASZ + BSZ] = reinterpret_cast<uint8_t (*)[ASZ + BSZ]>(smem);  // [buffer][A | B]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WVN, wn = wave % WVN;
     const int r32 = lane & 31, h = lane >> 5;
     int mt, nt;
     xcd_tile(blockIdx.x, (int)gridDim.x, (int)((p.M + BMT - 1) / BMT), (int)((p.N + BNT - 1) / BNT), mt, nt);
@@ -734,20 +746,37 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     // (lane % CPRW) ^ ((row / RPS) % CPRW) -- the same for every i.  Rows past M (N) re-read row
     // M - 1 (N - 1) and are never stored.
     const int c_l = (lane % CPRW) ^ (((64 * wave + lane) / CPRW / RPS) % CPRW);
-    const int8_t* asrc[NA];
-    const int8_t* bsrc[NB];
+    const int8_t* asrc[NA > 0 ? NA : 1];
+    const int8_t* bsrc[NB > 0 ? NB : 1];
 #pragma unroll
     for (int i = 0; i < NA; ++i)
         asrc[i] = p.xq + min(m0 + (512 * i + 64 * wave + lane) / CPRW, p.M - 1) * p.ldx + 16 * c_l;
 #pragma unroll
     for (int i = 0; i < NB; ++i)
         bsrc[i] = w8 + min(n0 + (512 * i + 64 * wave + lane) / CPRW, p.N - 1) * p.K + 16 * c_l;
+    // uneven grids: instruction j = wave + NW i fills chunks u = 64 j' + lane of its operand (j' its
+    // index there), row u / CPRW, physical chunk u % CPRW holding logical chunk u % CPRW ^ swizzle
+    const int8_t* usrc[NIW];
+    int udst[NIW];
+#pragma unroll
+    for (int i = 0; i < NIW; ++i) {
+        const int j = min(wave + NW * i, NIT - 1), ja = j < NIA ? j : j - NIA;
+        const int u = 64 * ja + lane, row = u / CPRW, c = (u % CPRW) ^ ((row / RPS) % CPRW);
+        usrc[i] = j < NIA ? p.xq + min(m0 + row, p.M - 1) * p.ldx + 16 * c : w8 + min(n0 + row, p.N - 1) * p.K + 16 * c;
+        udst[i] = j < NIA ? 1024 * ja : ASZ + 1024 * ja;
+    }
     auto dma = [&](int kt, int buf) {
         const int k0 = min(kt, ktiles - 1) * BK;
+        if constexpr (EVEN) {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) lds_dma16(asrc[i] + k0, &buf_of[buf][16 * (512 * i + 64 * wave)]);
+            for (int i = 0; i < NA; ++i) lds_dma16(asrc[i] + k0, &buf_of[buf][16 * (512 * i + 64 * wave)]);
 #pragma unroll
-        for (int i = 0; i < NB; ++i) lds_dma16(bsrc[i] + k0, &buf_of[buf][ASZ + 16 * (512 * i + 64 * wave)]);
+            for (int i = 0; i < NB; ++i) lds_dma16(bsrc[i] + k0, &buf_of[buf][ASZ + 16 * (512 * i + 64 * wave)]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NIW; ++i)
+                if (wave + NW * i < NIT) lds_dma16(usrc[i] + k0, &buf_of[buf][udst[i]]);
+        }
     };
     // L2 prefetch: half line u = tid + NT i of a k-tile is row u / HPR (A rows, then B rows), half
     // u % HPR; rows past M (N) touch row M - 1 (N - 1)
@@ -808,7 +837,7 @@ __global__ __launch_bounds__(512) void gemm_i8dma_kernel(GemmI8Args p, const int
     // Barrier without a memory fence: the DMA data this wave needs is covered by wait_vmcnt, and
     // the loop writes LDS only by DMA.  Each step issues its tile DMA, then the prefetch of the
     // tile after it; a step may leave the prefetch and the DMAs of later tiles in flight.
-    constexpr int ND = NA + NB;  // DMA instructions per k-tile and thread
+    constexpr int ND = NA + NB;  // DMA instructions per k-tile and thread (uneven grids: STAGES = 2, no wait count)
     constexpr int INFLIGHT = PFN + (STAGES - 2) * (ND + PFN);
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st) {
@@ -1118,6 +1147,13 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         if (ldu != -1 && ldu != DT_BF16 && ldu != DT_F16 && ldu != DT_F32) return hipErrorInvalidValue;
         if (tiles(256, 256) >= 192)
             go.template operator()<256, 256>();
+        // 128 x 160 tiles (2 x 5 waves, no LoRA term) when they make one round of at least 3/4 of
+        // the 256 CUs and 256 x 256 tiles would not fill the GPU (M1024 N5120: 256 of them)
+        else if (ldu == -1 && tiles(128, 160) >= 192 && tiles(128, 160) <= 256) {
+            const dim3 grid((unsigned)tiles(128, 160));
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 160, 128, 2, false, -1, 2, 5>), grid,
+                               dim3(i8dma_threads<2, 5>()), 0, st, p, p.w8);
+        }
         // 128 x 256 also when it fits one round on the 256 CUs and 128 x 128 would not: one round of
         // the larger tile beats 1.25 rounds of the smaller (M1024 K13824 N5120: 150.6 vs 157.1 us)
         else if (tiles(128, 256) >= 192 || (tiles(128, 256) <= 256 && tiles(128, 128) > 256))

@@ -172,7 +172,8 @@ def test_int8_residual_fused_equals_separate(m, n, k, odt, rdt):
 
 
 @pytest.mark.parametrize("m,n,k,bits,gs", [
-    (1024, 4096, 1024, 4, 64),   # grid decoded once, then the int8 DMA GEMM
+    (1024, 4096, 1024, 4, 64),   # grid decoded once, then the int8 DMA GEMM (128 x 256 tiles)
+    (1000, 5100, 1024, 6, 64),   # the same with 2 x 5 waves on 128 x 160 tiles (256 of them)
     (300, 24600, 1024, 6, 64),   # one 256-row tile over a wide grid: the fused-decode GEMM
     (100, 1000, 1024, 4, 16),    # group 16: the 128 x 128 decode-in-load kernel, residual kernel after
     (8, 512, 1024, 6, 64),       # small M

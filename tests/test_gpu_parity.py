@@ -654,7 +654,8 @@ A8_TILE_CASES = [
     (6, None, torch.float8_e4m3fn, 64, 256, 2047, 6136),
     # the same GEMM with 128 x 256 tiles (6 x 20 tiles of 256 x 256 would not fill the GPU) and 128 x 128
     (6, "auto", torch.float16, 64, 128, 1300, 5000),
-    (6, None, torch.float16, 64, 256, 1024, 4200),  # 136 tiles of 128 x 256 (one round), not 264 of 128 x 128
+    (6, None, torch.float16, 64, 256, 1024, 4200),  # 216 tiles of 128 x 160 (2 x 5 waves, one round)
+    (4, None, torch.float16, 64, 1024, 1000, 5100), # 256 tiles of 128 x 160, ragged M and N, 8 k-tiles
     (4, None, torch.float8_e4m3fn, 128, 256, 1024, 2000),
     # M < 512 with >= 192 tiles of 256 x 256: the fused-decode kernel, one scale table per thread
     # pair (group 128) and per thread (group 64)
