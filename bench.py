@@ -358,7 +358,7 @@ CONFIG_KERNELS = {
     "w6a8_m9504_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m9504_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "dit_layer_int8_convrot_m4608": "4x (prologue_kernel+gemm_wo_dma_kernel<256,3>)",
-    "gguf_q4_k_m512_k4096_n4096": "prologue_kernel+gguf_split_kernel<Q4_K,MT=2,32x32>",
+    "gguf_q4_k_m512_k4096_n4096": "gguf_split_kernel<Q4_K,MT=2,32x32> (8 m-tiles, one split)",
 }
 
 
