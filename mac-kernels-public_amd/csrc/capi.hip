@@ -378,7 +378,7 @@ qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x
         case QLIN_OP_INT8_LINEAR:
             if (!valid_group(param)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", param);
             if (param && K % param) return fail(QLIN_EUNSUPPORTED, "K %% group != 0");
-            if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
+            if (K > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
             return QLIN_OK;
         case QLIN_OP_W4A8_LINEAR:
             if (param != 4 && param != 6) return fail(QLIN_EUNSUPPORTED, "bits %d unsupported", param);
@@ -390,7 +390,7 @@ qlin_status qlin_query(int op, int64_t M, int64_t N, int64_t K, int param, int x
             if (!gguf::type_info(param, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", param);
             if (K % qk) return fail(QLIN_EUNSUPPORTED, "K %% block != 0 (rows straddle blocks)");
             if (K % 32) return fail(QLIN_EUNSUPPORTED, "K %% 32 != 0");
-            if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
+            if (K > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
             return QLIN_OK;
         }
     }
@@ -595,7 +595,7 @@ static qlin_status int8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     if (!valid_group(convrot_groupsize)) return fail(QLIN_EUNSUPPORTED, "ConvRot group %d unsupported", convrot_groupsize);
     if (convrot_groupsize && K % convrot_groupsize)
         return fail(QLIN_EINVAL, "K=%lld is not a multiple of the ConvRot group %d", (long long)K, convrot_groupsize);
-    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
+    if (K > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
     int64_t sst;
     if ((s = as_vector(scale, "scale", N, true, sst))) return s;
     if (!is_float(scale->dtype)) return fail(QLIN_EUNSUPPORTED, "scale dtype %d unsupported", scale->dtype);
@@ -765,7 +765,7 @@ static qlin_status gguf_linear_impl(const qlin_tensor* x, const void* weight, in
     if (!weight) return fail(QLIN_EINVAL, "weight is missing");
     if (K % qk) return fail(QLIN_EUNSUPPORTED, "K=%lld is not a whole number of %d-value blocks", (long long)K, qk);
     if (K % 32) return fail(QLIN_EUNSUPPORTED, "K %% 32 != 0");
-    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
+    if (K > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
     Mat X, Y;
     qlin_status s = check_xy(x, y, N, K, X, Y);
     if (s) return s;
@@ -884,7 +884,7 @@ qlin_status qlin_gguf_linear_lora(const qlin_tensor* x, const void* weight, int 
     if (!gguf::type_info(ggml_type, qk, ts)) return fail(QLIN_EUNSUPPORTED, "ggml type %d unsupported", ggml_type);
     if (!weight) return fail(QLIN_EINVAL, "weight is missing");
     if (K % qk) return fail(QLIN_EUNSUPPORTED, "K=%lld is not a whole number of %d-value blocks", (long long)K, qk);
-    if (K > QLIN_MAX_K) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K);
+    if (K > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
     Mat X, Y, D, U;
     qlin_status s = check_xy(x, y, N, K, X, Y);
     if (s) return s;
@@ -1109,7 +1109,7 @@ qlin_status qlin_dequantize_int8(const qlin_tensor* qdata, const qlin_tensor* sc
                                          (float*)O.data, st), "int8 dequantize")))
         return s;
     if (convrot_groupsize) {
-        if (Q.cols > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+        if (Q.cols > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
         PrologueArgs p;
         p.mode = PROLOGUE_ROT_F32; p.x_dtype = DT_F32; p.x = O.data; p.ldx = O.cols;
         p.M = O.rows; p.K = (int)O.cols; p.G = convrot_groupsize; p.fo = (float*)O.data; p.ldo = O.cols;
@@ -1159,7 +1159,7 @@ qlin_status qlin_dequantize_w4a8(const qlin_tensor* qdata, const qlin_tensor* s_
                                          (const float*)s_channel->data, cb, O.data, O.dtype, st), "w4a8 dequantize")))
         return s;
     if (convrot_groupsize) {
-        if (K > 32768) return fail(QLIN_EUNSUPPORTED, "K > 32768");
+        if (K > QLIN_MAX_K_WO) return fail(QLIN_EUNSUPPORTED, "K > %d", QLIN_MAX_K_WO);
         PrologueArgs p;
         p.mode = PROLOGUE_ROT_F32; p.x_dtype = DT_F32; p.x = O.data; p.ldx = K;
         p.M = N; p.K = (int)K; p.G = convrot_groupsize; p.fo = (float*)O.data; p.ldo = K;

@@ -319,7 +319,7 @@ static hipError_t launch_prologue(const PrologueArgs& a, hipStream_t st) {
 
 hipError_t run_prologue(const PrologueArgs& a, hipStream_t st) {
     if (a.M == 0) return hipSuccess;
-    if (a.K > QLIN_MAX_K) return hipErrorInvalidValue;
+    if (a.K > (a.mode == PROLOGUE_A8 ? QLIN_MAX_K : QLIN_MAX_K_WO)) return hipErrorInvalidValue;
     switch (a.mode) {
         case PROLOGUE_WO:
             if (a.x_dtype == DT_F16) return launch_prologue<f16, 0>(a, st);

@@ -107,10 +107,15 @@ hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st);
 // INT8 weight rows as a "format" of the small-M MFMA kernel (not a ggml type id): 32-value units
 // of raw int8 codes, the per-row scale applied in the epilogue.
 constexpr int INT8_ROWS = 1000;
-// Longest contraction the forward linears accept.  The fp16 MFMAs accumulate in fp32 over
-// normalized operands (|x'| <= 1), so range is not the limit; the A8 int32 sums stay exact while
+// Longest contraction of the A8 linear and activation quantizer: the int32 sums stay exact while
 // K * 128 * 127 < 2^31 (K < 132104).
 constexpr int QLIN_MAX_K = 131072;
+// Longest contraction of the weight-only linears (INT8, GGUF) and the rotating dequantizers: the
+// fp16 MFMAs accumulate in fp32 over normalized operands (|x'| <= 1), so range is not the limit
+// (the fp16 GEMM of a dequantizing backend overflows past 65504 terms; this one does not), and the
+// row prologue takes rows of any length in 32768-value chunks.  The bound keeps every index and
+// workspace size well inside 32-bit element counts per row.
+constexpr int QLIN_MAX_K_WO = 1 << 20;
 bool int8_smallm_supported(int64_t M, int64_t K, int64_t ldw, const void* w);
 hipError_t run_int8_smallm(const GgufSmallMArgs& a, hipStream_t st);
 

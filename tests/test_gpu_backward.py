@@ -50,6 +50,8 @@ INT8_CASES = [
     (300, 96, 1024, 256, torch.float16, torch.bfloat16, "f32", 1.0),
     (65, 33, 272, 16, torch.float16, torch.float32, "f32", 3.0),
     (1100, 256, 8192, 256, torch.bfloat16, None, "f32", 1.0),  # 288 workgroups: the two-per-CU kernel
+    (40, 128, 65536, 256, torch.float16, None, "f32", 1.0),    # wide rows: dx of 65536 and 196608 values
+    (8, 64, 196608, 128, torch.bfloat16, torch.float32, "f32", 1.0),
 ]
 
 

@@ -133,3 +133,64 @@ def test_quantize_act_int8_wide_k_bit_exact(dt):
         wq, ws = O.quantize_int8_rowwise(x.numpy())
     assert np.array_equal(q.cpu().numpy(), wq)
     assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), ws.reshape(-1).view(np.uint32))
+
+
+# Past the A8 linear's exact int32 range (K < 132104) the weight-only linears go on: their fp16
+# MFMAs accumulate in fp32 over normalized operands, and the prologue takes any number of chunks.
+
+@pytest.mark.parametrize("m,k,g,xdt", [(1, 196608, 256, torch.float16), (4, 196608, 128, torch.bfloat16),
+                                       (40, 196608, 256, torch.float16), (300, 196608, 0, torch.float32),
+                                       (40, 1 << 20, 256, torch.float16)])
+def test_int8_linear_wider_than_a8(m, k, g, xdt):
+    n = 64
+    gen = torch.Generator().manual_seed(k + m + g)
+    w = (torch.randn(n, k, generator=gen) * 0.002).numpy()  # outputs of order 1 over the long rows
+    q, s = qz().quantize_int8_convrot_weight(w, g) if g else qz().quantize_int8_rowwise(w)
+    s = s.astype(np.float32).reshape(-1)
+    x = (torch.randn(m, k, generator=gen) * 2).to(xdt)
+    y = qlin().int8_linear(x.to(DEV), torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV), None,
+                           torch.float32, convrot=bool(g), convrot_groupsize=g or 256)
+    rows = rows_of(m)
+    xr = x[torch.from_numpy(rows)].float().numpy()
+    if g:
+        xr = O.rotate(xr, g)
+    check(y[torch.from_numpy(rows).to(DEV)], O.linear_ref(xr, O.dequantize_int8(q, s)), f"int8 M={m} K={k} G={g}")
+
+
+@pytest.mark.parametrize("name,m,k", [("Q4_K", 1, 196608), ("Q4_K", 8, 196608), ("Q8_0", 40, 196608),
+                                      ("Q6_K", 100, 196608), ("IQ4_XS", 600, 196608), ("Q4_K", 8, 1 << 20)])
+def test_gguf_linear_wider_than_a8(name, m, k):
+    """One row and 8 rows (the small-M kernel: the GEMV stops at K = 8192), the K split, the
+    m-tiles, and above 512 rows the weight decoded once to fp16 (25 MB here)."""
+    n = 64
+    raw = random_gguf_blocks(name, n, k, seed=m + 11)
+    wdq = O.gguf_dequantize(raw, name, (n, k))
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m)) * 0.25).half()
+    y = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k), out_dtype=torch.float32)
+    rows = rows_of(m)
+    want = O.linear_ref(x[torch.from_numpy(rows)].float().numpy(), wdq)
+    check(y[torch.from_numpy(rows).to(DEV)], want, f"{name} M={m} K={k}")
+
+
+def test_a8_declines_past_its_exact_range():
+    """W4A8 at K = 132096 (its int32 sums could overflow): declined before launching, as a backend
+    that cannot take the call."""
+    n, k, gs = 8, 132096, 64
+    q = torch.zeros(n, k // 2, dtype=torch.uint8, device=DEV)
+    s_rel = torch.ones(n, k // gs, dtype=torch.float16, device=DEV)
+    s_ch = torch.ones(n, device=DEV)
+    x = torch.zeros(2, k, dtype=torch.float16, device=DEV)
+    with pytest.raises(qlin().NoCapableBackendError):
+        qlin().w4a8_int8_linear(x, q, s_rel, s_ch, None, None, None, gs, 256)
+
+
+@pytest.mark.parametrize("k,g", [(65536, 256), (196608, 128)])
+def test_dequantize_int8_convrot_wide(k, g):
+    """The original-basis dequantization of rows longer than 32768 values (the rotation in chunks)."""
+    n = 4
+    w = (torch.randn(n, k, generator=torch.Generator().manual_seed(k)) * 0.02).numpy()
+    q, s = qz().quantize_int8_convrot_weight(w, g)
+    got = qlin().dequantize_int8_convrot_weight(torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV),
+                                                g).cpu().numpy()
+    want = O.dequantize_int8_convrot(q, s.reshape(-1), g)
+    assert np.abs(got.astype(np.float64) - want).max() <= 1e-6 * np.abs(want).max() + 1e-12
