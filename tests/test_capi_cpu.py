@@ -39,10 +39,12 @@ def test_query_and_workspace():
     assert L.qlin_query(_lib.OP_W4A8_LINEAR, 8, 64, 3072, 4, _lib.DT_F16, _lib.DT_BF16) == 0
     assert L.qlin_query(_lib.OP_W4A8_LINEAR, 8, 64, 3072, 5, _lib.DT_F16, _lib.DT_F16) == 1
     assert b"bits" in L.qlin_last_error()
-    # contractions up to 131072 (two-pass prologue past 32768); longer ones decline
-    for op, p in ((_lib.OP_INT8_LINEAR, 128), (_lib.OP_W4A8_LINEAR, 6), (_lib.OP_GGUF_LINEAR, 12)):
-        assert L.qlin_query(op, 8, 64, 131072, p, _lib.DT_F16, _lib.DT_F16) == 0
-        assert L.qlin_query(op, 8, 64, 131072 + 256, p, _lib.DT_F16, _lib.DT_F16) == 1
+    # contractions: A8 up to 131072 (its int32 sums stay exact), the weight-only linears up to 2^20
+    # (chunked prologue past 32768, fp32 accumulation); longer ones decline
+    for op, p, kmax in ((_lib.OP_INT8_LINEAR, 128, 1 << 20), (_lib.OP_W4A8_LINEAR, 6, 131072),
+                        (_lib.OP_GGUF_LINEAR, 12, 1 << 20)):
+        assert L.qlin_query(op, 8, 64, kmax, p, _lib.DT_F16, _lib.DT_F16) == 0
+        assert L.qlin_query(op, 8, 64, kmax + 256, p, _lib.DT_F16, _lib.DT_F16) == 1
     ws = L.qlin_workspace_size(_lib.OP_INT8_LINEAR, 256, 3072, 3072, 128, _lib.DT_F16)
     assert ws >= 256 * 3072 * 2 + 256 * 4
 
