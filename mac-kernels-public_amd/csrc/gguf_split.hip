@@ -92,9 +92,12 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     // No load below branches on the lane: activation rows past M re-read row M - 1, weight rows
     // past N re-read row N - 1 (their results are never stored), and each wave's last weight unit
     // is re-read by the lanes past it.
-    // Stages held in registers ahead of LDS: a workgroup typically owns two 256-value stages, and
-    // both are requested before the first wait.
-    constexpr int PF = (SV == 256) ? 2 : 1;
+    // Stages held in registers ahead of LDS.  One: the next stage's loads go out as soon as the
+    // current one is committed to LDS, before its math.  Two (both of a workgroup's usual stages
+    // requested before the first wait) held 40 more registers and spilled Q8_0's 272-byte stage
+    // rows; one measured faster at K = N = 4096 (same process): Q8_0 M64 15.7 -> 13.6 us, the
+    // 4.5-bit formats at M64 4-5% and at M17 3-6%, within 2% either way at M256.
+    constexpr int PF = 1;
     u32x4 xq[PF][XPT];
     auto issue_x = [&](int st, u32x4* dst) {
         const int64_t k = (int64_t)min(st, last) * SV;
