@@ -352,11 +352,11 @@ CONFIGS = {
 CONFIG_KERNELS = {
     "int8_convrot_m256_k3072_n3072": "prologue_kernel+gemm_wo_dmas_kernel<64,64,256,3>",
     "int8_convrot_m1_k3072_n3072": "int8_gemv_kernel<1,3,2>",
-    "w4a8_m4096_k3072_n12288": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
+    "w4a8_m4096_k3072_n12288": "a8_prepass_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m1024_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
     "w6a8_m1024_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<128,160,2x5 waves>",
-    "w6a8_m9504_k5120_n13824": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
-    "w6a8_m9504_k13824_n5120": "prologue_kernel+a8_grid_kernel+gemm_i8dma_kernel<256,256>",
+    "w6a8_m9504_k5120_n13824": "a8_prepass_kernel+gemm_i8dma_kernel<256,256>",
+    "w6a8_m9504_k13824_n5120": "a8_prepass_kernel+gemm_i8dma_kernel<256,256>",
     "dit_layer_int8_convrot_m4608": "4x (prologue_kernel+gemm_wo_dma_kernel<256,3>)",
     "gguf_q4_k_m512_k4096_n4096": "gguf_split_kernel<Q4_K,MT=2,32x32> (8 m-tiles, one split)",
 }

@@ -1039,7 +1039,12 @@ static qlin_status w4a8_linear_impl(const qlin_tensor* x, const qlin_tensor* qda
     p.qo = qo;
     p.ldo = K;
     p.so = so;
-    if ((s = hip_status(run_prologue(p, st), "A8 prologue"))) return s;
+    if (a8_prepass_supported(p, g)) {  // the prologue and the grid decode in one launch
+        if ((s = hip_status(run_a8_prepass(p, g, st), "A8 prologue and grid decode"))) return s;
+        g.w8_ready = true;
+    } else if ((s = hip_status(run_prologue(p, st), "A8 prologue"))) {
+        return s;
+    }
     return hip_status(run_gemm_i8(g, st), L ? "A8 gemm with LoRA" : "A8 gemm");
 }
 
@@ -1155,6 +1160,13 @@ qlin_status qlin_dequantize_w4a8(const qlin_tensor* qdata, const qlin_tensor* s_
     if (N == 0 || K == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     const int srdt = (SR.dtype == QLIN_DT_U8) ? DT_E4M3 : SR.dtype;
+    if (O.dtype == QLIN_DT_I8) {  // the forward's grid decode (four threads per 64 codes) when its layout allows
+        GemmI8Args g;
+        g.N = N; g.K = K; g.q = (const uint8_t*)Q.data; g.ldq = Q.ld; g.bits = bits; g.group_size = group_size;
+        g.s_rel = SR.data; g.s_rel_dtype = srdt; g.ld_srel = SR.ld; g.s_ch = (const float*)s_channel->data;
+        g.codebook = cb; g.w8 = (int8_t*)O.data;
+        if (a8_grid_supported(g)) return hip_status(run_a8_grid(g, st), "w4a8 grid");
+    }
     if ((s = hip_status(run_dequant_w4a8((const uint8_t*)Q.data, N, K, Q.ld, bits, group_size, SR.data, srdt, SR.ld,
                                          (const float*)s_channel->data, cb, O.data, O.dtype, st), "w4a8 dequantize")))
         return s;

@@ -12,6 +12,7 @@
 // [N, K/4] (byte j holds bits 4-5 of codes 4j..4j+3).
 #include "qlin_internal.h"
 #include "lora_frag.h"
+#include "prologue_dev.h"
 
 namespace qlin {
 namespace {
@@ -617,13 +618,14 @@ __global__ __launch_bounds__(512) void gemm_a8_kernel(GemmI8Args p) {
 // + 15], so the lanes of a wave load contiguous runs (8 bytes of nibbles and, for 6 bits, 4 bytes
 // of high bits each) and store 16 contiguous bytes each.  The 4-bit level table (one grid byte per
 // code) is built a quarter per thread and exchanged within the quad.  Needs group_size % 64 == 0.
+// Thread t of the decode (quads of consecutive t share a segment; t % 4 == threadIdx.x % 4).
 template <int BITS, bool CB, typename TSrel>
-__global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __restrict__ w8) {
+__device__ __forceinline__ void a8_grid_quad(const GemmI8Args& p, int8_t* __restrict__ w8, uint32_t t) {
 #pragma clang fp contract(off)
     // 32-bit indices: the launchers refuse grids of 2^32 threads or more (4 per 64-code segment)
     const uint32_t segs = (uint32_t)p.K / 64u, total = (uint32_t)p.N * segs;
-    const uint32_t u = (blockIdx.x * 256u + threadIdx.x) >> 2;
-    const int q = threadIdx.x & 3;
+    const uint32_t u = t >> 2;
+    const int q = (int)(t & 3u);
     // Threads past the end work on the last segment (all four lanes of a quad take part in the
     // table exchange) and skip only the store.
     const bool live = u < total;
@@ -680,6 +682,54 @@ __global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __re
         }
     }
     if (live) *reinterpret_cast<u32x4*>(w8 + n * p.K + 64 * sg + 16 * q) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
+template <int BITS, bool CB, typename TSrel>
+__global__ __launch_bounds__(256) void a8_grid_kernel(GemmI8Args p, int8_t* __restrict__ w8) {
+    a8_grid_quad<BITS, CB, TSrel>(p, w8, blockIdx.x * 256u + threadIdx.x);
+}
+
+// The s_rel dtype and the codebook choice of a8_grid_quad, made at run time (uniform per launch).
+template <int BITS>
+__device__ __forceinline__ void a8_grid_quad_rt(const GemmI8Args& p, int8_t* __restrict__ w8, uint32_t t) {
+    auto by_srel = [&]<bool CB>() {
+        switch (p.s_rel_dtype) {
+            case DT_E4M3: a8_grid_quad<BITS, CB, uint8_t>(p, w8, t); break;
+            case DT_F16: a8_grid_quad<BITS, CB, f16>(p, w8, t); break;
+            case DT_BF16: a8_grid_quad<BITS, CB, bf16_t>(p, w8, t); break;
+            default: a8_grid_quad<BITS, CB, float>(p, w8, t); break;
+        }
+    };
+    if (BITS == 4 && p.codebook) by_srel.template operator()<true>();
+    else by_srel.template operator()<false>();
+}
+
+// The A8 pre-pass in one launch: workgroups 0 .. M - 1 are the activation prologue's rows, the rest
+// decode the weight grid (workgroup M + j: threads j NT .. j NT + NT - 1 of a8_grid_kernel's
+// decode).  Both roles compute exactly what their own kernels compute.  In one launch the decode
+// takes each CU as the prologue's last rows there finish, instead of after the whole prologue
+// (same process: W6A8 M9504 K13824 N5120 780 -> 739 us per call, M9504 K5120 N13824 773 -> 741,
+// W4A8 M4096 K3072 N12288 196 -> 183; at M1024 0.8-3.3 us slower, so fewer than A8_PREPASS_ROWS rows
+// keep two launches).  The two roles side by side were slower than in sequence: interleaved through
+// the grid 157 against 134 us (W6A8 M1024 K13824), and the two kernels on two streams 67 against
+// 50 us for the pair alone.
+struct A8PrepassArgs {
+    const void* x;
+    int64_t ldx;
+    bool vec_ok;
+    int8_t* qo;
+    float* so;
+};
+template <typename TIn, int G, int SLOTS, int BITS>
+__global__ __launch_bounds__(prologue_max_threads(SLOTS), SLOTS <= 2 ? 6 : 1) void a8_prepass_kernel(A8PrepassArgs a,
+                                                                                                     GemmI8Args p) {
+    const uint32_t b = blockIdx.x, rows = (uint32_t)p.M;
+    if (b < rows) {
+        prologue_row<TIn, PROLOGUE_A8, G, SLOTS>(b, (int)blockDim.x, (const TIn*)a.x, a.ldx, (int)p.K, a.vec_ok, nullptr,
+                                                 p.ldx, nullptr, a.qo, a.so, nullptr, nullptr);
+        return;
+    }
+    a8_grid_quad_rt<BITS>(p, p.w8, (b - rows) * blockDim.x + threadIdx.x);
 }
 
 // int8 GEMM y = epilogue(xq[M, K] . w8[N, K]^T), tile BMT x BNT x BK, 8 waves 4 (M) x 2 (N),
@@ -1113,6 +1163,12 @@ inline bool a8_smallm_ok(const GemmI8Args& p) {
            p.ldx % 16 == 0 && (uintptr_t)p.xq % 16 == 0;
 }
 
+// The decode-once branch of launch_o (the small-M kernel aside).
+inline bool a8_takes_decode_once(const GemmI8Args& p) {
+    return p.w8 && a8_decode_once(p.M, p.N, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
+           (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0;
+}
+
 template <int BITS, bool CB, typename TSrel>
 hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
     if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return hipErrorInvalidValue;
@@ -1124,14 +1180,15 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
         else hipLaunchKernelGGL((a8_smallm_kernel<BITS, CB, TSrel, 2>), grid, block, 0, st, p);
         return hipGetLastError();
     }
-    if (p.w8 && a8_decode_once(p.M, p.N, p.K) && p.group_size % 64 == 0 && p.ldx % 16 == 0 &&
-        (uintptr_t)p.xq % 16 == 0 && (uintptr_t)p.w8 % 16 == 0) {
+    if (a8_takes_decode_once(p)) {
         const int64_t segs = p.N * (p.K / 64);
         if (4 * segs + 256 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // the grid kernel's 32-bit indices
-        hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, TSrel>), dim3((unsigned)((4 * segs + 255) / 256)), dim3(256), 0, st,
-                           p, p.w8);
-        hipError_t err = hipGetLastError();
-        if (err != hipSuccess) return err;
+        if (!p.w8_ready) {
+            hipLaunchKernelGGL((a8_grid_kernel<BITS, CB, TSrel>), dim3((unsigned)((4 * segs + 255) / 256)), dim3(256), 0,
+                               st, p, p.w8);
+            hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
+        }
         auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
         // LoRA term in the epilogue by up dtype (none: -1)
         const int ldu = !p.lora.t ? -1 : p.lora.up_dt;
@@ -1241,6 +1298,46 @@ hipError_t run_a8_grid(const GemmI8Args& p, hipStream_t st) {
     if (!a8_grid_supported(p)) return hipErrorInvalidValue;
     if (p.bits == 4) return p.codebook ? launch_grid<4, true>(p, st) : launch_grid<4, false>(p, st);
     return launch_grid<6, false>(p, st);
+}
+
+bool a8_prepass_supported(const PrologueArgs& a, const GemmI8Args& p) {
+    if (p.M < A8_PREPASS_ROWS) return false;
+    if (a.mode != PROLOGUE_A8 || (a.x_dtype != DT_F16 && a.x_dtype != DT_BF16) || (a.G != 128 && a.G != 256)) return false;
+    if (a.M != p.M || a.M < 1 || a.K != p.K || a.K > PROLOGUE_ROW_MAX || a.qo != p.xq || a.so != p.sx || a.ldo != p.ldx ||
+        a.xr)
+        return false;
+    int nt = 0, slots = 0;
+    prologue_shape(a.K, nt, slots);
+    if (slots > 2) return false;
+    if (p.y_dtype != DT_F32 && p.y_dtype != DT_F16 && p.y_dtype != DT_BF16) return false;
+    if (p.s_rel_dtype != DT_E4M3 && p.s_rel_dtype != DT_F16 && p.s_rel_dtype != DT_BF16 && p.s_rel_dtype != DT_F32)
+        return false;
+    if (p.K % 64 || !a8_grid_supported(p) || a8_smallm_ok(p) || !a8_takes_decode_once(p)) return false;
+    const int64_t threads = 4 * p.N * (p.K / 64);
+    return threads + nt <= (int64_t)UINT32_MAX && p.M + (threads + nt - 1) / nt <= INT32_MAX;
+}
+
+hipError_t run_a8_prepass(const PrologueArgs& a, const GemmI8Args& p, hipStream_t st) {
+    if (!a8_prepass_supported(a, p)) return hipErrorInvalidValue;
+    int nt = 0, slots = 0;
+    prologue_shape(a.K, nt, slots);
+    const int64_t blocks = p.M + (4 * p.N * (p.K / 64) + nt - 1) / nt;
+    const A8PrepassArgs pa{a.x, a.ldx, (a.K % 16 == 0) && (a.ldx % 16 == 0) && (a.ldo % 16 == 0) && ((uintptr_t)a.x % 64 == 0),
+                           a.qo, a.so};
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3((unsigned)nt), 0, st, pa, p);
+        return hipGetLastError();
+    };
+    auto by_bits = [&]<typename TIn, int G, int SL>() {
+        return p.bits == 4 ? go(a8_prepass_kernel<TIn, G, SL, 4>) : go(a8_prepass_kernel<TIn, G, SL, 6>);
+    };
+    auto by_slots = [&]<typename TIn, int G>() {
+        return slots <= 1 ? by_bits.template operator()<TIn, G, 1>() : by_bits.template operator()<TIn, G, 2>();
+    };
+    auto by_group = [&]<typename TIn>() {
+        return a.G == 128 ? by_slots.template operator()<TIn, 128>() : by_slots.template operator()<TIn, 256>();
+    };
+    return a.x_dtype == DT_F16 ? by_group.template operator()<f16>() : by_group.template operator()<bf16_t>();
 }
 
 hipError_t run_gemm_i8(const GemmI8Args& p, hipStream_t st) {

@@ -293,6 +293,7 @@ struct GemmI8Args {
     int y_dtype = DT_F16;
     int64_t ldy = 0;
     int8_t* w8 = nullptr;            // workspace for the decoded int8 grid [N, K] (decode-once path)
+    bool w8_ready = false;           // w8 already holds the grid (run_a8_prepass decoded it)
     LoraTile lora;                   // decode-once DMA GEMM only (gemm_i8_fuses_lora)
     ResidualTile res;                // the large-tile kernels only (gemm_i8_fuses_residual)
 };
@@ -315,6 +316,13 @@ inline bool a8_decode_once(int64_t M, int64_t N, int64_t K) {
 // group_size a multiple of 64, 16-byte aligned code rows.
 bool a8_grid_supported(const GemmI8Args& p);
 hipError_t run_a8_grid(const GemmI8Args& p, hipStream_t st);
+// The A8 prologue a (into p.xq, p.sx) and the weight-grid decode into p.w8 in one launch, for calls
+// of at least A8_PREPASS_ROWS rows that run_gemm_i8 serves with the decode-once GEMM: 16-bit
+// activations, rotation group 128 or 256, rows of at most 32768 values.  After it, run_gemm_i8 with
+// p.w8_ready skips the decode.
+constexpr int64_t A8_PREPASS_ROWS = 2048;
+bool a8_prepass_supported(const PrologueArgs& a, const GemmI8Args& p);
+hipError_t run_a8_prepass(const PrologueArgs& a, const GemmI8Args& p, hipStream_t st);
 
 // Unmerged LoRA: y += scale * (x down^T) up^T after the base linear (lora.hip).
 struct LoraArgs {

@@ -699,6 +699,38 @@ def test_w4a8_linear_large_tiles(bits, cb, srdt, gs, k, m, n):
     assert (err <= lim).all(), f"bits={bits} large tiles: max error / bound {float((err / lim).max()):.3f}"
 
 
+@pytest.mark.parametrize("xdt,g,k,bits,gs,srdt", [
+    (torch.bfloat16, 256, 13824, 6, 64, torch.float16),       # two slots per prologue thread
+    (torch.bfloat16, 128, 3072, 4, 128, torch.float8_e4m3fn),
+    (torch.float16, 256, 5120, 4, 64, torch.bfloat16),
+    (torch.float16, 128, 1024, 6, 64, torch.float32),         # fp16 scales widened to fp32
+])
+def test_w4a8_prepass_one_launch(xdt, g, k, bits, gs, srdt):
+    """Decode-once shapes from 2048 rows with 16-bit activations and rotation group 128 or 256: the
+    activation prologue (M = 2053 workgroups) and the weight-grid decode (ragged N = 137) share one
+    launch.  The output replays exactly from the standalone quantizer's activations and the
+    oracle's grid."""
+    m, n = 2053, 137
+    rng = np.random.default_rng(k + bits)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    q, s_rel, s_ch, book = qz().quantize_w4a8_int8_weight(
+        w, bits=bits, group_size=gs, convrot_groupsize=g,
+        s_rel_dtype=torch.float16 if srdt == torch.float32 else srdt)
+    s_rel = s_rel.to(srdt)
+    x = x_fp16(m, k, seed=k, outliers=True).to(xdt)
+    Q = qlin()
+    y = Q.w4a8_int8_linear(x.to(DEV), q.to(DEV), s_rel.to(DEV), s_ch.to(DEV), None, None, None, gs, g)
+    assert y.dtype == xdt
+    w8 = O.w4a8_int8_grid(q.numpy(), s_rel.float().numpy(), None, k, bits, gs)
+    xq, sx = check_a8_activation_rows(Q, x.to(DEV), g, np.array([0, 1, 1030, m - 1]), f"{xdt} K={k}: activations")
+    xq, sx = xq.cpu().numpy(), sx.cpu().numpy().reshape(-1)
+    acc = O.int8_gemm_i64(xq, w8)
+    replay = torch.from_numpy(((acc.astype(np.float32) * sx[:, None]).astype(np.float32) *
+                               s_ch.numpy()[None, :]).astype(np.float32)).to(xdt)
+    bad = y.cpu().view(torch.int16) != replay.view(torch.int16)
+    assert not bad.any(), f"{int(bad.sum())} mismatches, first at {bad.nonzero()[:3].tolist()}"
+
+
 @pytest.mark.parametrize("case", ["gauss_96x1024", "heavy_96x1024"])
 @pytest.mark.parametrize("fmt,bits", [("w4a8", 4), ("w6a8", 6)])
 def test_dequantize_w4a8_golden(case, fmt, bits):
