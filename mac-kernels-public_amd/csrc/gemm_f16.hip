@@ -1025,6 +1025,20 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
         auto tiles = [&](int bm, int bn) { return ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn); };
         if (vec && tiles(256, 256) >= 160) {
             const dim3 grid((unsigned)tiles(256, 256));
+            const int64_t m1 = a.lora.t ? 0 : tail_split_rows(a.M, a.N);
+            if (m1) {  // whole rounds of 256 x 256 tiles, then the rest as one round of 128 x 256 tiles
+                GemmF16Args top = a, rest = a;
+                top.M = m1;
+                rest.M = a.M - m1;
+                rest.x = a.x + m1 * a.ldx;
+                if (a.xexp) rest.xexp = a.xexp + m1;
+                rest.y = (uint8_t*)a.y + m1 * a.ldy * dt_bytes(a.y_dtype);
+                if (a.res.r) rest.res.r = (const uint8_t*)a.res.r + m1 * a.res.ldr * dt_bytes(a.res.r_dt);
+                auto tiles_of = [](const GemmF16Args& g, int bm) { return ((g.M + bm - 1) / bm) * ((g.N + 255) / 256); };
+                hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), dim3((unsigned)tiles_of(top, 256)), dim3(512), 0, st, top);
+                hipLaunchKernelGGL((gemm_wo_dma_kernel<128, 3>), dim3((unsigned)tiles_of(rest, 128)), dim3(512), 0, st, rest);
+                return hipGetLastError();
+            }
             if (!a.lora.t) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), grid, dim3(512), 0, st, a);
             else if (a.lora.up_dt == DT_BF16) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3, DT_BF16>), grid, dim3(512), 0, st, a);
             else if (a.lora.up_dt == DT_F16) hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3, DT_F16>), grid, dim3(512), 0, st, a);

@@ -1202,6 +1202,22 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
             }
         };
         if (ldu != -1 && ldu != DT_BF16 && ldu != DT_F16 && ldu != DT_F32) return hipErrorInvalidValue;
+        const int64_t m1 = ldu == -1 && tiles(256, 256) >= 192 ? tail_split_rows(p.M, p.N) : 0;
+        if (m1) {  // whole rounds of 256 x 256 tiles, then the rest as one round of 128 x 256 tiles
+            GemmI8Args top = p, rest = p;
+            top.M = m1;
+            rest.M = p.M - m1;
+            rest.xq = p.xq + m1 * p.ldx;
+            rest.sx = p.sx + m1;
+            rest.y = (uint8_t*)p.y + m1 * p.ldy * dt_bytes(p.y_dtype);
+            if (p.res.r) rest.res.r = (const uint8_t*)p.res.r + m1 * p.res.ldr * dt_bytes(p.res.r_dt);
+            auto tiles_of = [](const GemmI8Args& g, int bm) { return ((g.M + bm - 1) / bm) * ((g.N + 255) / 256); };
+            hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2, false>), dim3((unsigned)tiles_of(top, 256)), dim3(512), 0,
+                               st, top, top.w8);
+            hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2, false>), dim3((unsigned)tiles_of(rest, 128)), dim3(512),
+                               0, st, rest, rest.w8);
+            return hipGetLastError();
+        }
         if (tiles(256, 256) >= 192)
             go.template operator()<256, 256>();
         // 128 x 160 tiles (2 x 5 waves, no LoRA term) when they make one round of at least 3/4 of

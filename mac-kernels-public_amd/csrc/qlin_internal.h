@@ -237,6 +237,22 @@ __device__ __forceinline__ void residual_apply8(const ResidualTile& R, const int
     residual_apply8<Q>(R, m, ncq, M, N, rsq, v);
 }
 
+// Bytes per element of an output, residual or activation dtype (f32, f16, bf16).
+inline int dt_bytes(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+// A grid of 256 x 256 output tiles on the 256 CUs whose last round leaves most CUs idle: the rows
+// returned (a multiple of 256) keep those tiles in whole rounds, the rest take one round of 128 x
+// 256 tiles in a second launch (about 0.6 of a 256 x 256 tile's time each); 0 when that does not
+// save a third of a round.
+inline int64_t tail_split_rows(int64_t M, int64_t N) {
+    const int64_t nt = (N + 255) / 256, tiles = (M + 255) / 256 * nt, rounds = (tiles + 255) / 256;
+    if (tiles <= 256) return 0;
+    const int64_t mt1 = (rounds - 1) * 256 / nt, m1 = 256 * mt1, rest = M - m1;
+    if (mt1 < 1 || rest <= 0 || (rest + 127) / 128 * nt > 256) return 0;
+    const double split = (double)((mt1 * nt + 255) / 256) + 0.6;
+    return split <= (double)rounds - 0.33 ? m1 : 0;
+}
+
 struct GemmF16Args {
     int wkind = WO_INT8;
     int gguf_type = 0;

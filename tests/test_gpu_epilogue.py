@@ -150,6 +150,7 @@ def _separate(Q, linear, res, rs, odt):
 
 @pytest.mark.parametrize("m,n,k", [
     (2048, 5120, 1024),   # 160 tiles of 256 x 256: the LDS-DMA GEMM
+    (2600, 6100, 512),    # 264 tiles: rows 0..2559 on 256 x 256 tiles, the last 40 on 128 x 256 tiles
     (1000, 2560, 1024),   # register-staged 128 x 128 tiles, a ragged M
     (100, 512, 1024),     # the DMA-ring kernel (a few hundred rows)
     (5, 512, 1024),       # small M: the linear in fp32, then the residual kernel
@@ -173,6 +174,7 @@ def test_int8_residual_fused_equals_separate(m, n, k, odt, rdt):
 
 @pytest.mark.parametrize("m,n,k,bits,gs", [
     (1024, 4096, 1024, 4, 64),   # grid decoded once, then the int8 DMA GEMM (128 x 256 tiles)
+    (2600, 6100, 512, 6, 64),    # 264 tiles of 256 x 256: the last 40 rows on 128 x 256 tiles
     (1000, 5100, 1024, 6, 64),   # the same with 2 x 5 waves on 128 x 160 tiles (256 of them)
     (300, 24600, 1024, 6, 64),   # one 256-row tile over a wide grid: the fused-decode GEMM
     (100, 1000, 1024, 4, 16),    # group 16: the 128 x 128 decode-in-load kernel, residual kernel after

@@ -468,10 +468,14 @@ def test_int8_linear(g, m):
 
 @pytest.mark.parametrize("g,m,n,xdt,odt", [(0, 2047, 6136, torch.float16, torch.float16),
                                            (128, 2303, 5880, torch.bfloat16, torch.bfloat16),
-                                           (128, 640, 4000, torch.float16, torch.float32)])
+                                           (128, 640, 4000, torch.float16, torch.float32),
+                                           (128, 2600, 6100, torch.float16, torch.float16),
+                                           (0, 2600, 6100, torch.bfloat16, torch.float32)])
 def test_int8_linear_large_tiles(g, m, n, xdt, odt):
-    """Shapes that take the 256 x 256 tile (192 and 207 tiles, ragged M and N) and the 128 x 128 tile
-    (640 x 4000: 160 tiles), with fp16 scales and a bias."""
+    """Shapes that take the 256 x 256 tile (192 and 207 tiles, ragged M and N), the 128 x 128 tile
+    (640 x 4000: 160 tiles), and 264 tiles of 256 x 256 whose last round would leave most CUs idle
+    (rows 0..2559 on 256 x 256 tiles, then rows 2560..2599 on 128 x 256 tiles in a second launch),
+    with fp16 scales and a bias."""
     k = 256
     rng = np.random.default_rng(17)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -657,6 +661,8 @@ A8_TILE_CASES = [
     (6, None, torch.float16, 64, 256, 1024, 4200),  # 216 tiles of 128 x 160 (2 x 5 waves, one round)
     (4, None, torch.float16, 64, 1024, 1000, 5100), # 256 tiles of 128 x 160, ragged M and N, 8 k-tiles
     (4, None, torch.float8_e4m3fn, 128, 256, 1024, 2000),
+    # 264 tiles of 256 x 256: rows 0..2559 in whole rounds of them, the last 41 on 128 x 256 tiles
+    (6, None, torch.float16, 64, 512, 2601, 6100),
     # M < 512 with >= 192 tiles of 256 x 256: the fused-decode kernel, one scale table per thread
     # pair (group 128) and per thread (group 64)
     (4, None, torch.float16, 128, 128, 300, 24600),
