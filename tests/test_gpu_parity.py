@@ -737,6 +737,46 @@ def test_w4a8_prepass_one_launch(xdt, g, k, bits, gs, srdt):
     assert not bad.any(), f"{int(bad.sum())} mismatches, first at {bad.nonzero()[:3].tolist()}"
 
 
+@pytest.mark.parametrize("kind", ["w6a8", "int8"])
+def test_prepass_and_tail_split_graph_replays(kind):
+    """Captured calls that take the one-launch A8 pre-pass (2601 rows) and the tail split (264 tiles
+    of 256 x 256: 2560 rows, then 41 on 128 x 256 tiles), replayed with new activations and eager
+    calls between the replays: every replay equals the eager call on the same input."""
+    Q = qlin()
+    m, n, k = 2601, 6100, 512
+    g = torch.Generator().manual_seed(71)
+    if kind == "w6a8":
+        from qlin.quantize import pack_codes
+        q = pack_codes(torch.randint(1, 64, (n, k), generator=g, dtype=torch.int32), 6).to(DEV)
+        s_rel = (2 + 2 * torch.rand(n, k // 64, generator=g)).half().to(DEV)
+        s_ch = (torch.rand(n, generator=g) * 2e-4 + 1e-4).to(DEV)
+        call = lambda x: Q.w4a8_int8_linear(x, q, s_rel, s_ch, None, None, None, 64, 128)
+    else:
+        w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(DEV)
+        s = (torch.rand(n, generator=g) * 1e-3).half().to(DEV)
+        call = lambda x: Q.int8_linear(x, w, s, convrot=True, convrot_groupsize=128)
+    xs = [x_fp16(m, k, seed=72 + i, outliers=True).to(DEV) for i in range(3)]
+    xin = xs[0].clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        call(xin)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yg = call(xin)
+    torch.cuda.synchronize()
+    for i in range(6):
+        xin.copy_(xs[i % 3])
+        graph.replay()
+        torch.cuda.synchronize()
+        got = yg.clone()
+        want = call(xs[i % 3])
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{kind}: replay {i} differs from the eager call"
+
+
 @pytest.mark.parametrize("case", ["gauss_96x1024", "heavy_96x1024"])
 @pytest.mark.parametrize("fmt,bits", [("w4a8", 4), ("w6a8", 6)])
 def test_dequantize_w4a8_golden(case, fmt, bits):
