@@ -470,7 +470,8 @@ def test_int8_linear(g, m):
                                            (128, 2303, 5880, torch.bfloat16, torch.bfloat16),
                                            (128, 640, 4000, torch.float16, torch.float32),
                                            (128, 2600, 6100, torch.float16, torch.float16),
-                                           (0, 2600, 6100, torch.bfloat16, torch.float32)])
+                                           (0, 2600, 6100, torch.bfloat16, torch.float32),
+                                           (128, 5000, 4000, torch.float16, torch.bfloat16)])
 def test_int8_linear_large_tiles(g, m, n, xdt, odt):
     """Shapes that take the 256 x 256 tile (192 and 207 tiles, ragged M and N), the 128 x 128 tile
     (640 x 4000: 160 tiles), and 264 tiles of 256 x 256 whose last round would leave most CUs idle
@@ -663,6 +664,8 @@ A8_TILE_CASES = [
     (4, None, torch.float8_e4m3fn, 128, 256, 1024, 2000),
     # 264 tiles of 256 x 256: rows 0..2559 in whole rounds of them, the last 41 on 128 x 256 tiles
     (6, None, torch.float16, 64, 512, 2601, 6100),
+    # 320 tiles of 256 x 256: rows 0..4095 in one round, the last 904 on 128 x 256 tiles
+    (4, "auto", torch.float8_e4m3fn, 128, 256, 5000, 4000),
     # M < 512 with >= 192 tiles of 256 x 256: the fused-decode kernel, one scale table per thread
     # pair (group 128) and per thread (group 64)
     (4, None, torch.float16, 128, 128, 300, 24600),
