@@ -406,13 +406,15 @@ def gpu_activations(m, k, seed, outliers=False):
     return x.half()
 
 
-def cpu_linear_baseline(pool, name, m, k, n, decode_rows, rows_n, rows_m=256):
+def cpu_linear_baseline(pool, name, m, k, n, decode_rows, rows_n=None, rows_m=None):
     """Dequantize-then-matmul on the host for one call: the oracle's C decode of `rows_n` weight
-    rows (row-parallel on all host threads), then an fp32 torch matmul of `rows_m` activation rows
-    against them; each leg the median of 5 after 2 warm-ups, scaled to the full M and N."""
+    rows (all N by default; row-parallel on all host threads), then an fp32 torch matmul of `rows_m`
+    activation rows (all M by default) against them; each leg the median of 5 after 2 warm-ups,
+    scaled to the full M and N when sampled."""
     import torch
     torch.set_num_threads(pool.threads)
-    rows_m = min(rows_m, m)
+    rows_n = min(rows_n or n, n)
+    rows_m = min(rows_m or m, m)
     wd = {}
 
     def decode():
@@ -429,7 +431,8 @@ def cpu_linear_baseline(pool, name, m, k, n, decode_rows, rows_n, rows_m=256):
         "kind": "port",
         "sample": (f"{name}: oracle C decode of {rows_n} of {n} weight rows to fp32 (original basis) on "
                    f"{pool.threads} threads, fp32 torch matmul of {rows_m} of {m} activation rows against them "
-                   f"on {pool.threads} threads; medians of 5 after 2 warm-ups, scaled to M={m}, N={n}"),
+                   f"on {pool.threads} threads; medians of 5 after 2 warm-ups"
+                   + ("" if (rows_m, rows_n) == (m, n) else f", scaled to M={m}, N={n}")),
         "decode_ms": round(dec_full, 2), "matmul_ms": round(mm_full, 2), "total_ms": round(total, 2),
     }
 
@@ -494,7 +497,7 @@ def run_configs(names, steps, warmup, pool):
             qn, srn, scn = q.view(torch.uint8).numpy(), sr.float().numpy(), sc.numpy()
             cpu = pool and cpu_linear_baseline(
                 pool, name, m, k, n,
-                lambda r0, r1: O.dequantize_w4a8(qn[r0:r1], srn[r0:r1], scn[r0:r1], None, gs, g, bits=bits), 1024)
+                lambda r0, r1: O.dequantize_w4a8(qn[r0:r1], srn[r0:r1], scn[r0:r1], None, gs, g, bits=bits))
             rec = {"us_per_call": round(us, 2), "TOPs": round(tops, 2),
                    "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "pool_copies": copies,
                    "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
@@ -521,7 +524,7 @@ def run_configs(names, steps, warmup, pool):
             tfl = flops / (us * 1e-6) / 1e12
             rn = raw.numpy()
             cpu = pool and cpu_linear_baseline(pool, name, m, k, n,
-                                               lambda r0, r1: O.gguf_dequantize(rn[r0:r1], t, (r1 - r0, k)), 1024)
+                                               lambda r0, r1: O.gguf_dequantize(rn[r0:r1], t, (r1 - r0, k)))
             rec = {"us_per_call": round(us, 2), "TFLOPs": round(tfl, 2),
                    "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "pool_copies": copies,
                    "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": FP16_PEAK_TFLOPS,
@@ -577,14 +580,14 @@ def run_configs(names, steps, warmup, pool):
                     qn, sn = q.numpy(), s.float().numpy()
                     parts.append(cpu_linear_baseline(
                         pool, f"{k}->{n}", m, k, n,
-                        lambda r0, r1, qn=qn, sn=sn: O.rotate(O.dequantize_int8(qn[r0:r1], sn[r0:r1]), g), 512))
+                        lambda r0, r1, qn=qn, sn=sn: O.rotate(O.dequantize_int8(qn[r0:r1], sn[r0:r1]), g)))
                 layer = sum(p["total_ms"] for p in parts)
                 cpu = {"value": round(flops / (layer * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "cores": pool.threads,
                        "kind": "port",
-                       "sample": (f"one layer's four linears, each: oracle C decode of 512 weight rows to fp32 "
-                                  f"(original basis) on {pool.threads} threads, fp32 torch matmul of 256 of {m} "
-                                  f"activation rows against them on {pool.threads} threads; medians of 5 after 2 "
-                                  f"warm-ups, scaled to the linear's M and N; x{DIT_LAYERS} for the stack"),
+                       "sample": (f"one layer's four linears in full, each: oracle C decode of all its weight "
+                                  f"rows to fp32 (original basis) on {pool.threads} threads, fp32 torch matmul of "
+                                  f"all {m} activation rows against them on {pool.threads} threads; medians of 5 "
+                                  f"after 2 warm-ups; x{DIT_LAYERS} for the stack"),
                        "decode_ms": round(sum(p["decode_ms"] for p in parts), 2),
                        "matmul_ms": round(sum(p["matmul_ms"] for p in parts), 2),
                        "layer_ms": round(layer, 2), "stack_ms": round(layer * DIT_LAYERS, 1)}
