@@ -181,20 +181,30 @@ def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
     weights = {t: make_gguf_weights(t, n, k, copies * len(ms), seed=i, raw=bases[t]) for i, t in enumerate(GGUF_SUITE)}
     g = torch.Generator().manual_seed(1)
     xs = {m: torch.randn(m, k, generator=g).half().cuda() for m in ms}
-    calls = []
+    # The step runs its calls M-major, all M = 1 calls, then M = 8, then M = 64, as a model's decode
+    # or prefill step runs its linears at one M; the type-major order (each type's three M in a row)
+    # switches kernel families on every call and is timed beside it for reference.
+    calls, calls_tm = [], []
     for c in range(copies):
+        for j, m in enumerate(ms):
+            for t in GGUF_SUITE:
+                calls.append((t, m, weights[t][c * len(ms) + j]))
         for t in GGUF_SUITE:
             for j, m in enumerate(ms):
-                calls.append((t, m, weights[t][c * len(ms) + j]))
+                calls_tm.append((t, m, weights[t][c * len(ms) + j]))
     tid = {t: qlin.GGUF_TYPES[t][0] for t in GGUF_SUITE}
 
-    def step_all():
-        for t, m, w in calls:
-            qlin.gguf_linear(xs[m], w, tid[t], (n, k))
+    def step_of(order):
+        def step():
+            for t, m, w in order:
+                qlin.gguf_linear(xs[m], w, tid[t], (n, k))
+        return step
 
+    step_all = step_of(calls)
     log(f"[gguf] {len(calls)} calls per graph replay ({copies} pool passes)")
     ms_replay, _ = time_graph(step_all, max(1, steps), warmup)
     ms_step = ms_replay / copies
+    ms_tm = time_graph(step_of(calls_tm), max(1, steps), warmup)[0] / copies
     alg_bytes = sum(gguf_bytes(t, n, k) + m * k * 2 + m * n * 2 for t in GGUF_SUITE for m in ms)
     flops = sum(2 * m * n * k for _ in GGUF_SUITE for m in ms)
     gbs = alg_bytes / (ms_step * 1e-3) / 1e9
@@ -227,6 +237,7 @@ def suite_gguf(steps, warmup, n=4096, k=4096, ms=(1, 8, 64)):
     return {
         "ms_per_step": ms_step, "value": gbs, "alg_bytes": alg_bytes, "flops": flops,
         "launches": len(GGUF_SUITE) * len(ms), "detail": detail, "copies": copies, "bases": bases,
+        "type_major": {"ms_per_step": round(ms_tm, 5), "GBps": round(alg_bytes / (ms_tm * 1e-3) / 1e9, 1)},
     }
 
 
@@ -927,9 +938,11 @@ def main():
                  "quantized on the host; W4/W6 random legal codes and group scales; activations fp16 N(0, 1)"),
         "config": {
             "workload": "gguf_decode_linear K=N=4096, M in {1,8,64}, types Q4_0 Q8_0 Q4_K Q5_K Q6_K IQ4_NL IQ4_XS "
-                        "(21 calls per step, weights cycled through a >=1 GiB pool, HIP-graph replay)",
+                        "(21 calls per step, M-major: the 7 types at M=1, then at M=8, then at M=64; weights "
+                        "cycled through a >=1 GiB pool, HIP-graph replay)",
             "K": 4096, "N": 4096, "M": [1, 8, 64], "types": list(GGUF_SUITE), "pool_copies": r["copies"],
             "tflops_step": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 3),
+            "type_major_step": r["type_major"],
         },
         "roofline": {
             "bound": "hbm", "achieved": dk["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
