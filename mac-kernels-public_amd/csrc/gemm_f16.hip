@@ -536,8 +536,8 @@ __global__ __launch_bounds__(512) void gemm_wo_i8_kernel(GemmF16Args a) {
 
 // INT8 weight-only GEMM with both operands moved by LDS DMA: y = epilogue(x[M, K] . w[N, K]^T), x the
 // normalized fp16 activations, w the int8 weights as stored (no widening before LDS, so a 64-value
-// k-tile brings in 32 KB of activations and 16 KB of weights).  Tile BMT x 256, 8 waves 4 (M) x
-// 2 (N), v_mfma_f32_32x32x16_f16, STAGES k-tiles in flight.
+// k-tile brings in 32 KB of activations and 16 KB of weights).  Tile BMT x 256, 8 waves 2 (M) x
+// 4 (N), v_mfma_f32_32x32x16_f16, STAGES k-tiles in flight.
 //
 // k order inside a 64-value k-tile: MFMA step s = 2p + e (p, e in {0, 1}) gives the lanes of half
 // h (lane / 32) the 8 values k = 32p + 16h + 8e .. + 7 in both operands, so one 16-byte read of a
@@ -1036,6 +1036,8 @@ hipError_t launch1(const GemmF16Args& a, hipStream_t st) {
                 if (a.res.r) rest.res.r = (const uint8_t*)a.res.r + m1 * a.res.ldr * dt_bytes(a.res.r_dt);
                 auto tiles_of = [](const GemmF16Args& g, int bm) { return ((g.M + bm - 1) / bm) * ((g.N + 255) / 256); };
                 hipLaunchKernelGGL((gemm_wo_dma_kernel<256, 3>), dim3((unsigned)tiles_of(top, 256)), dim3(512), 0, st, top);
+                const hipError_t err = hipGetLastError();
+                if (err != hipSuccess) return err;
                 hipLaunchKernelGGL((gemm_wo_dma_kernel<128, 3>), dim3((unsigned)tiles_of(rest, 128)), dim3(512), 0, st, rest);
                 return hipGetLastError();
             }

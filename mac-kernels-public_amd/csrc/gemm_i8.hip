@@ -1214,6 +1214,8 @@ hipError_t launch_o(const GemmI8Args& p, hipStream_t st) {
             auto tiles_of = [](const GemmI8Args& g, int bm) { return ((g.M + bm - 1) / bm) * ((g.N + 255) / 256); };
             hipLaunchKernelGGL((gemm_i8dma_kernel<256, 256, 128, 2, false>), dim3((unsigned)tiles_of(top, 256)), dim3(512), 0,
                                st, top, top.w8);
+            const hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
             hipLaunchKernelGGL((gemm_i8dma_kernel<128, 256, 128, 2, false>), dim3((unsigned)tiles_of(rest, 128)), dim3(512),
                                0, st, rest, rest.w8);
             return hipGetLastError();
