@@ -11,9 +11,13 @@
 //     1024 contiguous bytes per row, into LDS (rows padded by 16 bytes so the fragment reads are
 //     conflict-free), and all eight waves read their MFMA A fragments from there;
 //   * the eight waves form four pairs; a pair owns 32 weight rows (two 16-row n-tiles), stages them
-//     through LDS and splits each stage's K range in halves, one per wave.  A wave decodes with
-//     the policies the small-M kernel uses (exact fp16 integers, fp32 scales) and reuses each B
-//     fragment for its MT m-tiles; the two halves' accumulators are added through LDS at the end;
+//     through LDS and splits each stage's K range in halves, one per wave.  Up to 16 rows a wave
+//     decodes with the policies the small-M kernel uses (exact fp16 integers, fp32 scales applied
+//     per block to the MFMA results); with 32 x 32 tiles (more than 16 rows) it folds the scales
+//     into the operand (w * 2^k rounded to fp16, k per weight row and K half; measured at
+//     K = N = 4096 against the exact form: 3-7% faster at 64 rows, 5-27% at 256, relative
+//     Frobenius error 2-4e-4 of a float64 product).  Each B fragment feeds the MT m-tiles; the two
+//     halves' accumulators are added through LDS at the end;
 //   * the next stage's activations and weights are in flight while a stage is computed;
 //   * above 64 rows the grid's z dimension holds m-tiles of 64 rows, each decoding the weight
 //     again (measured at K = N = 4096: 2x faster than decoding the weight once to fp16 and running
@@ -238,81 +242,51 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
         for (int r = 0; r < 16; ++r) acc32[i][r] = 0.f;
     const uint8_t* srow32 = my + r32 * RS;
     const uint8_t* xrow32 = xs + r32 * XRS + 16 * h32;
-    auto bfrag = [&](int blk, int v0, auto&&... sc) {
+    // The B operand in the folded form: w * f rounded to fp16, f = 2^(15 - e) with |w| < 2^e over
+    // this wave's half of the stage for weight row r32 (both lanes of the row derive the same e),
+    // so that one MFMA chain runs over the whole half and the result is scaled back once.  Per
+    // 16-value step this replaces a block-scale multiply of every accumulator (and, with block
+    // minima, a second MFMA against the minima) by 4 packed fp16 multiplies of the operand.
+    auto bfragf = [&](int blk, int v0, float f) {
         if constexpr (VPL == 8) {
-            return F::get(srow32, blk * TS, v0, sc...);
+            return F::getf(srow32, blk * TS, v0, f);
         } else {
-            const f16x4 lo = F::get(srow32, blk * TS, v0, sc...), hi = F::get(srow32, blk * TS, v0 + 4, sc...);
+            const f16x4 lo = F::getf(srow32, blk * TS, v0, f), hi = F::getf(srow32, blk * TS, v0 + 4, f);
             return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
     };
     auto mfma32 = [](f16x8 a, f16x8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); };
     constexpr int STEPS = UNIT / 16;
     auto compute32 = [&]<int H>() {
-        const f16x8 ones8 = {(f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f, (f16)1.0f};
-        if constexpr (F::KIND == 0) {
+        constexpr int U0 = H * UH, B0 = U0 * UNIT / QK, B1 = ((U0 + UH) * UNIT - 1) / QK;
+        float bnd = 0.f;
 #pragma unroll
-            for (int uu = 0; uu < UH; ++uu) {
-                const int u = H * UH + uu;
-                const int blk = (u * UNIT) / QK;
-                f32x16 c[MT], c1[MT];
+        for (int blk = B0; blk <= B1; ++blk) bnd = fmaxf(bnd, F::bound(srow32, blk * TS));
+        const int e = __builtin_amdgcn_frexp_expf(bnd);  // bnd < 2^e
+        const float f = __builtin_ldexpf(1.0f, 15 - e);
+        f32x16 c[MT];
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) c[mt][r] = c1[mt][r] = 0.f;
-                float a = 0.f, b = 0.f;
+            for (int r = 0; r < 16; ++r) c[mt][r] = 0.f;
 #pragma unroll
-                for (int s = 0; s < STEPS; ++s) {
-                    const f16x8 bf = bfrag(blk, (u * UNIT) % QK + 16 * s + 8 * h32, a, b);
+        for (int uu = 0; uu < UH; ++uu) {
+            const int u = U0 + uu, blk = u * UNIT / QK;
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const f16x8 af = *reinterpret_cast<const f16x8*>(xrow32 + mt * 32 * XRS + 2 * (u * UNIT + 16 * s));
-                        c[mt] = mfma32(af, bf, c[mt]);
-                        if constexpr (F::MIN) c1[mt] = mfma32(af, ones8, c1[mt]);
-                    }
+            for (int s = 0; s < STEPS; ++s) {
+                const f16x8 bf = bfragf(blk, (u * UNIT) % QK + 16 * s + 8 * h32, f);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const f16x8 af = *reinterpret_cast<const f16x8*>(xrow32 + mt * 32 * XRS + 2 * (u * UNIT + 16 * s));
+                    c[mt] = mfma32(af, bf, c[mt]);
                 }
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        acc32[mt][r] += F::MIN ? a * c[mt][r] + b * c1[mt][r] : a * c[mt][r];
-            }
-        } else {
-            constexpr int U0 = H * UH;
-#pragma unroll
-            for (int blk = U0 / UPB; blk <= (U0 + UH - 1) / UPB; ++blk) {
-                f32x16 c1[MT], c2[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) c1[mt][r] = c2[mt][r] = 0.f;
-                const int ua = max(U0, blk * UPB), ub = min(U0 + UH, (blk + 1) * UPB);
-#pragma unroll
-                for (int u = ua; u < ub; ++u)
-#pragma unroll
-                    for (int s = 0; s < STEPS; ++s) {
-                        f16 mv;
-                        const f16x8 bf = bfrag(blk, (u - blk * UPB) * UNIT + 16 * s + 8 * h32, mv);
-                        const f16x8 bm = {mv, mv, mv, mv, mv, mv, mv, mv};
-#pragma unroll
-                        for (int mt = 0; mt < MT; ++mt) {
-                            const f16x8 af =
-                                *reinterpret_cast<const f16x8*>(xrow32 + mt * 32 * XRS + 2 * (u * UNIT + 16 * s));
-                            c1[mt] = mfma32(af, bf, c1[mt]);
-                            if constexpr (F::MIN) c2[mt] = mfma32(af, bm, c2[mt]);
-                        }
-                    }
-                float d, dmin;
-                F::block(srow32, blk * TS, d, dmin);
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        acc32[mt][r] += d * c1[mt][r];
-                        if constexpr (F::MIN) acc32[mt][r] -= dmin * c2[mt][r];
-                    }
             }
         }
+        const float inv = __builtin_ldexpf(1.0f, e - 15);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc32[mt][r] = __builtin_fmaf(c[mt][r], inv, acc32[mt][r]);
     };
 
 #pragma unroll

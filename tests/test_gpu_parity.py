@@ -424,6 +424,49 @@ def test_gguf_linear_large_activations_near_max_scales():
     assert np.isfinite(got.cpu().numpy()).all() and rel < REL_TOL
 
 
+SCALE_FIELDS = {"Q8_0": [0], "Q4_0": [0], "Q4_1": [0, 2], "Q5_1": [0, 2], "IQ4_NL": [0], "IQ4_XS": [0],
+                "Q4_K": [0, 2], "Q5_K": [0, 2], "Q6_K": [208], "Q2_K": [80, 82], "Q3_K": [108]}
+
+
+@pytest.mark.parametrize("m", [40, 100])
+@pytest.mark.parametrize("name", list(SCALE_FIELDS))
+def test_gguf_linear_folded_scale_ranges(name, m):
+    """Above 16 rows the split kernel folds block scales into fp16 operands with a power of two per
+    weight row and K half.  Weight rows whose fp16 block scales are all subnormal, mix 6e4 with
+    1e-3 and subnormals in one half, are all zero, or are ordinary: every output column within the
+    bar of its own fp64 product (a missing or misplaced exponent loses the small rows' precision
+    or overflows the large ones), zero rows exactly zero."""
+    n, k = 128, 2048
+    _, qk, ts = O.GGUF_TYPES[name]
+    raw = random_gguf_blocks(name, n, k, seed=17).reshape(n, -1, ts)
+    rng = np.random.default_rng(5)
+    for r in range(n):
+        kind = r % 4
+        for b in range(raw.shape[1]):
+            if kind == 0:    # all subnormal: |w| far below fp16's normal range
+                v = float(rng.choice([6e-8, -3e-7, 2e-6, 1.5e-5]))
+            elif kind == 1:  # a huge, a small and a subnormal scale in the same K half
+                v = float([60000.0, 1e-3, -4e-7, 250.0][b % 4])
+            elif kind == 2:
+                continue
+            else:
+                v = 0.0
+            for off in SCALE_FIELDS[name]:
+                raw[r, b, off:off + 2] = np.array([v], np.float16).view(np.uint8)
+    raw = raw.reshape(n, -1)
+    w = O.gguf_dequantize(raw, name, (n, k)).astype(np.float64)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).half()
+    want = x.double().numpy() @ w.T
+    got = qlin().gguf_linear(x.to(DEV), torch.from_numpy(raw).to(DEV), name, (n, k),
+                             out_dtype=torch.float32).double().cpu().numpy()
+    assert np.isfinite(got).all()
+    zero = np.abs(w).max(axis=1) == 0
+    assert zero[3::4].all() and not got[:, zero].any()
+    for c in np.flatnonzero(~zero):
+        rel = np.linalg.norm(got[:, c] - want[:, c]) / np.linalg.norm(want[:, c])
+        assert rel < REL_TOL, f"{name} M={m} row {c} (kind {c % 4}): rel_fro {rel:.3e}"
+
+
 def test_gguf_linear_shapes_and_empty():
     Q = qlin()
     name, n, k = "Q4_0", 48, 256
