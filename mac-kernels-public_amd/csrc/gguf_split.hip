@@ -11,13 +11,12 @@
 //     1024 contiguous bytes per row, into LDS (rows padded by 16 bytes so the fragment reads are
 //     conflict-free), and all eight waves read their MFMA A fragments from there;
 //   * the eight waves form four pairs; a pair owns 32 weight rows (two 16-row n-tiles), stages them
-//     through LDS and splits each stage's K range in halves, one per wave.  Up to 16 rows a wave
-//     decodes with the policies the small-M kernel uses (exact fp16 integers, fp32 scales applied
-//     per block to the MFMA results); with 32 x 32 tiles (more than 16 rows) it folds the scales
-//     into the operand (w * 2^k rounded to fp16, k per weight row and K half; measured at
-//     K = N = 4096 against the exact form: 3-7% faster at 64 rows, 5-27% at 256, relative
-//     Frobenius error 2-4e-4 of a float64 product).  Each B fragment feeds the MT m-tiles; the two
-//     halves' accumulators are added through LDS at the end;
+//     through LDS and splits each stage's K range in halves, one per wave.  A wave folds the block
+//     scales into its fp16 B operand (w * 2^k rounded to fp16, k per weight row and K half) instead
+//     of applying them per block to the MFMA results (measured at K = N = 4096 against that exact
+//     form: 3-7% faster at 64 rows, 5-27% at 256, Q6_K 6% at 5-16 rows; relative Frobenius error
+//     2-4e-4 of a float64 product).  Each B fragment feeds the MT m-tiles; the two halves'
+//     accumulators are added through LDS at the end;
 //   * the next stage's activations and weights are in flight while a stage is computed;
 //   * above 64 rows the grid's z dimension holds m-tiles of 64 rows, each decoding the weight
 //     again (measured at K = N = 4096: 2x faster than decoding the weight once to fp16 and running
@@ -145,87 +144,48 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < MT; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    V ones;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) ones[i] = (f16)1.0f;
-
     const uint8_t* srow[2] = {my + nl * RS, my + (16 + nl) * RS};
     const uint8_t* xrow = xs + nl * XRS + 2 * VPL * g;  // A fragment: row mt * 16 + nl, values VPL*g.. of a unit
 
-    // This wave's half of a stage: units H * UH .. H * UH + UH - 1.
+    // This wave's half of a stage (units H * UH .. H * UH + UH - 1) on 16 x 16 tiles, in the folded
+    // form described at the 32 x 32 path below: lane (nl, g) holds weight row nl of n-tile t in its
+    // B operand and column nl of n-tile t in its accumulators, so one power of two per (lane, t).
     auto compute = [&]<int H>() {
-        if constexpr (F::KIND == 0) {
+        constexpr int U0 = H * UH, B0 = U0 * UNIT / QK, B1 = ((U0 + UH) * UNIT - 1) / QK;
+        int e[2];
+        float f[2];
+        f32x4 c[2][MT];
 #pragma unroll
-            for (int uu = 0; uu < UH; ++uu) {
-                const int u = H * UH + uu;
-                const int blk = (u * UNIT) / QK;
-                const int v0 = (u * UNIT) % QK + VPL * g;
-                float a[2], b[2];
-                V bf[2];
+        for (int t = 0; t < 2; ++t) {
+            float bnd = 0.f;
 #pragma unroll
-                for (int t = 0; t < 2; ++t) bf[t] = F::get(srow[t], blk * TS, v0, a[t], b[t]);
+            for (int blk = B0; blk <= B1; ++blk) bnd = fmaxf(bnd, F::bound(srow[t], blk * TS));
+            e[t] = __builtin_amdgcn_frexp_expf(bnd);
+            f[t] = __builtin_ldexpf(1.0f, 15 - e[t]);
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const V af = *reinterpret_cast<const V*>(xrow + mt * 16 * XRS + 2 * UNIT * u);
-                    f32x4 c1 = f32x4{0.f, 0.f, 0.f, 0.f};
-                    if constexpr (F::MIN) c1 = mfma16<VPL>(af, ones, c1);
+            for (int mt = 0; mt < MT; ++mt) c[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const f32x4 c = mfma16<VPL>(af, bf[t], f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int uu = 0; uu < UH; ++uu) {
+            const int u = U0 + uu, blk = u * UNIT / QK, v0 = (u * UNIT) % QK + VPL * g;
+            V bf[2];
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (i < ilim) acc[t][mt][i] += F::MIN ? a[t] * c[i] + b[t] * c1[i] : a[t] * c[i];
-                    }
-                }
+            for (int t = 0; t < 2; ++t) bf[t] = F::getf(srow[t], blk * TS, v0, f[t]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const V af = *reinterpret_cast<const V*>(xrow + mt * 16 * XRS + 2 * UNIT * u);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) c[t][mt] = mfma16<VPL>(af, bf[t], c[t][mt]);
             }
-        } else {
-            constexpr int U0 = H * UH;
+        }
 #pragma unroll
-            for (int blk = U0 / UPB; blk <= (U0 + UH - 1) / UPB; ++blk) {
-                f32x4 c1[2][MT], c2[2][MT];
+        for (int t = 0; t < 2; ++t) {
+            const float inv = __builtin_ldexpf(1.0f, e[t] - 15);
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        c1[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                        c2[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    }
-                const int ua = max(U0, blk * UPB), ub = min(U0 + UH, (blk + 1) * UPB);
-#pragma unroll
-                for (int u = ua; u < ub; ++u) {
-                    const int v0 = (u - blk * UPB) * UNIT + VPL * g;
-                    V bf[2], bm[2];
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        f16 mv;
-                        bf[t] = F::get(srow[t], blk * TS, v0, mv);
-#pragma unroll
-                        for (int i = 0; i < VPL; ++i) bm[t][i] = mv;
-                    }
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const V af = *reinterpret_cast<const V*>(xrow + mt * 16 * XRS + 2 * UNIT * u);
-#pragma unroll
-                        for (int t = 0; t < 2; ++t) {
-                            c1[t][mt] = mfma16<VPL>(af, bf[t], c1[t][mt]);
-                            if constexpr (F::MIN) c2[t][mt] = mfma16<VPL>(af, bm[t], c2[t][mt]);
-                        }
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    float d, dmin;
-                    F::block(srow[t], blk * TS, d, dmin);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (i < ilim) {
-                                acc[t][mt][i] += d * c1[t][mt][i];
-                                if constexpr (F::MIN) acc[t][mt][i] -= dmin * c2[t][mt][i];
-                            }
-                }
-            }
+                for (int i = 0; i < 4; ++i)
+                    if (i < ilim) acc[t][mt][i] = __builtin_fmaf(c[t][mt][i], inv, acc[t][mt][i]);
         }
     };
 

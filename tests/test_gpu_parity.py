@@ -428,11 +428,11 @@ SCALE_FIELDS = {"Q8_0": [0], "Q4_0": [0], "Q4_1": [0, 2], "Q5_1": [0, 2], "IQ4_N
                 "Q4_K": [0, 2], "Q5_K": [0, 2], "Q6_K": [208], "Q2_K": [80, 82], "Q3_K": [108]}
 
 
-@pytest.mark.parametrize("m", [40, 100])
+@pytest.mark.parametrize("m", [8, 40, 100])
 @pytest.mark.parametrize("name", list(SCALE_FIELDS))
 def test_gguf_linear_folded_scale_ranges(name, m):
-    """Above 16 rows the split kernel folds block scales into fp16 operands with a power of two per
-    weight row and K half.  Weight rows whose fp16 block scales are all subnormal, mix 6e4 with
+    """The split kernel (Q6_K from 5 rows, every format from 17) folds block scales into fp16
+    operands with a power of two per weight row and K half.  Weight rows whose fp16 block scales are all subnormal, mix 6e4 with
     1e-3 and subnormals in one half, are all zero, or are ordinary: every output column within the
     bar of its own fp64 product (a missing or misplaced exponent loses the small rows' precision
     or overflows the large ones), zero rows exactly zero."""
