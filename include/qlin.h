@@ -156,7 +156,7 @@ qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata
 /* qlin_gguf_linear with unmerged LoRA in the epilogue: t = x @ lora_down^T (fp32, in the workspace),
  * then the K-split reduction of the split kernel adds lora_scale * t @ lora_up^T to each output tile
  * in fp32 after the bias and rounds once into y.  Taken from 17 rows to the split kernel's limit
- * (512 rows; 256 for Q2_K, Q3_K, Q6_K) where K holds at least two of its stages (the call then splits
+ * (512 rows) where K holds at least two of its stages (the call then splits
  * K at least in two), for a rank that is a multiple of 8 up to 128 with 16-byte aligned lora_up rows;
  * other calls return QLIN_EUNSUPPORTED before launching anything, and the caller runs the plain
  * linear and qlin_lora_apply_base.  Workspace: qlin_workspace_size(QLIN_OP_GGUF_LINEAR_LORA, M, N, K,

@@ -155,10 +155,10 @@ constexpr int64_t INT8_SMALLM_MAX_M = 16;
 int64_t gguf_split_min_m(int type) { return type == gguf::Q6_K ? 5 : 17; }
 // Largest M of the split kernel, whose 64-row m-tiles decode the weight in the load stage (above
 // it: the weight decoded once to fp16, then the fp16-weight GEMM).  Measured at K = N = 4096: the
-// split kernel is 2x faster at 65-128 rows and 1.1-1.3x at 512 rows (one round of 256 workgroups),
-// slower from 640 rows on (a second round); Q6_K, whose 16-value units cost more to decode per
-// m-tile, is 1.16x faster at 256 rows and slower at 384.
-int64_t gguf_fused_max_m(int type) { return (type == gguf::Q6_K || type == gguf::Q3_K || type == gguf::Q2_K) ? 256 : 512; }
+// split kernel is 2x faster at 65-128 rows and 1.1-1.3x at 512 rows (one round of 256 workgroups;
+// Q2_K, Q3_K, Q6_K 1.13-1.28x at 512 with the block scales folded into the operand), slower from
+// 640 rows on (a second round) for every format.
+int64_t gguf_fused_max_m(int) { return 512; }
 
 // K splits of the shared-activation kernel for this call, 0 when another kernel takes it.
 int gguf_split_for(int type, int64_t M, int64_t N, int64_t K) {
@@ -903,7 +903,7 @@ qlin_status qlin_gguf_linear_lora(const qlin_tensor* x, const void* weight, int 
     a.lora.up = U.data; a.lora.up_dt = U.dtype; a.lora.ld_up = U.ld; a.lora.R = R; a.lora.scale = lora_scale;
     if (S < 2 || !gguf_split_fuses_lora(a) || (uintptr_t)workspace % 16)
         return fail(QLIN_EUNSUPPORTED, "the GGUF LoRA term is fused only into the split kernel's reduction (17 to 512 "
-                                       "rows, 256 for Q2_K/Q3_K/Q6_K, K of two stages or more, a 4-byte aligned weight), "
+                                       "rows, K of two stages or more, a 4-byte aligned weight), "
                                        "for a rank that is a multiple of 8 up to 128 with 16-byte aligned lora_up rows");
     const size_t need = align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
                         align_up((size_t)S * M * N * 4) + ws_lora(M, K, R);

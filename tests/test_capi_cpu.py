@@ -52,8 +52,8 @@ def test_query_and_workspace():
 def test_workspace_sizes_follow_the_paths():
     """The sizes the C ABI asks for: the A8 int8 grid (N*K bytes) only where the call decodes the
     weight once (from 512 rows, with a group size that is a multiple of 64; counted when the group
-    size is not given), and the GGUF decoded fp16 copy above the split kernel's 512 rows (256 for
-    Q6_K), capped at 256 MiB; the split kernel's fp32 partials where it splits K."""
+    size is not given), and the GGUF decoded fp16 copy above the split kernel's 512 rows, capped at
+    256 MiB; the split kernel's fp32 partials where it splits K."""
     from qlin import _lib
     L = _lib.load()
     a = lambda v: (v + 255) // 256 * 256
@@ -79,7 +79,8 @@ def test_workspace_sizes_follow_the_paths():
     assert g(512, 4096) == base(512, 4096)
     assert g(384, 4096) == base(384, 4096)           # 192 tiles, 3/4 of the GPU: one split
     assert g(256, 4096) == base(256, 4096) + a(2 * 256 * 4096 * 4)  # 128 tiles: two splits
-    assert g(512, 4096, 14) == base(512, 4096) + a(4096 * 4096 * 2)  # Q6_K: the split kernel to 256 rows
+    assert g(512, 4096, 14) == base(512, 4096)       # Q6_K: the split kernel to 512 rows as well
+    assert g(520, 4096, 14) == base(520, 4096) + a(4096 * 4096 * 2)
 
 
 def _d(t, dt=None):

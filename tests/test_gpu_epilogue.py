@@ -203,11 +203,12 @@ def test_w4a8_residual_fused_equals_separate(m, n, k, bits, gs):
     ("Q4_0", 64, 1000, 2048),   # split kernel, 8 splits
     ("Q8_0", 65, 1000, 2048),   # split kernel, two m-tiles (the second one row)
     ("Q5_K", 512, 4096, 1024),  # split kernel, 256 tiles, one split: the kernel's own epilogue
-    ("Q6_K", 512, 1000, 2048),  # the GEMM over the decoded weight
+    ("Q6_K", 600, 1000, 2048),  # the GEMM over the decoded weight
+    ("Q6_K", 300, 1000, 2048),  # split kernel, 5 m-tiles
     ("IQ4_XS", 8, 1000, 2048),  # small-M kernel, then the residual kernel
 ])
 def test_gguf_residual_fused_equals_separate(name, m, n, k):
-    """From 17 to 512 rows (Q6_K 5 to 256) the split kernel, or its reduction, applies the residual;
+    """From 17 to 512 rows (Q6_K from 5) the split kernel, or its reduction, applies the residual;
     above, the GEMM over the decoded weight; fewer rows take the weight-streaming kernels and the
     residual kernel after them.  Every route gives the bits of the separate residual kernel."""
     Q = qlin()

@@ -346,11 +346,11 @@ def test_gguf_lora_fused_into_split(name, m, n, k, r, fdt, fused_calls):
     check_full(y, want, f"{name} fused full m={m} r={r}")
 
 
-@pytest.mark.parametrize("name,m,r", [("Q4_K", 16, 16), ("Q4_K", 600, 16), ("Q4_K", 64, 136), ("Q6_K", 300, 16),
+@pytest.mark.parametrize("name,m,r", [("Q4_K", 16, 16), ("Q4_K", 600, 16), ("Q4_K", 64, 136), ("Q6_K", 520, 16),
                                       ("Q4_K", 64, 12)])
 def test_gguf_lora_declines_to_the_separate_kernels(name, m, r, fused_calls):
-    """16 rows or fewer (the GEMV and small-M kernels), past the split kernel's rows (Q4_K 512, Q6_K
-    256: the GEMM over the decoded weight), rank above 128 or not a multiple of 8: the fused entry
+    """16 rows or fewer (the GEMV and small-M kernels), past the split kernel's 512 rows (the GEMM
+    over the decoded weight), rank above 128 or not a multiple of 8: the fused entry
     point declines before launching and the separate kernels give the result."""
     Q = qlin()
     from gguf_blocks import random_gguf_blocks

@@ -133,7 +133,7 @@ def test_gguf_linear(name, m):
     ("Q4_K", 33, 131, 256),     # one K stage: single split, epilogue in the kernel, ragged N
     ("Q4_0", 64, 131, 1280),    # five splits, N % 4 != 0 in the reduction
     ("Q8_0", 20, 12800, 1280),  # 100 row tiles: three splits over five stages (uneven)
-    ("Q3_K", 64, 200, 2048),    # two-block stages, sub-block minimum MFMA
+    ("Q3_K", 64, 200, 2048),    # two-block stages, signed sub-scales
     ("Q2_K", 40, 136, 1024),    # four splits, 16-value units with minimums
     ("IQ4_XS", 47, 256, 4096),  # eight splits
     # N a multiple of 1024: each row block's partials are added by workgroups of the XCD that wrote them
@@ -161,11 +161,14 @@ def test_gguf_linear_split_k(name, m, n, k):
     ("IQ4_XS", 300, 4096, 512), # 32 x 5 tiles, 2 splits
     ("Q4_0", 384, 4096, 1024),  # 32 x 6 tiles, 3/4 of the GPU: one split
     ("Q5_K", 512, 4096, 1024),  # 32 x 8 tiles: one split, the epilogue in the kernel
-    ("Q3_K", 130, 200, 1024),   # sub-block minimum MFMA across three m-tiles
+    ("Q3_K", 130, 200, 1024),   # signed sub-scales across three m-tiles
     ("Q2_K", 193, 136, 512),    # 16-value units, four m-tiles, the last one row
+    ("Q6_K", 450, 1024, 1024),  # 8 x 8 tiles, 2 splits
+    ("Q3_K", 512, 2048, 1024),  # 16 x 8 tiles, 2 splits
+    ("Q2_K", 400, 300, 512),    # 3 x 7 tiles, the last m-tile 16 rows
 ])
 def test_gguf_linear_split_m_tiles(name, m, n, k):
-    """From 65 to 512 rows (Q2_K, Q3_K, Q6_K: 256) the split kernel runs 64-row m-tiles along the
+    """From 65 to 512 rows the split kernel runs 64-row m-tiles along the
     grid's z, each decoding the weight in its load stage: ragged M and N, single and multiple splits,
     bias; no decoded copy is asked for."""
     from qlin import _lib
