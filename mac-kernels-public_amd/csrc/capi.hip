@@ -227,6 +227,10 @@ size_t ws_lora(int64_t M, int64_t K, int64_t R) {
     const int S = lora_splits(M, K, R);
     return align_up((size_t)(S > 1 ? S + 1 : 1) * M * (size_t)(R > 0 ? R : 0) * 4);
 }
+// A GGUF call's t: ws_lora for the separate down kernel, or the split kernel's own S partials.
+size_t ws_gguf_lora_t(int64_t M, int64_t K, int64_t R, int S) {
+    return std::max(ws_lora(M, K, R), align_up((size_t)std::max(S, 1) * M * (size_t)(R > 0 ? R : 0) * 4));
+}
 
 // LoRA operands of a fused linear call (qlin_int8_linear_lora, qlin_w4a8_linear_lora).
 struct LoraIn {
@@ -354,7 +358,7 @@ size_t qlin_workspace_size(int op, int64_t M, int64_t N, int64_t K, int param, i
         case QLIN_OP_GGUF_LINEAR_LORA: {  // param: ggml type | R << 8
             const int S = gguf_lora_splits(param & 0xFF, M, N, K);
             return align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
-                   align_up((size_t)std::max(S, 1) * M * N * 4) + ws_lora(M, K, param >> 8);
+                   align_up((size_t)std::max(S, 1) * M * N * 4) + ws_gguf_lora_t(M, K, param >> 8, S);
         }
         // the residual variants: the linear's workspace, then room for its fp32 output when the
         // call's kernel does not apply the residual itself
@@ -906,16 +910,26 @@ qlin_status qlin_gguf_linear_lora(const qlin_tensor* x, const void* weight, int 
                                        "rows, K of two stages or more, a 4-byte aligned weight), "
                                        "for a rank that is a multiple of 8 up to 128 with 16-byte aligned lora_up rows");
     const size_t need = align_up((size_t)(M * K * 2)) + align_up((size_t)M * 4) + align_up((size_t)N * 4) +
-                        align_up((size_t)S * M * N * 4) + ws_lora(M, K, R);
+                        align_up((size_t)S * M * N * 4) + ws_gguf_lora_t(M, K, R, S);
     if (workspace_bytes < need) return fail(QLIN_EWORKSPACE, "workspace %zu < %zu", workspace_bytes, need);
     if (M == 0 || N == 0) return QLIN_OK;
     hipStream_t st = (hipStream_t)stream;
     Carver ws{(uint8_t*)workspace, workspace_bytes};
-    float* t = (float*)ws.take(ws_lora(M, K, R));
-    const float* tf = nullptr;
-    if ((s = hip_status(run_lora_t(lora_down_args(X, D, t), st, &tf), "lora down"))) return s;
-    a.lora.t = tf;
+    float* t = (float*)ws.take(ws_gguf_lora_t(M, K, R, S));
+    // t = x down^T: by the split kernel itself from the activation slices it stages (its S partials,
+    // added and scaled by the row exponents in the reduction), or by the separate down kernel first
+    const int NR = gguf_split_down_ranks(a, (int)R, D.dtype, D.ld, D.data);
+    if (!NR) {
+        const float* tf = nullptr;
+        if ((s = hip_status(run_lora_t(lora_down_args(X, D, t), st, &tf), "lora down"))) return s;
+        a.lora.t = tf;
+    }
     if ((s = wo_activations(X, 0, ws, st, a.x, a.ldx, a.xexp))) return s;
+    if (NR) {
+        a.down.down = D.data; a.down.dt = D.dtype; a.down.ld = D.ld; a.down.R = (int)R; a.down.NR = NR;
+        a.down.tpart = t;
+        a.lora.t = t; a.lora.t_parts = S; a.lora.t_stride = M * R; a.lora.t_exp = a.xexp;
+    }
     a.part = (float*)ws.take((size_t)S * M * N * 4);
     return hip_status(run_gguf_split(a, st), "gguf split-K with LoRA");
 }

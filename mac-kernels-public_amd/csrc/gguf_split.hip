@@ -40,12 +40,12 @@ constexpr int SP_ROWS = 16 * SP_WAVES;  // weight rows per workgroup
 constexpr int SP_TARGET_BLOCKS = 256;   // one workgroup per CU
 constexpr int SP_MAX_SPLITS = 8;        // partial tiles added by the reduction kernel
 
-template <int T, int MT, bool W32>
+template <int T, int MT, bool W32, bool LD>
 __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     const f16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ xexp,
     const uint8_t* __restrict__ w, int64_t row_bytes, int N, int K, int S,
     const void* __restrict__ bias, int bias_dt, void* __restrict__ y, int y_dt, int64_t ldy,
-    float* __restrict__ part, ResidualTile res) {
+    float* __restrict__ part, ResidualTile res, LoraDownRows dn) {
     using F = SM<T>;
     constexpr int QK = F::QK, TS = F::TS, UNIT = F::UNIT, VPL = UNIT / 4, SBLK = F::SBLK;
     constexpr int SV = SBLK * QK;                    // values per stage
@@ -72,6 +72,9 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
 
     __shared__ __attribute__((aligned(16))) uint8_t xs[XR * XRS];
     __shared__ __attribute__((aligned(16))) uint8_t wsm[SP_ROWS * RS];
+    // LD: this workgroup's LoRA down rows for the stage (NR <= 2 rows of SV values, f32 at most)
+    constexpr int DSM = LD ? 2 * SV * 4 : 16;
+    __shared__ __attribute__((aligned(16))) uint8_t dsm[DSM];
 
     // Waves 0..3 and 4..7 cover the first and second half of every stage's units; wave w % 4 of
     // each half owns weight rows 32 (w % 4) .. + 31 of the tile (two n-tiles), so every activation
@@ -136,6 +139,61 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
             const int u = unit_of(i), r = u / UPR;
             const int off = min((u - r * UPR) * 16, RSB - 16);
             *reinterpret_cast<LU*>(my + r * RS + off) = src[i];
+        }
+    };
+    // LD: the stage's slice of this workgroup's down rows, 16 bytes per thread (NR * SV * es bytes,
+    // at most SP_THREADS pieces); row j is rank blockIdx.x + gridDim.x * j (past R: rank R - 1, never
+    // stored).
+    const int des = LD && dn.dt == DT_F32 ? 4 : 2;
+    const int dpieces = LD ? dn.NR * SV * des / 16 : 0;
+    u32x4 dq[PF];
+    auto issue_d = [&](int st, u32x4& dst) {
+        if constexpr (LD) {
+            if (tid < dpieces) {
+                const int j = tid * 16 / (SV * des), o = tid * 16 - j * SV * des;
+                const int64_t r = min((int)blockIdx.x + (int)gridDim.x * j, dn.R - 1);
+                dst = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(dn.down) +
+                                                      (r * dn.ld + (int64_t)min(st, last) * SV) * des + o);
+            }
+        }
+    };
+    auto commit_d = [&](const u32x4& src) {
+        if constexpr (LD) {
+            if (tid < dpieces) *reinterpret_cast<u32x4*>(dsm + tid * 16) = src;
+        }
+    };
+    // LD: thread (pair p = tid / TPP, part kc = tid % TPP) sums x[m] . down[j] over values
+    // kc * KCN .. + KCN - 1 of each stage, m = p % XR, j = p / XR; the TPP parts meet by xor
+    // shuffles at the end (fixed order).
+    const int tpp = LD ? SP_THREADS / (XR * max(dn.NR, 1)) : 1, kcn = SV / tpp;
+    const int dkc = tid % tpp, dp = tid / tpp, dm = dp % XR, dj = dp / XR;
+    float tacc = 0.f;
+    auto down_dot = [&]() {
+        if constexpr (LD) {
+            const uint8_t* xp = xs + dm * XRS + 2 * dkc * kcn;
+            const uint8_t* dq8 = dsm + ((int64_t)dj * SV + dkc * kcn) * des;
+            for (int i = 0; i < kcn; i += 8) {
+                const f16x8 xv = *reinterpret_cast<const f16x8*>(xp + 2 * i);
+                float dv[8];
+                if (dn.dt == DT_F32) {
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(dq8 + 4 * i);
+                    const f32x4 b = *reinterpret_cast<const f32x4*>(dq8 + 4 * i + 16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dv[e] = a[e];
+                        dv[4 + e] = b[e];
+                    }
+                } else {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(dq8 + 2 * i);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dv[2 * e] = bits_to_f32_rt(a[e] & 0xFFFFu, dn.dt);
+                        dv[2 * e + 1] = bits_to_f32_rt(a[e] >> 16, dn.dt);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) tacc = __builtin_fmaf((float)xv[e], dv[e], tacc);
+            }
         }
     };
 
@@ -253,6 +311,7 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
     for (int j = 0; j < PF; ++j) {
         issue_x(st0 + j, xq[j]);
         issue_w(st0 + j, pf[j]);
+        issue_d(st0 + j, dq[j]);
     }
     for (int c0 = st0; c0 < st1; c0 += PF)
 #pragma unroll
@@ -262,9 +321,11 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
         lds_barrier();  // every wave is done with the previous stage's LDS
         commit_x(xq[jp]);
         commit_w(pf[jp]);
+        commit_d(dq[jp]);
         if (st + PF < st1) {  // refill the freed registers with the stage PF ahead (uniform branch)
             issue_x(st + PF, xq[jp]);
             issue_w(st + PF, pf[jp]);
+            issue_d(st + PF, dq[jp]);
         }
         __builtin_amdgcn_sched_barrier(0);  // the next stages' loads stay ahead of this stage's math
         lds_barrier();  // this stage is in LDS
@@ -275,6 +336,12 @@ __global__ __launch_bounds__(SP_THREADS) void gguf_split_kernel(
             if (kh == 0) compute.template operator()<0>();
             else compute.template operator()<1>();
         }
+        down_dot();
+    }
+    if constexpr (LD) {
+        for (int o = tpp / 2; o >= 1; o /= 2) tacc += __shfl_xor(tacc, o, 64);
+        const int r = (int)blockIdx.x + (int)gridDim.x * dj;
+        if (dkc == 0 && dm < M && r < dn.R) dn.tpart[((int64_t)split * Mall + m0 + dm) * dn.R + r] = tacc;
     }
 
     // The two K halves meet in LDS (reusing the activation buffer) in a fixed order, and the
@@ -480,14 +547,23 @@ hipError_t launch_t(const GgufSplitArgs& a, hipStream_t st) {
     // above 64 rows: m-tiles of 64 rows (32 x 32 MFMA tiles) along the grid's z
     dim3 grid((unsigned)((a.N + SP_ROWS - 1) / SP_ROWS), (unsigned)a.S, (unsigned)((a.M + 63) / 64)), block(SP_THREADS);
     float* part = a.S > 1 ? a.part : nullptr;
-#define QLIN_SP_LAUNCH(MTV, W32V)                                                                          \
-    hipLaunchKernelGGL((gguf_split_kernel<T, MTV, W32V>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
-                       a.row_bytes, a.N, a.K, a.S, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, part, a.res)
+#define QLIN_SP_LAUNCH(MTV, W32V, LDV)                                                                          \
+    hipLaunchKernelGGL((gguf_split_kernel<T, MTV, W32V, LDV>), grid, block, 0, st, a.x, a.ldx, a.M, a.xexp, a.w, \
+                       a.row_bytes, a.N, a.K, a.S, a.bias, a.bias_dtype, a.y, a.y_dtype, a.ldy, part, a.res, a.down)
     // 16-row m-tiles up to 16 rows, then 32 x 32 tiles (the 32 x 32 x 16 MFMA moves about 1.7x the
     // values per cycle of the 16 x 16 x 32 form)
-    if (a.M <= 16) QLIN_SP_LAUNCH(1, false);
-    else if (a.M <= 32) QLIN_SP_LAUNCH(1, true);
-    else QLIN_SP_LAUNCH(2, true);
+    const bool ld = a.down.down != nullptr;
+    if (ld && (a.M <= 16 || a.S < 2 || !a.down.tpart || a.down.NR < 1 || a.down.NR > 2 ||
+               (int64_t)grid.x * a.down.NR < a.down.R))
+        return hipErrorInvalidValue;
+    if (a.M <= 16) QLIN_SP_LAUNCH(1, false, false);
+    else if (a.M <= 32) {
+        if (ld) QLIN_SP_LAUNCH(1, true, true);
+        else QLIN_SP_LAUNCH(1, true, false);
+    } else {
+        if (ld) QLIN_SP_LAUNCH(2, true, true);
+        else QLIN_SP_LAUNCH(2, true, false);
+    }
 #undef QLIN_SP_LAUNCH
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || a.S == 1) return err;
@@ -553,6 +629,18 @@ int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_byte
                                                            SP_MAX_SPLITS));
     });
     return parts;
+}
+
+int gguf_split_down_ranks(const GgufSplitArgs& a, int R, int down_dt, int64_t ld_down, const void* down) {
+    // measured at K = N = 4096 (Q4_K, 4 calls per graph, against the separate down kernel): 2.5-4 us
+    // faster at 24-128 rows with 1 or 2 ranks per column and 4 or more splits; 1.5-4.7 us slower
+    // with 4 ranks per column (rank 128), and with 2 splits (256 rows and more: 6-43 us)
+    if (a.M <= 16 || a.S < 4 || !down || R < 1) return 0;
+    if (down_dt != DT_F32 && down_dt != DT_F16 && down_dt != DT_BF16) return 0;
+    const int es = down_dt == DT_F32 ? 4 : 2;
+    if ((uintptr_t)down % 16 || (ld_down * es) % 16) return 0;
+    const int64_t blocks = (a.N + SP_ROWS - 1) / SP_ROWS, nr = (R + blocks - 1) / blocks;
+    return nr <= 1 ? 1 : nr <= 2 ? 2 : 0;
 }
 
 bool gguf_split_fuses_lora(const GgufSplitArgs& a) {

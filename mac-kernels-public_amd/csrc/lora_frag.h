@@ -123,7 +123,8 @@ __device__ __forceinline__ void mfma_raw(const Raw8<DA>& ra, const Raw8<DB>& rb,
 // LoRA term of a GEMM workgroup's BMT x BNT output tile, added by its waves to accumulators that
 // already hold their fp32 base values (after bias).  The whole rank (R <= RC) is staged at once: all
 // NT threads load the tile's t rows [BMT x RC] (fp32) and up rows [BNT x RC] together (every load in
-// flight at once, zeros past R).  t is multiplied by L.scale and split into bf16 hi and lo on its
+// flight at once, zeros past R; t's K-split partials summed in split order and scaled by
+// 2^t_exp[m] where L asks for it).  t is multiplied by L.scale and split into bf16 hi and lo on its
 // way into LDS, once per workgroup; up goes in as loaded.  Each wave then takes its TJ column blocks
 // in turn: it reads (and, for f16 / f32, splits) the up fragments of the block once, and runs the
 // bf16 MFMAs hi.hi, lo.hi (and hi.lo) of (scale t) . up^T for each of its TI row blocks straight into
@@ -170,14 +171,31 @@ __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* l
     uint8_t* tl = lds + BMT * TBPR;
     uint8_t* us = lds + 2 * BMT * TBPR;
     const int r32 = lane & 31, h = lane >> 5;
-    u32x4 tv[TP][2], uv[UP];
+    float tv[TP][8];
+    u32x4 uv[UP];
     const int64_t ldt = L.ld_t ? L.ld_t : L.R;
 #pragma unroll
     for (int i = 0; i < TP; ++i) {
         const int p = tid + NT * i, row = p / (RC / 8), c = 8 * (p % (RC / 8));
         const int64_t m = min(m0 + row, M - 1), k = min<int64_t>(c, L.R - 8);
-        tv[i][0] = *reinterpret_cast<const u32x4*>(L.t + m * ldt + k);
-        tv[i][1] = *reinterpret_cast<const u32x4*>(L.t + m * ldt + k + 4);
+        const float* tp = L.t + m * ldt + k;
+        // K-split partials of t (at most 8), added in split order
+#pragma unroll
+        for (int sp = 0; sp < 8; ++sp) {
+            if (sp > 0 && sp >= L.t_parts) break;
+            const u32x4 a0 = *reinterpret_cast<const u32x4*>(tp + sp * L.t_stride);
+            const u32x4 a1 = *reinterpret_cast<const u32x4*>(tp + sp * L.t_stride + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                tv[i][e] = sp ? tv[i][e] + __uint_as_float(a0[e]) : __uint_as_float(a0[e]);
+                tv[i][4 + e] = sp ? tv[i][4 + e] + __uint_as_float(a1[e]) : __uint_as_float(a1[e]);
+            }
+        }
+        if (L.t_exp) {
+            const int e = L.t_exp[m];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) tv[i][q] = __builtin_ldexpf(tv[i][q], e);
+        }
     }
 #pragma unroll
     for (int i = 0; i < UP; ++i) {
@@ -191,10 +209,7 @@ __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* l
         const int p = tid + NT * i, row = p / (RC / 8), c = 8 * (p % (RC / 8));
         float v[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[e] = c < L.R ? __uint_as_float(tv[i][0][e]) * L.scale : 0.f;
-            v[4 + e] = c < L.R ? __uint_as_float(tv[i][1][e]) * L.scale : 0.f;
-        }
+        for (int e = 0; e < 8; ++e) v[e] = c < L.R ? tv[i][e] * L.scale : 0.f;
         bf16x8 hi, lo;
         split8(v, hi, lo);
         *reinterpret_cast<bf16x8*>(th + lora_chunk<TBPR>(row, c / 8)) = hi;

@@ -66,7 +66,9 @@ struct ResidualTile {
 
 // LoRA term added by a GEMM epilogue to its own output tile: y = dtype(base + scale * t up^T), t the
 // fp32 low-rank activation [M, R] (row stride R), up [N, R] (f32 / f16 / bf16, row stride ld_up).
-// t == nullptr: no LoRA term.
+// t == nullptr: no LoRA term.  With t_parts > 1, t holds that many K-split partials t_s [M, R]
+// (t_stride floats apart), added in split order when the tile loads them; with t_exp, row m of
+// the sum is scaled by 2^t_exp[m] (the row exponent of normalized activations).
 struct LoraTile {
     const float* t = nullptr;
     const void* up = nullptr;
@@ -75,6 +77,22 @@ struct LoraTile {
     int64_t R = 0;
     float scale = 1.0f;
     int64_t ld_t = 0;                // row stride of t (0: R)
+    int t_parts = 1;
+    int64_t t_stride = 0;
+    const int32_t* t_exp = nullptr;
+};
+
+// The LoRA down product computed by the GGUF split kernel from the activation slices it already
+// holds in LDS: t_s[m, r] = sum over split s's K range of x[m, k] down[r, k], fp32 partials
+// [S][M][R] (row stride R).  Workgroup column b (of ceil(N / 128)) takes ranks b, b + blocks, ...:
+// NR of them (1 or 2).  down: f32 / f16 / bf16 rows of 16-byte aligned 8-value pieces.
+struct LoraDownRows {
+    const void* down = nullptr;      // [R, K], row stride ld (elements); nullptr: no down product
+    int dt = DT_BF16;
+    int64_t ld = 0;
+    int R = 0;
+    int NR = 0;
+    float* tpart = nullptr;
 };
 
 struct GgufSplitArgs {
@@ -90,6 +108,7 @@ struct GgufSplitArgs {
     float* part = nullptr;           // S > 1: fp32 partials [S][M][N]
     ResidualTile res;                // y = r + rs * (linear + bias), in the kernel that writes y
     LoraTile lora;                   // + scale * t up^T in the reduction (gguf_split_fuses_lora)
+    LoraDownRows down;               // t's partials from the split kernel (gguf_split_down_ranks)
     const void* bias = nullptr;
     int bias_dtype = DT_NONE;
     void* y = nullptr;
@@ -101,6 +120,10 @@ int gguf_split_parts(int type, int64_t M, int64_t N, int64_t K, int64_t row_byte
 // The reduction carries a LoRA term (lora.t, 16-byte aligned): more than 16 rows (32 x 32 tiles),
 // S > 1, no residual, rank a multiple of 8 up to 128, 16-byte aligned up rows.
 bool gguf_split_fuses_lora(const GgufSplitArgs& a);
+// Ranks per workgroup column (1 or 2) with which the split kernel itself computes t's partials for
+// a LoRA call of rank R (a.down), 0 when it does not: fewer than 17 rows, fewer than 4 K splits,
+// more than 2 ranks per column, a down factor without 16-byte aligned 8-value pieces.
+int gguf_split_down_ranks(const GgufSplitArgs& a, int R, int down_dt, int64_t ld_down, const void* down);
 hipError_t run_gguf_split(const GgufSplitArgs& a, hipStream_t st);
 
 // ---- GGUF single-row linear (gguf_gemv.hip) ----

@@ -321,11 +321,19 @@ def test_w4a8_lora_fused_into_gemm(bits, m, n, r, fdt, fused_calls):
     ("Q4_0", 512, 4096, 1024, 16, torch.bfloat16), # 256 tiles: one split without the LoRA, two with it
     ("IQ4_XS", 17, 520, 512, 8, torch.bfloat16),   # one m-tile of 17 rows, a ragged column block
     ("Q2_K", 100, 136, 1024, 24, torch.bfloat16),  # 16-value units, 2 m-tiles
+    ("Q6_K", 48, 4096, 2048, 64, torch.float16),   # t by the split kernel: 2 ranks per column, 4 splits
+    ("Q5_K", 40, 4096, 4096, 32, torch.float32),   # t by the split kernel, fp32 down, 1 rank per column
+    ("Q4_1", 24, 1024, 2048, 8, torch.bfloat16),   # t by the split kernel: 32-row m-tile
+    ("Q4_K", 100, 4096, 2048, 64, torch.float16),  # t by the split kernel over 2 m-tiles
+    ("Q8_0", 48, 4096, 4096, 128, torch.bfloat16), # 4 ranks per column: the separate down kernel
 ])
 def test_gguf_lora_fused_into_split(name, m, n, k, r, fdt, fused_calls):
     """GGUF calls from 17 rows to the split kernel's limit: the K-split reduction adds the LoRA term
     to each 64 x 128 output tile before its one rounding (the reference's GGUF LoRA in the epilogue,
-    to rank 128).  Against the separate kernels, the exact side term and the oracle's linear."""
+    to rank 128).  With 4 or more splits and at most 2 ranks per column of the grid, the split kernel also
+    forms t = x down^T from the activation slices it stages (its K-split partials summed in the
+    reduction); otherwise the separate down kernel does.  Against the separate kernels, the exact
+    side term and the oracle's linear."""
     Q = qlin()
     from gguf_blocks import random_gguf_blocks
     raw = random_gguf_blocks(name, n, k, seed=m + r)
