@@ -521,7 +521,7 @@ __global__ __launch_bounds__(SPL_NT) void gguf_split_lora_reduce_kernel(
         const int64_t m = min(m0 + 32 * wi + 8 * (r / 4) + 4 * h + r % 4, (int64_t)M - 1);
         acc[0][0][r] = __builtin_ldexpf(sum, xexp ? xexp[m] : 0) + bvn;
     }
-    lora_tile_epilogue_ranks<DU, SPL_BM, BNT, RC, NT, 1, 1>(L, lds, m0, n0, M, N, 32 * wi, 32 * wj, tid, lane, acc);
+    lora_tile_epilogue_ranks<DU, SPL_BM, BNT, RC, NT, 1, 1, true>(L, lds, m0, n0, M, N, 32 * wi, 32 * wj, tid, lane, acc);
     float* ot = reinterpret_cast<float*>(lds);
 #pragma unroll
     for (int r = 0; r < 16; ++r) ot[(32 * wi + 8 * (r / 4) + 4 * h + r % 4) * ORW + 32 * wj + r32] = acc[0][0][r];

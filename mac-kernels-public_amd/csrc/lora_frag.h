@@ -123,8 +123,8 @@ __device__ __forceinline__ void mfma_raw(const Raw8<DA>& ra, const Raw8<DB>& rb,
 // LoRA term of a GEMM workgroup's BMT x BNT output tile, added by its waves to accumulators that
 // already hold their fp32 base values (after bias).  The whole rank (R <= RC) is staged at once: all
 // NT threads load the tile's t rows [BMT x RC] (fp32) and up rows [BNT x RC] together (every load in
-// flight at once, zeros past R; t's K-split partials summed in split order and scaled by
-// 2^t_exp[m] where L asks for it).  t is multiplied by L.scale and split into bf16 hi and lo on its
+// flight at once, zeros past R; with PARTS, t's K-split partials summed in split order and scaled
+// by 2^t_exp[m] as L asks).  t is multiplied by L.scale and split into bf16 hi and lo on its
 // way into LDS, once per workgroup; up goes in as loaded.  Each wave then takes its TJ column blocks
 // in turn: it reads (and, for f16 / f32, splits) the up fragments of the block once, and runs the
 // bf16 MFMAs hi.hi, lo.hi (and hi.lo) of (scale t) . up^T for each of its TI row blocks straight into
@@ -157,7 +157,7 @@ __device__ __forceinline__ int lora_chunk(int row, int c) {
     return row * BPR + 16 * (c ^ ((row / RPL) % SW));
 }
 
-template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, typename AccT>
+template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, bool PARTS, typename AccT>
 __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* lds, int64_t m0, int64_t n0, int64_t M,
                                                    int64_t N, int wr0, int wc0, int tid, int lane, AccT (&acc)[TI][TJ]) {
     static_assert(sizeof(AccT) == sizeof(f32x16), "32 x 32 accumulators: fp32 values or their int32 bits");
@@ -179,22 +179,28 @@ __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* l
         const int p = tid + NT * i, row = p / (RC / 8), c = 8 * (p % (RC / 8));
         const int64_t m = min(m0 + row, M - 1), k = min<int64_t>(c, L.R - 8);
         const float* tp = L.t + m * ldt + k;
-        // K-split partials of t (at most 8), added in split order
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(tp), a1 = *reinterpret_cast<const u32x4*>(tp + 4);
 #pragma unroll
-        for (int sp = 0; sp < 8; ++sp) {
-            if (sp > 0 && sp >= L.t_parts) break;
-            const u32x4 a0 = *reinterpret_cast<const u32x4*>(tp + sp * L.t_stride);
-            const u32x4 a1 = *reinterpret_cast<const u32x4*>(tp + sp * L.t_stride + 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                tv[i][e] = sp ? tv[i][e] + __uint_as_float(a0[e]) : __uint_as_float(a0[e]);
-                tv[i][4 + e] = sp ? tv[i][4 + e] + __uint_as_float(a1[e]) : __uint_as_float(a1[e]);
-            }
+        for (int e = 0; e < 4; ++e) {
+            tv[i][e] = __uint_as_float(a0[e]);
+            tv[i][4 + e] = __uint_as_float(a1[e]);
         }
-        if (L.t_exp) {
-            const int e = L.t_exp[m];
+        if constexpr (PARTS) {
+            // K-split partials 1 .. t_parts - 1 of t, added in split order, then 2^t_exp[m]
+            for (int sp = 1; sp < L.t_parts; ++sp) {
+                const u32x4 b0 = *reinterpret_cast<const u32x4*>(tp + sp * L.t_stride);
+                const u32x4 b1 = *reinterpret_cast<const u32x4*>(tp + sp * L.t_stride + 4);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) tv[i][q] = __builtin_ldexpf(tv[i][q], e);
+                for (int e = 0; e < 4; ++e) {
+                    tv[i][e] += __uint_as_float(b0[e]);
+                    tv[i][4 + e] += __uint_as_float(b1[e]);
+                }
+            }
+            if (L.t_exp) {
+                const int e = L.t_exp[m];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) tv[i][q] = __builtin_ldexpf(tv[i][q], e);
+            }
         }
     }
 #pragma unroll
@@ -270,19 +276,19 @@ __device__ __forceinline__ void lora_tile_epilogue(const LoraTile& L, uint8_t* l
 // The same for ranks up to 2 RC: ranks 0 .. RC - 1 first, then the rest, each pass staged on its
 // own; the second pass continues the MFMA chain of the first on the same accumulators, so the
 // terms are added in rank order.  Requires R % 8 == 0 and 8 <= R <= 2 RC.
-template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, typename AccT>
+template <int DU, int BMT, int BNT, int RC, int NT, int TI, int TJ, bool PARTS = false, typename AccT>
 __device__ __forceinline__ void lora_tile_epilogue_ranks(const LoraTile& L, uint8_t* lds, int64_t m0, int64_t n0,
                                                          int64_t M, int64_t N, int wr0, int wc0, int tid, int lane,
                                                          AccT (&acc)[TI][TJ]) {
     LoraTile p = L;
     p.ld_t = L.R;
     p.R = L.R < RC ? L.R : RC;
-    lora_tile_epilogue<DU, BMT, BNT, RC, NT, TI, TJ>(p, lds, m0, n0, M, N, wr0, wc0, tid, lane, acc);
+    lora_tile_epilogue<DU, BMT, BNT, RC, NT, TI, TJ, PARTS>(p, lds, m0, n0, M, N, wr0, wc0, tid, lane, acc);
     if (L.R > RC) {
         p.t = L.t + RC;
         p.up = reinterpret_cast<const uint8_t*>(L.up) + RC * (DU == DT_F32 ? 4 : 2);
         p.R = L.R - RC;
-        lora_tile_epilogue<DU, BMT, BNT, RC, NT, TI, TJ>(p, lds, m0, n0, M, N, wr0, wc0, tid, lane, acc);
+        lora_tile_epilogue<DU, BMT, BNT, RC, NT, TI, TJ, PARTS>(p, lds, m0, n0, M, N, wr0, wc0, tid, lane, acc);
     }
 }
 
