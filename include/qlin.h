@@ -153,7 +153,9 @@ qlin_status qlin_w4a8_linear_lora(const qlin_tensor* x, const qlin_tensor* qdata
                                   const qlin_tensor* lora_down, const qlin_tensor* lora_up, float lora_scale,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* qlin_gguf_linear with unmerged LoRA in the epilogue: t = x @ lora_down^T (fp32, in the workspace),
+/* qlin_gguf_linear with unmerged LoRA in the epilogue: t = x @ lora_down^T (fp32, in the workspace;
+ * formed by the split kernel itself from the activation slices it stages when K is split 4 or more
+ * ways and each column of its grid needs at most 2 ranks, else by a separate down kernel first),
  * then the K-split reduction of the split kernel adds lora_scale * t @ lora_up^T to each output tile
  * in fp32 after the bias and rounds once into y.  Taken from 17 rows to the split kernel's limit
  * (512 rows) where K holds at least two of its stages (the call then splits
