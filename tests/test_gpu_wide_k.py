@@ -6,7 +6,7 @@ max first, then the outputs), and the GEMMs accumulate in fp32 over normalized o
 fp16 range is never the limit; the A8 int32 sums stay exact for K < 132104.
 
 Each case runs at K = 65536 or 73728 through the kernel its row count selects (the small-M
-kernels, the K-split and tiled GEMMs) and is held to the BASELINE bar against the oracle's float64
+kernels, the K-split and tiled GEMMs) and is held to the parity bar against the oracle's float64
 linear over the same dequantized operands: relative Frobenius error < 1e-3, max-abs < 2e-2.  The
 A8 activation quantization is bit-exact against the oracle, and the A8 linear equals an exact
 replay of its int8 GEMM and epilogue.
