@@ -354,6 +354,42 @@ def test_gguf_lora_fused_into_split(name, m, n, k, r, fdt, fused_calls):
     check_full(y, want, f"{name} fused full m={m} r={r}")
 
 
+@pytest.mark.parametrize("m,r", [(64, 64), (24, 16), (200, 32)])
+def test_gguf_lora_fused_graph_replays(m, r, fused_calls):
+    """A fused GGUF LoRA call captured in a HIP graph and replayed with new activations, eager calls
+    (their own workspace) between the replays: every replay equals the eager call bit for bit (the
+    split kernel's t partials at 64 and 24 rows, the separate down kernel at 200; sums in a fixed
+    order either way)."""
+    Q = qlin()
+    from gguf_blocks import random_gguf_blocks
+    name, n, k = "Q4_K", 4096, 2048
+    rd = torch.from_numpy(random_gguf_blocks(name, n, k, seed=71)).to(DEV)
+    down, up = factors(n, k, r, torch.bfloat16, torch.bfloat16, seed=72)
+    down, up = down.to(DEV), up.to(DEV)
+    xs = [(torch.randn(m, k, generator=torch.Generator().manual_seed(73 + i)) * 0.5).half().to(DEV) for i in range(3)]
+    xin = xs[0].clone()
+    kw = dict(lora_down=down, lora_up=up, lora_scale=0.6)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        Q.gguf_linear(xin, rd, name, (n, k), **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        yg = Q.gguf_linear(xin, rd, name, (n, k), **kw)
+    torch.cuda.synchronize()
+    for i in range(6):
+        xin.copy_(xs[i % 3])
+        g.replay()
+        torch.cuda.synchronize()
+        got = yg.clone()
+        want = Q.gguf_linear(xs[i % 3], rd, name, (n, k), **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i} differs from the eager call"
+    assert all(fused_calls)
+
+
 @pytest.mark.parametrize("name,m,r", [("Q4_K", 16, 16), ("Q4_K", 600, 16), ("Q4_K", 64, 136), ("Q6_K", 520, 16),
                                       ("Q4_K", 64, 12)])
 def test_gguf_lora_declines_to_the_separate_kernels(name, m, r, fused_calls):
