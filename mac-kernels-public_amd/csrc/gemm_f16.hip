@@ -642,13 +642,19 @@ __global__ __launch_bounds__(512) void gemm_wo_dma_kernel(GemmF16Args a) {
     for (int st = 0; st < STAGES - 1; ++st) dma(st, st);
     wait_vmcnt<(STAGES - 2) * ND>();
     __builtin_amdgcn_s_barrier();
-    for (int kt = 0; kt < ktiles; ++kt) {
-        dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(kt % STAGES);
-        wait_lgkmcnt0();
-        wait_vmcnt<(STAGES - 2) * ND>();  // tile kt + 1 has landed
-        __builtin_amdgcn_s_barrier();
+    // unrolled by STAGES: every stage buffer index is a constant (1-2% faster on the A8 configs)
+    for (int k0 = 0; k0 < ktiles; k0 += STAGES) {
+#pragma unroll
+        for (int s = 0; s < STAGES; ++s) {
+            const int kt = k0 + s;
+            if (kt >= ktiles) break;
+            dma(kt + STAGES - 1, (s + STAGES - 1) % STAGES);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(s);
+            wait_lgkmcnt0();
+            wait_vmcnt<(STAGES - 2) * ND>();  // tile kt + 1 has landed
+            __builtin_amdgcn_s_barrier();
+        }
     }
     wait_vmcnt<0>();
 
@@ -927,13 +933,19 @@ __global__ __launch_bounds__((64 * wo_dmas_waves<BMT, BNT, KT>())) void gemm_wo_
     for (int st = 0; st < STAGES - 1; ++st) dma(st, st);
     wait_stages<STAGES>(nd);
     __builtin_amdgcn_s_barrier();
-    for (int kt = 0; kt < ktiles; ++kt) {
-        dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(kt % STAGES);
-        wait_lgkmcnt0();
-        wait_stages<STAGES>(nd);  // tile kt + 1 has landed
-        __builtin_amdgcn_s_barrier();
+    // unrolled by STAGES: every stage buffer index is a constant (1-2% faster on the A8 configs)
+    for (int k0 = 0; k0 < ktiles; k0 += STAGES) {
+#pragma unroll
+        for (int s = 0; s < STAGES; ++s) {
+            const int kt = k0 + s;
+            if (kt >= ktiles) break;
+            dma(kt + STAGES - 1, (s + STAGES - 1) % STAGES);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(s);
+            wait_lgkmcnt0();
+            wait_stages<STAGES>(nd);  // tile kt + 1 has landed
+            __builtin_amdgcn_s_barrier();
+        }
     }
     wait_vmcnt<0>();
     __syncthreads();

@@ -896,17 +896,23 @@ __global__ __launch_bounds__(64 * WVM * WVN) void gemm_i8dma_kernel(GemmI8Args p
     }
     wait_vmcnt<INFLIGHT>();
     __builtin_amdgcn_s_barrier();
-    for (int kt = 0; kt < ktiles; ++kt) {
-        // past the end: re-reads the last tile into a buffer no step reads
-        dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        l2pf(kt + STAGES);
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas(kt % STAGES);
-        // this wave's fragment reads of buffer kt % STAGES are complete before the barrier, after
-        // which the next step's DMA may overwrite it; tile kt + 1 has landed
-        wait_lgkmcnt0();
-        wait_vmcnt<INFLIGHT>();
-        __builtin_amdgcn_s_barrier();
+    // unrolled by STAGES: every stage buffer index is a constant (1-2% faster on the A8 configs)
+    for (int k0 = 0; k0 < ktiles; k0 += STAGES) {
+#pragma unroll
+        for (int s = 0; s < STAGES; ++s) {
+            const int kt = k0 + s;
+            if (kt >= ktiles) break;
+            // past the end: re-reads the last tile into a buffer no step reads
+            dma(kt + STAGES - 1, (s + STAGES - 1) % STAGES);
+            l2pf(kt + STAGES);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(s);
+            // this wave's fragment reads of buffer s are complete before the barrier, after which
+            // the next step's DMA may overwrite it; tile kt + 1 has landed
+            wait_lgkmcnt0();
+            wait_vmcnt<INFLIGHT>();
+            __builtin_amdgcn_s_barrier();
+        }
     }
     wait_vmcnt<0>();
 
