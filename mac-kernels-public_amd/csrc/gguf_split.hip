@@ -480,15 +480,17 @@ __global__ __launch_bounds__(256) void gguf_split_reduce_kernel(
     store4_rt(y, y_dt, (int64_t)m * ldy + n, o, min(4, N - n), vec);
 }
 
-// The reduction with an unmerged LoRA term (S > 1): one workgroup per 64 x 128 output tile, each
-// wave a 32 x 32 sub-tile in the MFMA C layout (lane l, register r: row 8 (r / 4) + 4 (l / 32) +
-// r % 4, column l % 32).  The S partials are added in split order and the base ldexp(sum, xexp[m]) +
-// bias[n] formed as in gguf_split_reduce_kernel; lora_tile_epilogue_ranks then adds lora_scale *
-// t up^T to those fp32 values (bf16 MFMAs on exact hi / lo parts, ranks up to 2 x 64), and the tile
-// leaves through LDS as 8-output row pieces, rounded once.  Workgroup b takes row block b % blocks,
-// so with a multiple of 8 row blocks it runs on the XCD that wrote that block's partials (measured
-// at K = N = 4096, M = 64: 1.3 us faster than 32 x 64 tiles, whose grid is 4x larger).
-constexpr int SPL_BM = 64, SPL_BN = SP_ROWS, SPL_NT = SP_THREADS, SPL_LDS = 48 * 1024;
+// The reduction with an unmerged LoRA term (S > 1): one workgroup of 4 waves per 32 x 128 output
+// tile, each wave a 32 x 32 sub-tile in the MFMA C layout (lane l, register r: row 8 (r / 4) +
+// 4 (l / 32) + r % 4, column l % 32).  The S partials are added in split order and the base
+// ldexp(sum, xexp[m]) + bias[n] formed as in gguf_split_reduce_kernel; lora_tile_epilogue_ranks then
+// adds lora_scale * t up^T to those fp32 values (bf16 MFMAs on exact hi / lo parts, ranks up to
+// 2 x 64), and the tile leaves through LDS as 8-output row pieces, rounded once.  Workgroup b takes
+// row block b % blocks, so with a multiple of 8 row blocks it runs on the XCD that wrote that
+// block's partials.  Measured at K = N = 4096 (Q4_K, rank 16-128, same process): 0.1-1.9 us per
+// call faster than 64 x 128 tiles of 8 waves (half the workgroups, each reading twice the partials
+// of y and of t), which were 1.3 us faster than 32 x 64 tiles at M = 64.
+constexpr int SPL_BM = 32, SPL_BN = SP_ROWS, SPL_NT = 256, SPL_LDS = 48 * 1024;
 template <int DU, int S>
 __global__ __launch_bounds__(SPL_NT) void gguf_split_lora_reduce_kernel(
     const float* __restrict__ part, int M, int N, const int32_t* __restrict__ xexp, const void* __restrict__ bias,
