@@ -45,6 +45,8 @@ __device__ __forceinline__ f16x2 h2(uint32_t u) { return __builtin_bit_cast(f16x
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(h2(a), h2(b), c, false);
 }
+// s + x.lo + x.hi for an fp16 pair x: one v_dot2_f32_f16 against (1, 1) (the products are exact)
+__device__ __forceinline__ float pair_sum(uint32_t x, float s) { return dot2(x, 0x3C003C00u, s); }
 // (x & 0x000F000F) | 0x64006400: fp16 pair (1024 + low nibble of byte 0, 1024 + low nibble of byte 2)
 __device__ __forceinline__ uint32_t nib_pair(uint32_t w) { return (w & 0x000F000Fu) | 0x64006400u; }
 // bytes 0 and 2 (< 256) -> fp16 pair (1024 + b0, 1024 + b2)
@@ -121,8 +123,7 @@ template <int T> struct GVK45 {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const f16x2 p = h2(xn[16 * g + i]);
-                s += (float)p.x + (float)p.y;
+                s = pair_sum(xn[16 * g + i], s);
             }
             xs[g] = s;
         }
@@ -192,8 +193,7 @@ template <> struct GV<gguf::Q8_0> {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const f16x2 p = h2(xn[16 * g + i]);
-                s += (float)p.x + (float)p.y;
+                s = pair_sum(xn[16 * g + i], s);
             }
             xs[g] = s;
         }
@@ -236,8 +236,7 @@ template <int T> struct GVTab32 {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const f16x2 p = h2(xn[16 * b + i]);
-                s += (float)p.x + (float)p.y;
+                s = pair_sum(xn[16 * b + i], s);
             }
             xs[b] = s;
         }
@@ -349,8 +348,7 @@ template <> struct GV<gguf::Q6_K> {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const f16x2 p = h2(xn[8 * g + i]);
-                s += (float)p.x + (float)p.y;
+                s = pair_sum(xn[8 * g + i], s);
             }
             xs[g] = s;
         }
