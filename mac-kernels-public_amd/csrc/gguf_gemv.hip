@@ -49,8 +49,12 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 __device__ __forceinline__ float pair_sum(uint32_t x, float s) { return dot2(x, 0x3C003C00u, s); }
 // (x & 0x000F000F) | 0x64006400: fp16 pair (1024 + low nibble of byte 0, 1024 + low nibble of byte 2)
 __device__ __forceinline__ uint32_t nib_pair(uint32_t w) { return (w & 0x000F000Fu) | 0x64006400u; }
+// (x & 0x00F000F0) | 0x64006400: fp16 pair (1024 + 16 * high nibble of byte 0, of byte 2), exact
+__device__ __forceinline__ uint32_t nib16_pair(uint32_t w) { return (w & 0x00F000F0u) | 0x64006400u; }
 // bytes 0 and 2 (< 256) -> fp16 pair (1024 + b0, 1024 + b2)
 __device__ __forceinline__ uint32_t byte_pair(uint32_t w) { return (w & 0x00FF00FFu) | 0x64006400u; }
+// bytes 1 and 3 -> fp16 pair (1024 + b1, 1024 + b3): one v_perm against 0x64 bytes (no shift)
+__device__ __forceinline__ uint32_t byte_pair_hi(uint32_t w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u); }
 
 // Interleave two fp16 pairs (a0, a1), (b0, b1) -> (a0, b0) and (a1, b1).
 __device__ __forceinline__ uint32_t lo_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
@@ -145,14 +149,16 @@ template <int T> struct GVK45 {
                 lo = (w & 0x0F0F0F0Fu) | (((qh >> sbl) & 0x01010101u) << 4);
                 hi = ((w >> 4) & 0x0F0F0F0Fu) | (((qh >> (sbl + 1)) & 0x01010101u) << 4);
                 S[2 * pair] = dot2(byte_pair(lo), xp[4 * j], S[2 * pair]);
-                S[2 * pair] = dot2(byte_pair(lo >> 8), xp[4 * j + 1], S[2 * pair]);
+                S[2 * pair] = dot2(byte_pair_hi(lo), xp[4 * j + 1], S[2 * pair]);
                 S[2 * pair + 1] = dot2(byte_pair(hi), xp[4 * j + 2], S[2 * pair + 1]);
-                S[2 * pair + 1] = dot2(byte_pair(hi >> 8), xp[4 * j + 3], S[2 * pair + 1]);
+                S[2 * pair + 1] = dot2(byte_pair_hi(hi), xp[4 * j + 3], S[2 * pair + 1]);
             } else {
+                // high nibbles as 1024 + 16 q (no shift): their sums carry 16x the code term
+                (void)hi;
                 S[2 * pair] = dot2(nib_pair(lo), xp[4 * j], S[2 * pair]);
                 S[2 * pair] = dot2(nib_pair(lo >> 8), xp[4 * j + 1], S[2 * pair]);
-                S[2 * pair + 1] = dot2(nib_pair(hi), xp[4 * j + 2], S[2 * pair + 1]);
-                S[2 * pair + 1] = dot2(nib_pair(hi >> 8), xp[4 * j + 3], S[2 * pair + 1]);
+                S[2 * pair + 1] = dot2(nib16_pair(w), xp[4 * j + 2], S[2 * pair + 1]);
+                S[2 * pair + 1] = dot2(nib16_pair(w >> 8), xp[4 * j + 3], S[2 * pair + 1]);
             }
         }
         float acc = 0.0f;
@@ -169,7 +175,8 @@ template <int T> struct GVK45 {
             }
             (void)sb;
             const float a = d * (float)sc, b = dmin * (float)mn;
-            acc += a * S[g] - (1024.0f * a + b) * xs[g];
+            if (T == gguf::Q4_K && (g & 1)) acc += (0.0625f * a) * S[g] - (64.0f * a + b) * xs[g];
+            else acc += a * S[g] - (1024.0f * a + b) * xs[g];
         }
         return acc;
     }
@@ -207,7 +214,7 @@ template <> struct GV<gguf::Q8_0> {
             constexpr int j = decltype(J)::value;
             const uint32_t w = dw_at<o + 2 + 4 * j>(r) ^ 0x80808080u;
             S = dot2(byte_pair(w), xp[16 * B + 2 * j], S);
-            S = dot2(byte_pair(w >> 8), xp[16 * B + 2 * j + 1], S);
+            S = dot2(byte_pair_hi(w), xp[16 * B + 2 * j + 1], S);
         });
         return d * (S - 1152.0f * xsum);
     }
@@ -368,9 +375,9 @@ template <> struct GV<gguf::Q6_K> {
             const uint32_t hi = ((ql >> 4) & 0x0F0F0F0Fu) | (((qh >> (sl + 4)) & 0x03030303u) << 4);
             const int glo = j / 4, ghi = 4 + j / 4;  // 16-value groups of v = 4j and 64 + 4j
             S[glo] = dot2(byte_pair(lo), xp[4 * j], S[glo]);
-            S[glo] = dot2(byte_pair(lo >> 8), xp[4 * j + 1], S[glo]);
+            S[glo] = dot2(byte_pair_hi(lo), xp[4 * j + 1], S[glo]);
             S[ghi] = dot2(byte_pair(hi), xp[4 * j + 2], S[ghi]);
-            S[ghi] = dot2(byte_pair(hi >> 8), xp[4 * j + 3], S[ghi]);
+            S[ghi] = dot2(byte_pair_hi(hi), xp[4 * j + 3], S[ghi]);
         }
         float acc = 0.0f;
 #pragma unroll
