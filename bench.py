@@ -283,7 +283,7 @@ def kernel_of(t, m):
     the C ABI).  The K-split path is two launches per call: the split kernel and its reduction."""
     if m == 1:
         return "gguf_gemv_kernel"
-    return SPLIT_PATH if m >= (5 if t == "Q6_K" else 17) else "gguf_smallm_kernel"
+    return SPLIT_PATH if m >= (3 if t == "Q6_K" else 17) else "gguf_smallm_kernel"
 
 
 def kernel_breakdown(detail):

@@ -151,8 +151,9 @@ constexpr int64_t GGUF_SMALLM_MAX_M = 64;
 constexpr int64_t INT8_SMALLM_MAX_M = 16;
 // Measured at K = N = 4096: the split kernel costs ~10 us at any M (two launches, partials) and
 // wins from M = 17 on, except Q6_K, whose 16-value units make the per-wave K-split kernel slower
-// (11.8 vs 13.9 us at M = 8).
-int64_t gguf_split_min_m(int type) { return type == gguf::Q6_K ? 5 : 17; }
+// (same process: split 10.6 us against 10.9 / 12.1 / 14.1 us at M = 3 / 4 / 8; at M = 2 10.0
+// against 10.6).
+int64_t gguf_split_min_m(int type) { return type == gguf::Q6_K ? 3 : 17; }
 // Largest M of the split kernel, whose 64-row m-tiles decode the weight in the load stage (above
 // it: the weight decoded once to fp16, then the fp16-weight GEMM).  Measured at K = N = 4096: the
 // split kernel is 2x faster at 65-128 rows and 1.1-1.3x at 512 rows (one round of 256 workgroups;

@@ -32,7 +32,7 @@ def test_headline_kernel_map_follows_the_dispatch():
     n = k = 4096
     for t in HEADLINE_TYPES:
         tid = O.GGUF_TYPES[t][0]
-        for m in (1, 2, 4, 5, 8, 16, 17, 64):
+        for m in (1, 2, 3, 4, 5, 8, 16, 17, 64):
             size = L.qlin_workspace_size(_lib.OP_GGUF_LINEAR, m, n, k, tid, _lib.DT_F16)
             split = size > a(m * k * 2) + a(m * 4) + a(n * 4)
             kern = bench.kernel_of(t, m)

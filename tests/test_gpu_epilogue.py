@@ -208,7 +208,7 @@ def test_w4a8_residual_fused_equals_separate(m, n, k, bits, gs):
     ("IQ4_XS", 8, 1000, 2048),  # small-M kernel, then the residual kernel
 ])
 def test_gguf_residual_fused_equals_separate(name, m, n, k):
-    """From 17 to 512 rows (Q6_K from 5) the split kernel, or its reduction, applies the residual;
+    """From 17 to 512 rows (Q6_K from 3) the split kernel, or its reduction, applies the residual;
     above, the GEMM over the decoded weight; fewer rows take the weight-streaming kernels and the
     residual kernel after them.  Every route gives the bits of the separate residual kernel."""
     Q = qlin()

@@ -434,7 +434,7 @@ SCALE_FIELDS = {"Q8_0": [0], "Q4_0": [0], "Q4_1": [0, 2], "Q5_1": [0, 2], "IQ4_N
 @pytest.mark.parametrize("m", [1, 4, 8, 40, 100])
 @pytest.mark.parametrize("name", list(SCALE_FIELDS))
 def test_gguf_linear_folded_scale_ranges(name, m):
-    """The split kernel (Q6_K from 5 rows, every format from 17) folds block scales into fp16
+    """The split kernel (Q6_K from 3 rows, every format from 17) folds block scales into fp16
     operands with a power of two per weight row and K half; the one-row kernel (M = 1) and the
     small-M kernel (M = 4) apply them in fp32 after exact fp16 code products.  Weight rows whose fp16 block scales are all subnormal, mix 6e4 with
     1e-3 and subnormals in one half, are all zero, or are ordinary: every output column within the
